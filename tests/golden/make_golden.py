@@ -1,0 +1,207 @@
+"""Write golden vectors for the HiF4 attention path by running the reference on CPU.
+
+Run in the development container only (the reference never travels):
+
+    PYTHONPATH=/root/reference/src python tests/golden/make_golden.py
+
+Why an import is needed: the reference's own tests pin the HiF4 codec with a
+single known-answer vector (levels 123 only) and pin the tiled simulator only
+with the int format (their module fake omits ``quant_format``).  The HiF4 levels
+12/13 codec, the exact fp32 stage order of the Hadamard and the simulator's
+HiF4 Q/K/P/V outputs are pinned by nothing else, so this script records them.
+Inputs are regenerated from ``oracle.inputs`` (numpy PCG64), so only outputs and
+an input checksum are stored.
+
+Fixtures (numpy .npz, float32 unless noted):
+  hif4_codec.npz      fake_quantize(hif4) for levels 123/12/13 on fp32 and bf16
+                      inputs, adversarial rows, tails of width 70/100, and the
+                      compact parameters of the same blocks.
+  hadamard.npz        hadamard_transform n=64/128 and chunked_block_hadamard_transform
+                      (block 64) on fp32 rows; Qwen/Wan prologue outputs (bf16).
+  attention.npz       simulated_flash_attention_forward with HiF4 Q/K/P/V at the
+                      configuration shapes listed in CASES.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import os
+import sys
+from types import SimpleNamespace
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, REPO)
+
+from oracle import inputs  # noqa: E402
+from tests.golden.cases import CASES, build_inputs  # noqa: E402
+
+from faquant import hif4 as ref_hif4  # noqa: E402  (reference, via PYTHONPATH)
+from faquant.quantization import fake_quantize  # noqa: E402
+from faquant.rotation import chunked_block_hadamard_transform, hadamard_transform  # noqa: E402
+from faquant.simulated_flash_attention import (  # noqa: E402
+    new_simulated_attention_stats,
+    simulated_flash_attention_forward,
+)
+
+
+def digest(*arrays: np.ndarray) -> str:
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a, dtype=np.float32).tobytes())
+    return h.hexdigest()
+
+
+def codec_rows(seed: int) -> np.ndarray:
+    """Adversarial [R, 128] float32 rows for the codec fixtures."""
+    g = inputs.rng(seed)
+    rows = [
+        g.standard_normal((48, 128), dtype=np.float32),
+        g.standard_t(3.0, size=(16, 128)).astype(np.float32),
+        (g.standard_normal((8, 128)) * 1e-12).astype(np.float32),
+        (g.standard_normal((8, 128)) * 3e5).astype(np.float32),
+        np.exp(g.uniform(-40, 10, size=(8, 128))).astype(np.float32)
+        * np.sign(g.standard_normal((8, 128))).astype(np.float32),
+    ]
+    special = np.zeros((8, 128), dtype=np.float32)
+    special[1, :] = 1.0  # all-equal block
+    special[2, :64] = 7.0
+    special[2, 64:] = -0.5
+    special[3, :] = np.linspace(-1, 1, 128, dtype=np.float32)
+    special[4, :] = np.float32(2.0**-60)  # below the 2^-48 scale clamp
+    special[5, :] = np.float32(1e30)  # above the 49152 clamp
+    special[6, ::2] = -0.0
+    special[6, 1::2] = np.float32(0.49999997)
+    # values one ulp either side of rounding boundaries relative to a unit block max
+    special[7, 0] = 1.0
+    special[7, 1:] = np.nextafter(np.float32(np.arange(1, 128) / 128.0), np.float32(0))
+    rows.append(special)
+    return np.concatenate(rows, axis=0)
+
+
+def make_codec() -> dict[str, np.ndarray]:
+    out: dict[str, np.ndarray] = {}
+    x = codec_rows(11)
+    out["x"] = x
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    out["x_bf16"] = xb.float().numpy()
+    tails = {w: inputs.rng(12 + w).standard_normal((16, w), dtype=np.float32) for w in (70, 100)}
+    for w, t in tails.items():
+        out[f"tail{w}"] = t
+    for levels in ("123", "12", "13"):
+        kw = dict(quant_format="hif4", bits=4, group_size=64, hif4_levels=levels)
+        out[f"y_{levels}"] = fake_quantize(torch.from_numpy(x), **kw).numpy()
+        out[f"yb_{levels}"] = fake_quantize(xb, **kw).float().numpy()
+        for w, t in tails.items():
+            out[f"ytail{w}_{levels}"] = fake_quantize(torch.from_numpy(t), **kw).numpy()
+        blocks = torch.from_numpy(x).reshape(-1, 64)
+        p = ref_hif4.fit_hif4_compact_parameters(blocks, levels=levels)
+        out[f"scale_{levels}"] = p.scale.reshape(-1).numpy()
+        out[f"rec_{levels}"] = p.reciprocal.reshape(-1).numpy()
+        out[f"lv2_{levels}"] = p.scale_lv2_exponent.reshape(-1, 8).numpy()
+        out[f"lv3_{levels}"] = p.scale_lv3_exponent.reshape(-1, 16).numpy()
+    return out
+
+
+def make_hadamard() -> dict[str, np.ndarray]:
+    out: dict[str, np.ndarray] = {}
+    g = inputs.rng(21)
+    x = (g.standard_normal((64, 128)) * g.uniform(0.1, 10, size=(64, 1))).astype(np.float32)
+    out["x"] = x
+    t = torch.from_numpy(x)
+    out["h128"] = hadamard_transform(t).numpy()
+    out["h64"] = hadamard_transform(t.reshape(-1, 64)).reshape(64, 128).numpy()
+    out["blk64"] = chunked_block_hadamard_transform(t, block_size=64).numpy()
+    # Qwen prologue: bf16 post-RoPE in, one fp32 excursion, one bf16 cast (qwen3.py:97-130).
+    q, k, _ = inputs.qwen(31, 2, 1, 40)
+    qb = torch.from_numpy(q).to(torch.bfloat16)
+    kb = torch.from_numpy(k).to(torch.bfloat16)
+    out["qwen_q"] = q
+    out["qwen_k"] = k
+    out["qwen_q_h128"] = hadamard_transform(qb.float()).to(torch.bfloat16).float().numpy()
+    out["qwen_k_h128"] = hadamard_transform(kb.float()).to(torch.bfloat16).float().numpy()
+    out["qwen_q_blk64"] = chunked_block_hadamard_transform(qb.float(), block_size=64).to(torch.bfloat16).float().numpy()
+    scale = (g.uniform(0.25, 4.0, size=(128,))).astype(np.float32)
+    offset = (g.standard_normal((1, 1, 128)) * 0.5).astype(np.float32)
+    out["smooth_scale"] = scale
+    out["key_offset"] = offset
+    kf = (kb.float() - torch.from_numpy(offset)) / torch.from_numpy(scale)
+    out["qwen_k_offset_smooth_h128"] = hadamard_transform(kf).to(torch.bfloat16).float().numpy()
+    qf = qb.float() * torch.from_numpy(scale)
+    out["qwen_q_smooth_h128"] = hadamard_transform(qf).to(torch.bfloat16).float().numpy()
+    return out
+
+
+def _module(*, qk: bool, pv: bool, mode: str, query_chunk: int = 256, key_chunk: int = 128, causal: bool = True):
+    return SimpleNamespace(
+        is_causal=causal,
+        training=False,
+        faquant_attention_query_chunk_size=query_chunk,
+        faquant_attention_key_chunk_size=key_chunk,
+        faquant_qk_matmul_quant=qk,
+        faquant_pv_matmul_quant=pv,
+        faquant_pv_normalizer_mode=mode,
+        faquant_matmul_quant_kwargs={
+            "quant_format": "hif4",
+            "bits": 4,
+            "group_size": 64,
+            "symmetric": True,
+            "clip_ratio": 1.0,
+        },
+        faquant_simulated_attention_stats=new_simulated_attention_stats(),
+    )
+
+
+def make_attention() -> dict[str, np.ndarray]:
+    out: dict[str, np.ndarray] = {}
+    for case, (builder, mod_kw, call_kw, levels, rot) in CASES.items():
+        q, k, v, dtype_name = build_inputs(builder)
+        dtype = torch.bfloat16 if dtype_name == "bfloat16" else torch.float32
+        out[f"{case}__input_sha256"] = np.frombuffer(bytes.fromhex(digest(q, k, v)), dtype=np.uint8)
+        qt = torch.from_numpy(q).to(dtype)
+        kt = torch.from_numpy(k).to(dtype)
+        vt = torch.from_numpy(v).to(dtype)
+        if rot is not None:
+            if rot == 128:
+                qt = hadamard_transform(qt.float()).to(dtype)
+                kt = hadamard_transform(kt.float()).to(dtype)
+            else:
+                qt = chunked_block_hadamard_transform(qt.float(), block_size=rot).to(dtype)
+                kt = chunked_block_hadamard_transform(kt.float(), block_size=rot).to(dtype)
+        saved = dict(ref_hif4.HIF4_ATTN_OPERAND_SCALE_LEVELS)
+        ref_hif4.HIF4_ATTN_OPERAND_SCALE_LEVELS.update(dict.fromkeys("qkpv", levels))
+        try:
+            module = _module(**mod_kw)
+            result, _ = simulated_flash_attention_forward(module, qt, kt, vt, None, **call_kw)
+        finally:
+            ref_hif4.HIF4_ATTN_OPERAND_SCALE_LEVELS.clear()
+            ref_hif4.HIF4_ATTN_OPERAND_SCALE_LEVELS.update(saved)
+        res = result.float().numpy()
+        if case == "c1_unq":
+            res = res[:, :, :4]  # half the heads keep the fixture small
+        if dtype == torch.bfloat16:
+            # bf16 values: store their upper 16 bits (exact)
+            out[f"{case}__out_bf16bits"] = (res.view(np.uint32) >> 16).astype(np.uint16)
+        else:
+            out[f"{case}__out"] = res
+        stats = module.faquant_simulated_attention_stats
+        out[f"{case}__stats_keys"] = np.array(sorted(stats), dtype="U32")
+        out[f"{case}__stats"] = np.array([stats[key] for key in sorted(stats)], dtype=np.int64)
+        print(f"{case}: out {tuple(result.shape)} stats qk_tiles={stats['qk_tiles']}")
+    return out
+
+
+def main() -> None:
+    torch.set_num_threads(os.cpu_count() or 1)
+    np.savez_compressed(os.path.join(HERE, "hif4_codec.npz"), **make_codec())
+    np.savez_compressed(os.path.join(HERE, "hadamard.npz"), **make_hadamard())
+    np.savez_compressed(os.path.join(HERE, "attention.npz"), **make_attention())
+    for name in ("hif4_codec.npz", "hadamard.npz", "attention.npz"):
+        print(name, os.path.getsize(os.path.join(HERE, name)))
+
+
+if __name__ == "__main__":
+    main()
