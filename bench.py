@@ -1,0 +1,228 @@
+"""HiF4 QK/PV attention benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen8b_32k] [--no-cpu-baseline]
+
+A step is one pass of the hot path over one batch of synthetic, HBM-resident
+input: the Q/K prologue (post-RoPE block Hadamard, one bf16 cast, HiF4 QDQ),
+the V QDQ (written transposed) and the HiF4 QK/PV flash-attention kernel.
+``value`` = algorithmic QK+PV FLOPs / step time (TFLOP/s).  ``roofline`` is the
+attention kernel alone: the same FLOPs / its mean launch time measured with HIP
+events on the stream it runs on, against the 2.5 PFLOP/s dense bf16 MFMA peak.
+``cpu_baseline`` times the numpy oracle (the CPU restatement of the reference
+simulator) on a bounded sample of the same workload: the last ``rows`` query rows
+of one KV group (``G`` query heads), scaled by its own algorithmic FLOPs.
+One JSON line is printed on rank 0.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "faquant-public_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    # name: B, Hq, Hkv, L, causal, hadamard block, levels, key distribution, per-head scale
+    "qwen8b_32k": dict(B=1, Hq=32, Hkv=8, L=32768, causal=True, hadamard=64, levels="123", keys="normal",
+                       workload="Qwen3-8B causal GQA prefill 32k (32q/8kv, d128), block Hadamard r64, HiF4 123"),
+    "qwen8b_8k": dict(B=1, Hq=32, Hkv=8, L=8192, causal=True, hadamard=64, levels="123", keys="normal",
+                      workload="Qwen3-8B causal GQA prefill 8k (32q/8kv, d128), block Hadamard r64, HiF4 123"),
+    "qwen32b_16k": dict(B=1, Hq=64, Hkv=8, L=16384, causal=True, hadamard=64, levels="12", keys="student_t",
+                        workload="Qwen3-32B causal GQA prefill 16k (64q/8kv, d128), r64, Student-t keys, HiF4 12"),
+    "wan480p": dict(B=1, Hq=40, Hkv=40, L=32760, causal=False, hadamard=128, levels="123", keys="normal",
+                    workload="Wan2.2 DiT self-attention 480p (40 heads, 32760 tokens), Hadamard 128, HiF4 123"),
+    "wan720p": dict(B=1, Hq=40, Hkv=40, L=75600, causal=False, hadamard=128, levels="123", keys="normal",
+                    head_scale=True,
+                    workload="Wan2.2 DiT self-attention 720p (40 heads, 75600 tokens), Hadamard 128, HiF4 123"),
+}
+
+
+def rope_(x, theta=1.0e6):
+    """In-place-free HF rotate-half RoPE over positions 0..L-1 (fp32 math, bf16 out)."""
+    import torch
+
+    L, D = x.shape[-2], x.shape[-1]
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2, device=x.device, dtype=torch.float64) / D))
+    ang = torch.arange(L, device=x.device, dtype=torch.float64)[:, None] * inv[None, :]
+    emb = torch.cat([ang, ang], dim=-1)
+    cos, sin = emb.cos().float(), emb.sin().float()
+    xf = x.float()
+    rot = torch.cat([-xf[..., D // 2:], xf[..., : D // 2]], dim=-1)
+    return (xf * cos + rot * sin).to(torch.bfloat16)
+
+
+def make_inputs(cfg, dev, seed=0):
+    import torch
+
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    B, Hq, Hkv, L = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"]
+    q = torch.randn((B, Hq, L, 128), device=dev, generator=gen)
+    if cfg["keys"] == "student_t":
+        # Student-t(3) = N / sqrt(chi2_3 / 3)
+        n = torch.randn((B, Hkv, L, 128), device=dev, generator=gen)
+        chi = torch.randn((3, B, Hkv, L, 128), device=dev, generator=gen).pow(2).sum(0)
+        k = n / (chi / 3).sqrt()
+    else:
+        k = torch.randn((B, Hkv, L, 128), device=dev, generator=gen)
+    v = torch.randn((B, Hkv, L, 128), device=dev, generator=gen)
+    if cfg.get("head_scale"):
+        s = torch.rand((1, Hq, 1, 1), device=dev, generator=gen) * 3.5 + 0.5
+        q, k, v = q * s, k * s, v * s
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    if cfg["causal"]:  # the Qwen configurations apply RoPE to Q/K
+        q, k = rope_(q), rope_(k)
+    return q, k, v
+
+
+def cpu_baseline(cfg, rows):
+    """Time the numpy oracle on the last `rows` query rows of one KV group."""
+    import numpy as np
+
+    from faquant_amd._ops import attention_flops
+    from oracle import attention as OA
+    from oracle import hadamard as OH
+    from oracle import hif4 as OQ
+    from oracle import inputs as OI
+
+    G = cfg["Hq"] // cfg["Hkv"]
+    L = cfg["L"]
+    g = OI.rng(99)
+    q = OQ.bf16_round(g.standard_normal((1, G, rows, 128), dtype=np.float32))
+    k = OQ.bf16_round(g.standard_normal((1, 1, L, 128), dtype=np.float32))
+    v = OQ.bf16_round(g.standard_normal((1, 1, L, 128), dtype=np.float32))
+    blk = cfg["hadamard"]
+    mconf = OA.SimConfig(pv_normalizer_mode="quantized_same", levels=dict.fromkeys("qkpv", cfg["levels"]),
+                         is_causal=cfg["causal"])
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = 1
+    t0 = time.perf_counter()
+    qr = OH.qk_rotation(q, block_size=blk, out_round=OQ.bf16_round)
+    kr = OH.qk_rotation(k, block_size=blk, out_round=OQ.bf16_round)
+    OA.simulated_flash_attention(qr, kr, v, mconf, dtype="bfloat16")
+    dt = time.perf_counter() - t0
+    flops = attention_flops(1, G, rows, L, cfg["causal"])
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"numpy oracle (CPU restatement of the reference simulator) on the last {rows} query rows "
+                   f"x {G} query heads of one KV group over {L} keys, prologue included: "
+                   f"{flops / 1e9:.2f} GFLOP in {dt:.2f} s; BLAS threads {threads}, elementwise numpy single-threaded"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="qwen8b_32k", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-rows", type=int, default=512)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from faquant_amd import _ops
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, k, v = make_inputs(cfg, dev)
+    B, Hq, Hkv, L = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"]
+    causal = cfg["causal"]
+    levels = cfg["levels"]
+    flops = _ops.attention_flops(B, Hq, L, L, causal)
+    out = torch.empty((B, L, Hq, 128), device=dev, dtype=torch.bfloat16)
+    qh = torch.empty((B, Hq, L, 128), device=dev, dtype=torch.bfloat16)
+    kh = torch.empty((B, Hkv, L, 128), device=dev, dtype=torch.bfloat16)
+
+    ev = []
+
+    def step(record=False):
+        _ops.operand_prep(q, levels=levels, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16, out=qh)
+        _ops.operand_prep(k, levels=levels, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16, out=kh)
+        vt = _ops.operand_prep_vt(v, levels=levels)
+        if record:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+        _ops.attention_fwd(qh, kh, vt, L, causal=causal, scale=128**-0.5, quant_p=True, p_levels=levels,
+                           norm_same=True, out=out.transpose(1, 2))
+        if record:
+            b.record()
+            ev.append((a, b))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(record=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    kern_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    kern_mean = sum(kern_ms) / len(kern_ms)
+    kern_median = kern_ms[len(kern_ms) // 2]
+    achieved = flops / (kern_mean * 1e-3) / 1e12
+    value = flops / (ms_step * 1e-3) / 1e12
+
+    result = {
+        "metric": "HiF4 QK/PV attn TFLOP/s + % MFMA peak, Qwen3-8B causal prefill 32k, 1 GPU",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": cfg["workload"],
+            "name": args.config,
+            "batch": B, "q_heads": Hq, "kv_heads": Hkv, "seq_len": L, "head_dim": 128,
+            "causal": causal, "qk_hadamard_block": cfg["hadamard"], "hif4_levels": levels,
+            "pv_normalizer": "quantized_same", "key_tile": 128,
+            "flops_per_step": flops,
+        },
+        "pct_mfma_peak": round(100.0 * value / MFMA_BF16_PEAK_TFLOPS, 2),
+        "attention_kernel_ms_mean": round(kern_mean, 4),
+        "attention_kernel_ms_median": round(kern_median, 4),
+        "prologue_ms": round(ms_step - kern_mean, 4),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_rows)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

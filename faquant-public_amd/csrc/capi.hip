@@ -1,0 +1,273 @@
+// C ABI of the HiF4 attention path (declarations and contracts: include/faquant_amd.h).
+// Validates arguments on the host, selects the kernel instantiation, launches it on the
+// caller's stream and reports errors through a thread-local message.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/faquant_amd.h"
+#include "hif4_attention.hip"
+#include "hif4_quant.hip"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(FAQ_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  g_err.clear();
+  return FAQ_OK;
+}
+
+bool valid_levels(int lv) { return lv == 123 || lv == 12 || lv == 13; }
+bool valid_dtype(int dt) { return dt == FAQ_F32 || dt == FAQ_BF16 || dt == FAQ_F16; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+unsigned grid_for(int64_t threads) { return static_cast<unsigned>((threads + 255) / 256); }
+
+template <typename T>
+void launch_qdq(const faq::QdqRowsArgs& a, int levels, int64_t threads, hipStream_t st) {
+  const dim3 grid(grid_for(threads));
+  if (levels == 123) hipLaunchKernelGGL((faq::qdq_rows_kernel<T, 123>), grid, dim3(256), 0, st, a);
+  else if (levels == 12) hipLaunchKernelGGL((faq::qdq_rows_kernel<T, 12>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((faq::qdq_rows_kernel<T, 13>), grid, dim3(256), 0, st, a);
+}
+
+template <typename Tin, typename Tout>
+void launch_hadamard(const faq::HadamardRowsArgs& a, int64_t threads, hipStream_t st) {
+  hipLaunchKernelGGL((faq::hadamard_rows_kernel<Tin, Tout>), dim3(grid_for(threads)), dim3(256), 0, st, a);
+}
+
+template <typename Tin>
+void launch_hadamard_in(const faq::HadamardRowsArgs& a, int out_dtype, int64_t threads, hipStream_t st) {
+  if (out_dtype == FAQ_F32) launch_hadamard<Tin, float>(a, threads, st);
+  else if (out_dtype == FAQ_BF16) launch_hadamard<Tin, __hip_bfloat16>(a, threads, st);
+  else launch_hadamard<Tin, __half>(a, threads, st);
+}
+
+template <typename Tin, typename Tround>
+void launch_prep(const faq::OperandPrepArgs& a, int levels, int64_t threads, hipStream_t st) {
+  const dim3 grid(grid_for(threads));
+  if (levels == 12) hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 12>), grid, dim3(256), 0, st, a);
+  else if (levels == 13) hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 13>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 123>), grid, dim3(256), 0, st, a);
+}
+
+template <typename Tin>
+void launch_prep_in(const faq::OperandPrepArgs& a, int round_dtype, int levels, int64_t threads, hipStream_t st) {
+  if (round_dtype == FAQ_F32) launch_prep<Tin, float>(a, levels, threads, st);
+  else if (round_dtype == FAQ_BF16) launch_prep<Tin, __hip_bfloat16>(a, levels, threads, st);
+  else launch_prep<Tin, __half>(a, levels, threads, st);
+}
+
+template <typename Tin>
+void launch_prep_vt(const faq::OperandPrepVtArgs& a, int levels, dim3 grid, hipStream_t st) {
+  if (levels == 12) hipLaunchKernelGGL((faq::operand_prep_vt_kernel<Tin, 12>), grid, dim3(256), 0, st, a);
+  else if (levels == 13) hipLaunchKernelGGL((faq::operand_prep_vt_kernel<Tin, 13>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((faq::operand_prep_vt_kernel<Tin, 123>), grid, dim3(256), 0, st, a);
+}
+
+template <int LV>
+void launch_attn_lv(const faq::AttnArgs& a, int quant_p, int same, dim3 grid, hipStream_t st) {
+  if (quant_p && same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true>), grid, dim3(256), 0, st, a);
+  else if (quant_p) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, false, false>), grid, dim3(256), 0, st, a);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* faq_last_error(void) { return g_err.c_str(); }
+
+const char* faq_version(void) { return "faquant_amd 0.1 gfx950"; }
+
+int faq_hif4_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, int levels, float* scale,
+                      float* rec, int8_t* lv2, int8_t* lv3, uint8_t* codes, uint8_t* scale_byte, uint8_t* lv2_bits,
+                      uint16_t* lv3_bits, faq_stream_t stream) {
+  if (!x || !y) return fail(FAQ_EINVAL, "faq_hif4_qdq_rows: null input or output");
+  if (rows < 0 || cols <= 0) return fail(FAQ_EINVAL, "HiF4 fake quantization does not support an empty axis");
+  if (!valid_dtype(dtype)) return fail(FAQ_EINVAL, "faq_hif4_qdq_rows: unsupported dtype %d", dtype);
+  if (!valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
+  if (codes && cols % 64) return fail(FAQ_EINVAL, "faq_hif4_qdq_rows: packed codes need cols %% 64 == 0");
+  if (rows == 0) return FAQ_OK;
+  faq::QdqRowsArgs a{};
+  a.x = x;
+  a.y = y;
+  a.rows = rows;
+  a.cols = cols;
+  a.vec = (cols % 8 == 0) && aligned16(x) && aligned16(y);
+  a.scale = scale;
+  a.rec = rec;
+  a.lv2 = lv2;
+  a.lv3 = lv3;
+  a.codes = codes;
+  a.scale_byte = scale_byte;
+  a.lv2_bits = lv2_bits;
+  a.lv3_bits = lv3_bits;
+  const int64_t threads = rows * ((cols + 63) / 64) * 8;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FAQ_F32) launch_qdq<float>(a, levels, threads, st);
+  else if (dtype == FAQ_BF16) launch_qdq<__hip_bfloat16>(a, levels, threads, st);
+  else launch_qdq<__half>(a, levels, threads, st);
+  return check_launch("faq_hif4_qdq_rows");
+}
+
+int faq_hadamard_rows(const void* x, void* y, int64_t rows, int64_t cols, int block, int in_dtype, int out_dtype,
+                      faq_stream_t stream) {
+  if (!x || !y) return fail(FAQ_EINVAL, "faq_hadamard_rows: null input or output");
+  if (block < 2 || block > 512 || (block & (block - 1)))
+    return fail(FAQ_EINVAL, "Hadamard dimension must be a power of two, got %d", block);
+  if (cols <= 0 || cols % block)
+    return fail(FAQ_EINVAL, "dimension %lld must be divisible by power-of-two block_size=%d",
+                static_cast<long long>(cols), block);
+  if (cols % 8) return fail(FAQ_EUNSUP, "faq_hadamard_rows: row width must be a multiple of 8");
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype)) return fail(FAQ_EINVAL, "faq_hadamard_rows: bad dtype");
+  if (!aligned16(x) || !aligned16(y)) return fail(FAQ_EINVAL, "faq_hadamard_rows: pointers must be 16-byte aligned");
+  if (rows == 0) return FAQ_OK;
+  faq::HadamardRowsArgs a{x, y, rows, cols, block, static_cast<float>(std::sqrt(static_cast<double>(block)))};
+  const int64_t threads = rows * (cols / 8);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (in_dtype == FAQ_F32) launch_hadamard_in<float>(a, out_dtype, threads, st);
+  else if (in_dtype == FAQ_BF16) launch_hadamard_in<__hip_bfloat16>(a, out_dtype, threads, st);
+  else launch_hadamard_in<__half>(a, out_dtype, threads, st);
+  return check_launch("faq_hadamard_rows");
+}
+
+int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
+                     const float* key_offset, int64_t off_sh, const float* smooth, int64_t smooth_sh,
+                     int smooth_divide, int hadamard, int round_dtype, void* rotated, void* y, int64_t yb,
+                     int64_t yh, int64_t yl, int levels, faq_stream_t stream) {
+  if (!x || !y) return fail(FAQ_EINVAL, "faq_operand_prep: null input or output");
+  if (B < 0 || H < 0 || L < 0) return fail(FAQ_EINVAL, "faq_operand_prep: negative size");
+  if (!valid_dtype(in_dtype) || !valid_dtype(round_dtype)) return fail(FAQ_EINVAL, "faq_operand_prep: bad dtype");
+  if (hadamard != 0 && hadamard != 64 && hadamard != 128)
+    return fail(FAQ_EUNSUP, "faq_operand_prep: Hadamard block must be 64 or 128, got %d", hadamard);
+  if (levels != 0 && !valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
+  if (!aligned16(x) || !aligned16(y)) return fail(FAQ_EINVAL, "faq_operand_prep: pointers must be 16-byte aligned");
+  const int esz = in_dtype == FAQ_F32 ? 4 : 2;
+  if ((sb * esz) % 16 || (sh * esz) % 16 || (sl * esz) % 16 || (yb * 2) % 16 || (yh * 2) % 16 || (yl * 2) % 16)
+    return fail(FAQ_EINVAL, "faq_operand_prep: strides must keep 16-byte alignment");
+  const int64_t rows = static_cast<int64_t>(B) * H * L;
+  if (rows == 0) return FAQ_OK;
+  faq::OperandPrepArgs a{};
+  a.x = x;
+  a.sb = sb;
+  a.sh = sh;
+  a.sl = sl;
+  a.B = B;
+  a.H = H;
+  a.L = L;
+  a.key_offset = key_offset;
+  a.off_sh = off_sh;
+  a.smooth = smooth;
+  a.smooth_sh = smooth_sh;
+  a.smooth_divide = smooth_divide;
+  a.hadamard = hadamard;
+  a.sqrt_n = hadamard ? static_cast<float>(std::sqrt(static_cast<double>(hadamard))) : 1.0f;
+  a.rotated = rotated;
+  a.y = y;
+  a.yb = yb;
+  a.yh = yh;
+  a.yl = yl;
+  a.quant = levels != 0;
+  const int64_t threads = rows * 16;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (in_dtype == FAQ_F32) launch_prep_in<float>(a, round_dtype, levels, threads, st);
+  else if (in_dtype == FAQ_BF16) launch_prep_in<__hip_bfloat16>(a, round_dtype, levels, threads, st);
+  else launch_prep_in<__half>(a, round_dtype, levels, threads, st);
+  return check_launch("faq_operand_prep");
+}
+
+int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
+                        int Lpad, uint16_t* vt, int levels, faq_stream_t stream) {
+  if (!x || !vt) return fail(FAQ_EINVAL, "faq_operand_prep_vt: null input or output");
+  if (B < 0 || H < 0 || L < 0) return fail(FAQ_EINVAL, "faq_operand_prep_vt: negative size");
+  if (Lpad % 128 || Lpad < L) return fail(FAQ_EINVAL, "faq_operand_prep_vt: Lpad must be a multiple of 128 >= L");
+  if (!valid_dtype(in_dtype)) return fail(FAQ_EINVAL, "faq_operand_prep_vt: bad dtype");
+  if (levels != 0 && !valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
+  if (!aligned16(x) || !aligned16(vt)) return fail(FAQ_EINVAL, "faq_operand_prep_vt: pointers must be 16-byte aligned");
+  const int esz = in_dtype == FAQ_F32 ? 4 : 2;
+  if ((sb * esz) % 16 || (sh * esz) % 16 || (sl * esz) % 16)
+    return fail(FAQ_EINVAL, "faq_operand_prep_vt: strides must keep 16-byte alignment");
+  if (static_cast<int64_t>(B) * H * Lpad == 0) return FAQ_OK;
+  faq::OperandPrepVtArgs a{x, sb, sh, sl, B, H, L, Lpad, vt, levels != 0};
+  const dim3 grid(Lpad / 64, B * H);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (in_dtype == FAQ_F32) launch_prep_vt<float>(a, levels, grid, st);
+  else if (in_dtype == FAQ_BF16) launch_prep_vt<__hip_bfloat16>(a, levels, grid, st);
+  else launch_prep_vt<__half>(a, levels, grid, st);
+  return check_launch("faq_operand_prep_vt");
+}
+
+int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k, int64_t k_sb,
+                      int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh, int64_t v_sd,
+                      int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq,
+                      int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels, int norm_same,
+                      float* row_den, faq_stream_t stream) {
+  if (!q || !k || !vt || !o) return fail(FAQ_EINVAL, "faq_attention_fwd: null operand");
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "faq_attention_fwd: bad sizes");
+  if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
+  if (Lpad % 128 || Lpad < Lk) return fail(FAQ_EINVAL, "faq_attention_fwd: Lpad must be a multiple of 128 >= Lk");
+  if (o_dtype != FAQ_F32 && o_dtype != FAQ_BF16) return fail(FAQ_EUNSUP, "faq_attention_fwd: output must be fp32 or bf16");
+  if (quant_p && !valid_levels(p_levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", p_levels);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(vt) || !aligned16(o))
+    return fail(FAQ_EINVAL, "faq_attention_fwd: pointers must be 16-byte aligned");
+  if ((q_sb | q_sh | q_sl | k_sb | k_sh | k_sl | v_sb | v_sh | v_sd) & 7)
+    return fail(FAQ_EINVAL, "faq_attention_fwd: operand strides must be multiples of 8 elements");
+  if (o_dtype == FAQ_BF16 ? ((o_sb | o_sh | o_sl) & 3) : ((o_sb | o_sh | o_sl) & 3))
+    return fail(FAQ_EINVAL, "faq_attention_fwd: output strides must be multiples of 4 elements");
+  if (v_sd < Lpad) return fail(FAQ_EINVAL, "faq_attention_fwd: v_sd must be >= Lpad");
+  if (B == 0 || Lq == 0) return FAQ_OK;
+  const int G = Hq / Hkv;
+  const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+  const int pos_per_wg = 32 * (4 / hpw);
+  faq::AttnArgs a{};
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_sl = q_sl;
+  a.k = k;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_sl = k_sl;
+  a.vt = vt;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.v_sd = v_sd;
+  a.o = o;
+  a.o_sb = o_sb;
+  a.o_sh = o_sh;
+  a.o_sl = o_sl;
+  a.o_f32 = o_dtype == FAQ_F32;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.Lq = Lq;
+  a.Lk = Lk;
+  a.causal = causal != 0;
+  a.c1 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  a.hpw = hpw;
+  a.n_pblocks = (Lq + pos_per_wg - 1) / pos_per_wg;
+  a.row_den = row_den;
+  const dim3 grid(static_cast<unsigned>(B * Hkv * (G / hpw)), static_cast<unsigned>(a.n_pblocks));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int lv = quant_p ? p_levels : 123;
+  if (lv == 12) launch_attn_lv<12>(a, quant_p, norm_same, grid, st);
+  else if (lv == 13) launch_attn_lv<13>(a, quant_p, norm_same, grid, st);
+  else launch_attn_lv<123>(a, quant_p, norm_same, grid, st);
+  return check_launch("faq_attention_fwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,402 @@
+// HBM-bound kernels of the HiF4 attention path on gfx950:
+//   qdq_rows_kernel        fake_quantize_hif4 / fit_hif4_compact_parameters / packed encode
+//                          (reference: src/faquant/hif4.py:143-271, 346-390)
+//   hadamard_rows_kernel   hadamard_transform / chunked_block_hadamard_transform
+//                          (reference: src/faquant/rotation.py:14-29, 117-135)
+//   operand_prep_kernel    post-RoPE Q/K excursion (key offset, Smooth-QK, Hadamard, one
+//                          cast) fused with the operand QDQ, writing the attention operand
+//                          (reference: src/faquant/qwen3.py:97-136,
+//                          src/faquant/simulated_flash_attention.py:588-619,
+//                          src/faquant/wan22_attention.py:186-192, 219-221)
+//   operand_prep_vt_kernel V QDQ written transposed ([d][key], keys padded with zeros to
+//                          a multiple of 128) for the attention kernel's PV operand.
+//
+// Layout: one lane owns 8 consecutive values of a row (one 16-byte bf16 vector); a
+// 64-value HiF4 group spans 8 adjacent lanes and its maxima reduce with xor shuffles
+// inside those 8 lanes.  A Hadamard butterfly of stride 8*m pairs lane l with lane l^m.
+#include "hif4_device.h"
+
+namespace faq {
+
+template <typename T>
+struct Io;
+
+template <>
+struct Io<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
+  static __device__ __forceinline__ float round(float v) { return v; }
+  static __device__ __forceinline__ void load8(const float* p, float* v) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store8(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
+template <>
+struct Io<__hip_bfloat16> {
+  using T = __hip_bfloat16;
+  static __device__ __forceinline__ float load(const T* p) {
+    return bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
+  }
+  static __device__ __forceinline__ void store(T* p, float v) {
+    *reinterpret_cast<uint16_t*>(p) = f32_to_bf16_bits_rne(v);
+  }
+  static __device__ __forceinline__ float round(float v) { return bf16_rne(v); }
+  static __device__ __forceinline__ void load8(const T* p, float* v) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+  static __device__ __forceinline__ void store8(T* p, const float* v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(f32_to_bf16_bits_rne(v[2 * i])) |
+             (static_cast<uint32_t>(f32_to_bf16_bits_rne(v[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+template <>
+struct Io<__half> {
+  using T = __half;
+  static __device__ __forceinline__ float load(const T* p) { return __half2float(*p); }
+  static __device__ __forceinline__ void store(T* p, float v) { *p = __float2half_rn(v); }
+  static __device__ __forceinline__ float round(float v) { return __half2float(__float2half_rn(v)); }
+  static __device__ __forceinline__ void load8(const T* p, float* v) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __half2float(p[i]);
+  }
+  static __device__ __forceinline__ void store8(T* p, const float* v) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = __float2half_rn(v[i]);
+  }
+};
+
+__device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
+
+// Block maximum over the 8 lanes holding one 64-value group.
+__device__ __forceinline__ float group_max8(float v) {
+  v = xor_max(v, 1);
+  v = xor_max(v, 2);
+  v = xor_max(v, 4);
+  return v;
+}
+
+// HiF4 QDQ of the 8 values a lane owns (signed, |x| based).  Lanes 8j..8j+7 must hold
+// one 64-value group in order.  `nan_in_group` reproduces the reference's NaN
+// propagation: a NaN anywhere in a block makes the whole block NaN.
+template <int LV>
+__device__ __forceinline__ void qdq8(float* v, float* s_out = nullptr, float* rec_out = nullptr,
+                                     int* ka_out = nullptr, int* kb_out = nullptr, uint32_t* codes = nullptr) {
+  float m3a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  float m3b = fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7])));
+  int nan = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) nan |= v[i] != v[i];
+  nan = __shfl_xor(nan, 1, 64) | nan;
+  nan = __shfl_xor(nan, 2, 64) | nan;
+  nan = __shfl_xor(nan, 4, 64) | nan;
+  const float m1 = group_max8(fmaxf(m3a, m3b));
+  float s, rec;
+  hif4_scale<LV>(m1, s, rec);
+  int ka, kb;
+  hif4_micro<LV>(m3a, m3b, rec, ka, kb);
+  float qa, da, qb, db;
+  hif4_group_mults(s, rec, ka, qa, da);
+  hif4_group_mults(s, rec, kb, qb, db);
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float qm4 = i < 4 ? qa : qb;
+    const float dq = i < 4 ? da : db;
+    const float a = fabsf(v[i]);
+    if (codes) {
+      const uint32_t c = hif4_code(a, qm4);
+      packed |= ((v[i] < 0.0f ? 8u : 0u) | c) << (4 * i);
+    }
+    const float y = hif4_element(a, qm4, dq);
+    v[i] = nan ? __builtin_nanf("") : (v[i] < 0.0f ? -y : y);
+  }
+  if (s_out) *s_out = s;
+  if (rec_out) *rec_out = rec;
+  if (ka_out) *ka_out = ka;
+  if (kb_out) *kb_out = kb;
+  if (codes) *codes = packed;
+}
+
+// ------------------------------------------------------------------ qdq_rows
+
+struct QdqRowsArgs {
+  const void* x;
+  void* y;
+  int64_t rows;
+  int64_t cols;
+  int vec;  // 1: rows are 16-byte aligned and cols % 8 == 0
+  float* scale;      // [rows, groups] or null
+  float* rec;        // [rows, groups] or null
+  int8_t* lv2;       // [rows, groups, 8] or null
+  int8_t* lv3;       // [rows, groups, 16] or null
+  uint8_t* codes;    // [rows, cols / 2] or null (cols % 64 == 0)
+  uint8_t* scale_byte;   // [rows, groups] or null
+  uint8_t* lv2_bits;     // [rows, groups] or null
+  uint16_t* lv3_bits;    // [rows, groups] or null
+};
+
+template <typename T, int LV>
+__global__ __launch_bounds__(256) void qdq_rows_kernel(QdqRowsArgs a) {
+  const int64_t groups = (a.cols + 63) / 64;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t unit = tid >> 3;  // one (row, group)
+  const int part = threadIdx.x & 7;
+  // Lanes past the end still take part in the shuffles (with zeros) but store nothing.
+  const bool live = unit < a.rows * groups;
+  const int64_t row = live ? unit / groups : 0;
+  const int64_t g = live ? unit % groups : 0;
+  const int64_t c0 = g * 64 + part * 8;
+  const T* x = static_cast<const T*>(a.x) + row * a.cols;
+  T* y = static_cast<T*>(a.y) + row * a.cols;
+  float v[8];
+  if (live && a.vec && c0 < a.cols) {
+    Io<T>::load8(x + c0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (live && c0 + i < a.cols) ? Io<T>::load(x + c0 + i) : 0.0f;
+  }
+  float s, rec;
+  int ka, kb;
+  uint32_t codes = 0;
+  qdq8<LV>(v, &s, &rec, &ka, &kb, a.codes ? &codes : nullptr);
+  if (!live) return;
+  if (a.vec && c0 < a.cols) {
+    Io<T>::store8(y + c0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (c0 + i < a.cols) Io<T>::store(y + c0 + i, v[i]);
+  }
+  const int64_t gi = row * groups + g;
+  // k = lv2 + lv3 per 4-group.  For levels 123, lv2 = 1 forces the larger 4-group to
+  // lv3 = 1 (its m3 rec is the 8-group's m2 rec >= 4), so lv2 = [ka == 2 or kb == 2].
+  const int e2 = LV == 123 ? (ka == 2 || kb == 2) : (LV == 12 ? ka : 0);
+  const int e3a = ka - e2;
+  const int e3b = kb - e2;
+  if (a.lv2) a.lv2[gi * 8 + part] = static_cast<int8_t>(e2);
+  if (a.lv3) {
+    a.lv3[gi * 16 + 2 * part] = static_cast<int8_t>(e3a);
+    a.lv3[gi * 16 + 2 * part + 1] = static_cast<int8_t>(e3b);
+  }
+  if (a.scale && part == 0) a.scale[gi] = s;
+  if (a.rec && part == 0) a.rec[gi] = rec;
+  if (a.codes) *reinterpret_cast<uint32_t*>(a.codes + row * (a.cols / 2) + c0 / 2) = codes;
+  if (a.scale_byte || a.lv2_bits || a.lv3_bits) {
+    // The 8 lanes of a group share one byte of lv2 bits and 16 lv3 bits.
+    uint32_t b2 = static_cast<uint32_t>(e2) << part;
+    uint32_t b3 = (static_cast<uint32_t>(e3a) | (static_cast<uint32_t>(e3b) << 1)) << (2 * part);
+    // (reductions run on live lanes only; a group's 8 lanes are all live or all dead)
+    b2 |= __shfl_xor(b2, 1, 8);
+    b2 |= __shfl_xor(b2, 2, 8);
+    b2 |= __shfl_xor(b2, 4, 8);
+    b3 |= __shfl_xor(b3, 1, 8);
+    b3 |= __shfl_xor(b3, 2, 8);
+    b3 |= __shfl_xor(b3, 4, 8);
+    if (part == 0) {
+      if (a.lv2_bits) a.lv2_bits[gi] = static_cast<uint8_t>(b2);
+      if (a.lv3_bits) a.lv3_bits[gi] = static_cast<uint16_t>(b3);
+      if (a.scale_byte) {
+        const uint32_t b = __float_as_uint(s);
+        const int e = static_cast<int>(b >> 23) - 127;
+        a.scale_byte[gi] = static_cast<uint8_t>(((e + 48) << 2) | ((b >> 21) & 3u));
+      }
+    }
+  }
+}
+
+
+// ------------------------------------------------------------------ Hadamard
+
+// In-register stages of stride 1, 2, 4 (8 consecutive values per lane), then
+// cross-lane stages of stride 8 m for m = 1, 2, ... < n / 8, pairing lane l with l ^ m.
+// Each stage writes (left + right, left - right) with the left half at the lower
+// index, the order of rotation.py:21-28.
+__device__ __forceinline__ void fwht8_lanes(float* v, int n) {
+#pragma unroll
+  for (int s = 1; s < 8; s <<= 1) {
+    if (s >= n) break;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if ((i & s) == 0) {
+        const float l = v[i];
+        const float r = v[i + s];
+        v[i] = l + r;
+        v[i + s] = l - r;
+      }
+    }
+  }
+  for (int m = 1; m * 8 < n; m <<= 1) {
+    const bool upper = (threadIdx.x & m) != 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float other = __shfl_xor(v[i], m, 64);
+      v[i] = upper ? other - v[i] : v[i] + other;
+    }
+  }
+}
+
+struct HadamardRowsArgs {
+  const void* x;
+  void* y;
+  int64_t rows;
+  int64_t cols;   // multiple of n and of 8
+  int n;          // block size, power of two in [2, 512]
+  float sqrt_n;   // fp32(sqrt(n)); the transform divides by it (true division)
+};
+
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(256) void hadamard_rows_kernel(HadamardRowsArgs a) {
+  const int64_t lanes_per_row = a.cols / 8;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool live = tid < a.rows * lanes_per_row;
+  const int64_t row = live ? tid / lanes_per_row : 0;
+  const int64_t c0 = live ? (tid % lanes_per_row) * 8 : 0;
+  float v[8];
+  if (live) {
+    Io<Tin>::load8(static_cast<const Tin*>(a.x) + row * a.cols + c0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  }
+  fwht8_lanes(v, a.n);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = v[i] / a.sqrt_n;
+  if (live) Io<Tout>::store8(static_cast<Tout*>(a.y) + row * a.cols + c0, v);
+}
+
+// ------------------------------------------------------------------ operand prologue
+
+struct OperandPrepArgs {
+  const void* x;                 // [B, H, L, 128], last stride 1
+  int64_t sb, sh, sl;            // element strides of x
+  int B, H, L;
+  const float* key_offset;       // subtracted first (keys), [H or 1, 128] or null
+  int64_t off_sh;                // head stride of key_offset (0 to broadcast)
+  const float* smooth;           // Smooth-QK scale, [H or 1, 128] or null
+  int64_t smooth_sh;
+  int smooth_divide;             // 1 for keys (k / s), 0 for queries (q * s)
+  int hadamard;                  // 0, 64 or 128
+  float sqrt_n;
+  void* rotated;                 // optional: the rotated operand in the round dtype, [B, H, L, 128] contiguous
+  void* y;                       // bf16 output [B, H, L, 128] with strides below
+  int64_t yb, yh, yl;
+  int quant;                     // 1: HiF4 QDQ after the cast
+};
+
+// One lane owns 8 of a row's 128 values; a row spans 16 lanes.
+template <typename Tin, typename Tround, int LV>
+__global__ __launch_bounds__(256) void operand_prep_kernel(OperandPrepArgs a) {
+  const int64_t rows = static_cast<int64_t>(a.B) * a.H * a.L;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool live = (tid >> 4) < rows;
+  const int64_t r = live ? (tid >> 4) : 0;
+  const int part = threadIdx.x & 15;
+  const int l = static_cast<int>(r % a.L);
+  const int h = static_cast<int>((r / a.L) % a.H);
+  const int b = static_cast<int>(r / (static_cast<int64_t>(a.L) * a.H));
+  const int d0 = part * 8;
+  float v[8];
+  if (live) {
+    Io<Tin>::load8(static_cast<const Tin*>(a.x) + b * a.sb + h * a.sh + l * a.sl + d0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  }
+  if (a.key_offset) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] - a.key_offset[h * a.off_sh + d0 + i];
+  }
+  if (a.smooth) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float sc = a.smooth[h * a.smooth_sh + d0 + i];
+      v[i] = a.smooth_divide ? v[i] / sc : v[i] * sc;
+    }
+  }
+  if (a.hadamard) {
+    fwht8_lanes(v, a.hadamard);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] / a.sqrt_n;
+  }
+  // the single cast back to the operand dtype (qwen3.py:129-130)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = Io<Tround>::round(v[i]);
+  if (a.rotated && live) Io<Tround>::store8(static_cast<Tround*>(a.rotated) + r * 128 + d0, v);
+  if (a.quant) qdq8<LV>(v);
+  if (live) {
+    Io<__hip_bfloat16>::store8(
+        reinterpret_cast<__hip_bfloat16*>(static_cast<uint16_t*>(a.y) + b * a.yb + h * a.yh + l * a.yl + d0), v);
+  }
+}
+
+struct OperandPrepVtArgs {
+  const void* x;            // V [B, H, L, 128], last stride 1
+  int64_t sb, sh, sl;
+  int B, H, L;
+  int Lpad;                 // multiple of 128, >= L
+  uint16_t* vt;             // bf16 [B, H, 128, Lpad]
+  int quant;
+};
+
+// 64 keys x 128 dims per block: QDQ rows in registers, transpose through LDS, store
+// 16-byte runs of keys for each dim.  Keys >= L are zeros.
+template <typename Tin, int LV>
+__global__ __launch_bounds__(256) void operand_prep_vt_kernel(OperandPrepVtArgs a) {
+  constexpr int KB = 64;
+  constexpr int PITCH = KB + 8;  // uint16 elements per LDS row (16-byte aligned rows)
+  __shared__ uint16_t tile[128 * PITCH];
+  const int bh = blockIdx.y;
+  const int b = bh / a.H;
+  const int h = bh % a.H;
+  const int key0 = blockIdx.x * KB;
+  const int part = threadIdx.x & 15;
+  const int d0 = part * 8;
+  const Tin* x = static_cast<const Tin*>(a.x) + b * a.sb + h * a.sh;
+#pragma unroll
+  for (int it = 0; it < KB / 16; ++it) {
+    const int rr = it * 16 + (threadIdx.x >> 4);
+    const int key = key0 + rr;
+    float v[8];
+    if (key < a.L) {
+      Io<Tin>::load8(x + static_cast<int64_t>(key) * a.sl + d0, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = Io<Tin>::round(v[i]);
+    if (a.quant) qdq8<LV>(v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tile[(d0 + i) * PITCH + rr] = f32_to_bf16_bits_rne(v[i]);
+  }
+  __syncthreads();
+  uint16_t* out = a.vt + (static_cast<int64_t>(b) * a.H + h) * 128 * a.Lpad + key0;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int c = threadIdx.x + 256 * it;
+    const int d = c >> 3;
+    const int k8 = (c & 7) * 8;
+    const uint4 w = *reinterpret_cast<const uint4*>(&tile[d * PITCH + k8]);
+    *reinterpret_cast<uint4*>(out + static_cast<int64_t>(d) * a.Lpad + k8) = w;
+  }
+}
+
+}  // namespace faq

@@ -1,0 +1,115 @@
+"""ctypes binding of ``libfaquant_amd.so`` (the C ABI in include/faquant_amd.h).
+
+The library is built in-tree by ``faquant-public_amd/build.py``.  There is no
+fallback: if the library is missing or a tensor is not on a ROCm device, the
+call raises.  Status codes map to the exception types the reference raises
+for the same conditions (ValueError / NotImplementedError).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_NAME = "libfaquant_amd.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+F32, BF16, F16 = 0, 1, 2
+_DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+OK, EINVAL, EUNSUP, ELAUNCH = 0, -1, -2, -3
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_float = ctypes.c_float
+_vp = ctypes.c_void_p
+
+_SIGNATURES = {
+    "faq_last_error": ([], ctypes.c_char_p),
+    "faq_version": ([], ctypes.c_char_p),
+    "faq_hif4_qdq_rows": (
+        [_vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+        _c_int,
+    ),
+    "faq_hadamard_rows": ([_vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp], _c_int),
+    "faq_operand_prep": (
+        [
+            _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+            _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _vp,
+        ],
+        _c_int,
+    ),
+    "faq_operand_prep_vt": (
+        [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_int, _vp],
+        _c_int,
+    ),
+    "faq_attention_fwd": (
+        [
+            _vp, _c_i64, _c_i64, _c_i64,
+            _vp, _c_i64, _c_i64, _c_i64,
+            _vp, _c_i64, _c_i64, _c_i64, _c_int,
+            _vp, _c_int, _c_i64, _c_i64, _c_i64,
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp, _vp,
+        ],
+        _c_int,
+    ),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP extension first "
+                "(python faquant-public_amd/build.py, or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    if status == OK:
+        return
+    message = load().faq_last_error().decode(errors="replace")
+    if status == EUNSUP:
+        raise NotImplementedError(message)
+    if status == EINVAL:
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}") from None
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError(
+                "faquant_amd kernels run on the MI355X: move tensors to a ROCm device "
+                "(this build has no CPU path)"
+            )
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

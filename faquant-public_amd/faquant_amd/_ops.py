@@ -1,0 +1,232 @@
+"""Tensor-level launchers over the C ABI: allocate outputs, check shapes, launch.
+
+All tensors must live on a ROCm device; every launch is enqueued on the current
+torch stream of that device.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+KEY_TILE = 128
+
+
+def _pad_keys(length: int) -> int:
+    return max(KEY_TILE, (length + KEY_TILE - 1) // KEY_TILE * KEY_TILE)
+
+
+def qdq_rows(
+    x: torch.Tensor,
+    levels: str,
+    *,
+    out: torch.Tensor | None = None,
+    compact: bool = False,
+    packed: bool = False,
+):
+    """HiF4 QDQ of ``x`` along its last axis (any leading shape); returns y (and metadata).
+
+    ``compact`` adds (scale, rec, lv2, lv3) shaped like the reference's
+    CompactHiF4Parameters for the grouped view [..., groups, 64]; ``packed`` adds
+    (codes [..., C/2] uint8, scale_byte, lv2_bits, lv3_bits).
+    """
+    _lib.require_device(x)
+    lib = _lib.load()
+    cols = x.shape[-1]
+    if x.ndim == 0:
+        raise ValueError("HiF4 fake quantization requires at least one dimension")
+    if cols == 0:
+        raise ValueError("HiF4 fake quantization does not support an empty axis")
+    xc = x.contiguous()
+    rows = xc.numel() // cols
+    y = torch.empty_like(xc) if out is None else out
+    groups = (cols + 63) // 64
+    lead = tuple(x.shape[:-1])
+    extra = {}
+    if compact:
+        extra["scale"] = torch.empty(lead + (groups, 1, 1, 1), device=x.device, dtype=torch.float32)
+        extra["rec"] = torch.empty_like(extra["scale"])
+        extra["lv2"] = torch.empty(lead + (groups, 8, 1, 1), device=x.device, dtype=torch.int8)
+        extra["lv3"] = torch.empty(lead + (groups, 8, 2, 1), device=x.device, dtype=torch.int8)
+    if packed:
+        if cols % 64:
+            raise ValueError("packed HiF4 codes need a width that is a multiple of 64")
+        extra["codes"] = torch.empty(lead + (cols // 2,), device=x.device, dtype=torch.uint8)
+        extra["scale_byte"] = torch.empty(lead + (groups,), device=x.device, dtype=torch.uint8)
+        extra["lv2_bits"] = torch.empty(lead + (groups,), device=x.device, dtype=torch.uint8)
+        extra["lv3_bits"] = torch.empty(lead + (groups,), device=x.device, dtype=torch.uint16)
+    g = extra.get
+    _lib.check(
+        lib.faq_hif4_qdq_rows(
+            xc.data_ptr(), y.data_ptr(), rows, cols, _lib.dtype_code(x.dtype), int(levels),
+            _lib.ptr(g("scale")), _lib.ptr(g("rec")), _lib.ptr(g("lv2")), _lib.ptr(g("lv3")),
+            _lib.ptr(g("codes")), _lib.ptr(g("scale_byte")), _lib.ptr(g("lv2_bits")), _lib.ptr(g("lv3_bits")),
+            _lib.stream_ptr(x.device),
+        )
+    )
+    y = y.view(x.shape)
+    if not extra:
+        return y
+    return y, extra
+
+
+def hadamard_rows(x: torch.Tensor, block: int, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Block Hadamard over the last axis in fp32, rounded once to ``out_dtype``."""
+    _lib.require_device(x)
+    lib = _lib.load()
+    xc = x.contiguous()
+    cols = x.shape[-1]
+    rows = xc.numel() // cols if cols else 0
+    y = torch.empty(x.shape, device=x.device, dtype=out_dtype or x.dtype)
+    _lib.check(
+        lib.faq_hadamard_rows(
+            xc.data_ptr(), y.data_ptr(), rows, cols, int(block), _lib.dtype_code(x.dtype),
+            _lib.dtype_code(y.dtype), _lib.stream_ptr(x.device),
+        )
+    )
+    return y
+
+
+def _bhld_strides(x: torch.Tensor) -> tuple[int, int, int]:
+    if x.stride(-1) != 1:
+        raise ValueError("operands need a unit stride along head_dim")
+    return x.stride(0), x.stride(1), x.stride(2)
+
+
+def operand_prep(
+    x: torch.Tensor,
+    *,
+    levels: str | None,
+    hadamard: int = 0,
+    key_offset: torch.Tensor | None = None,
+    smooth: torch.Tensor | None = None,
+    smooth_divide: bool = False,
+    round_dtype: torch.dtype | None = None,
+    want_rotated: bool = False,
+    out: torch.Tensor | None = None,
+):
+    """Q/K operand prologue on x [B, H, L, 128] (any strides, unit last stride).
+
+    Returns the bf16 operand [B, H, L, 128] (or writes ``out``) and, when
+    ``want_rotated``, the rotated tensor in ``round_dtype`` before quantization.
+    """
+    _lib.require_device(x, key_offset, smooth)
+    lib = _lib.load()
+    if x.ndim != 4 or x.shape[-1] != HEAD_DIM:
+        raise NotImplementedError("the HIP operand prologue supports [B, H, L, 128] tensors")
+    B, H, L, _ = x.shape
+    sb, sh, sl = _bhld_strides(x)
+    rdt = round_dtype or x.dtype
+    y = torch.empty((B, H, L, HEAD_DIM), device=x.device, dtype=torch.bfloat16) if out is None else out
+    rot = torch.empty((B, H, L, HEAD_DIM), device=x.device, dtype=rdt) if want_rotated else None
+
+    def per_head(t):
+        if t is None:
+            return None, 0
+        t = t.to(device=x.device, dtype=torch.float32).contiguous()
+        if t.numel() == HEAD_DIM:
+            return t.reshape(HEAD_DIM), 0
+        if t.numel() == H * HEAD_DIM:
+            return t.reshape(H, HEAD_DIM), HEAD_DIM
+        raise ValueError(f"per-dim tensor must hold 128 or H*128 values, got shape {tuple(t.shape)}")
+
+    off, off_sh = per_head(key_offset)
+    sm, sm_sh = per_head(smooth)
+    _lib.check(
+        lib.faq_operand_prep(
+            x.data_ptr(), _lib.dtype_code(x.dtype), sb, sh, sl, B, H, L,
+            _lib.ptr(off), off_sh, _lib.ptr(sm), sm_sh, int(bool(smooth_divide)), int(hadamard),
+            _lib.dtype_code(rdt), _lib.ptr(rot), y.data_ptr(), y.stride(0), y.stride(1), y.stride(2),
+            int(levels) if levels else 0, _lib.stream_ptr(x.device),
+        )
+    )
+    return y, rot
+
+
+def operand_prep_vt(v: torch.Tensor, *, levels: str | None) -> torch.Tensor:
+    """V [B, H, L, 128] -> HiF4-QDQ'd, transposed bf16 [B, H, 128, Lpad] (zero padded)."""
+    _lib.require_device(v)
+    lib = _lib.load()
+    if v.ndim != 4 or v.shape[-1] != HEAD_DIM:
+        raise NotImplementedError("the HIP operand prologue supports [B, H, L, 128] tensors")
+    B, H, L, _ = v.shape
+    sb, sh, sl = _bhld_strides(v)
+    lpad = _pad_keys(L)
+    vt = torch.empty((B, H, HEAD_DIM, lpad), device=v.device, dtype=torch.bfloat16)
+    _lib.check(
+        lib.faq_operand_prep_vt(
+            v.data_ptr(), _lib.dtype_code(v.dtype), sb, sh, sl, B, H, L, lpad, vt.data_ptr(),
+            int(levels) if levels else 0, _lib.stream_ptr(v.device),
+        )
+    )
+    return vt
+
+
+def attention_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    vt: torch.Tensor,
+    key_length: int,
+    *,
+    causal: bool,
+    scale: float,
+    quant_p: bool,
+    p_levels: str,
+    norm_same: bool,
+    out: torch.Tensor,
+    row_den: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Attention over bf16 operands q [B, Hq, Lq, 128], k [B, Hkv, Lk, 128] and
+    vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16)."""
+    _lib.require_device(q, k, vt, out, row_den)
+    lib = _lib.load()
+    B, Hq, Lq, D = q.shape
+    Hkv = k.shape[1]
+    if D != HEAD_DIM or k.shape[-1] != HEAD_DIM:
+        raise NotImplementedError(f"the HIP attention kernel supports head_dim 128, got {D}")
+    for t in (q, k, vt):
+        if t.dtype != torch.bfloat16:
+            raise TypeError("attention operands must be bf16")
+    if out.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("attention output must be fp32 or bf16")
+    qs, ks_, vs = _bhld_strides(q), _bhld_strides(k), _bhld_strides(vt)
+    os_ = (out.stride(0), out.stride(1), out.stride(2))
+    if out.stride(3) != 1:
+        raise ValueError("attention output needs a unit stride along head_dim")
+    _lib.check(
+        lib.faq_attention_fwd(
+            q.data_ptr(), *qs, k.data_ptr(), *ks_, vt.data_ptr(), *vs, vt.shape[-1],
+            out.data_ptr(), _lib.dtype_code(out.dtype), *os_,
+            B, Hq, Hkv, Lq, int(key_length), int(bool(causal)), float(scale),
+            int(bool(quant_p)), int(p_levels), int(bool(norm_same)), _lib.ptr(row_den),
+            _lib.stream_ptr(q.device),
+        )
+    )
+    return out
+
+
+def attention_pairs(query_length: int, key_length: int, causal: bool) -> int:
+    """Unmasked (query, key) pairs; causal rows p see keys <= p + Lk - Lq."""
+    if not causal:
+        return query_length * key_length
+    seen = np.clip(np.arange(query_length, dtype=np.int64) + (key_length - query_length) + 1, 0, key_length)
+    return int(seen.sum())
+
+
+def attention_flops(batch: int, heads: int, query_length: int, key_length: int, causal: bool,
+                    head_dim: int = HEAD_DIM) -> float:
+    """Algorithmic QK + PV FLOPs: 4 B H D N_pairs (masked-out pairs not counted)."""
+    return 4.0 * batch * heads * head_dim * attention_pairs(query_length, key_length, causal)
+
+
+def default_scale(head_dim: int = HEAD_DIM) -> float:
+    return head_dim**-0.5
+
+
+def log2e() -> float:
+    return 1.0 / math.log(2.0)

@@ -1,0 +1,123 @@
+"""Qwen3 post-RoPE attention core on the MI355X (the hot-path part of faquant.qwen3).
+
+Reference: src/faquant/qwen3.py:90-166, the section of ``_attention_forward``
+between RoPE and ``o_proj``:
+  * one fp32 excursion over Q and K: key offset, Smooth-QK scale (with optional
+    ``exp(delta)``), 128-point or block Hadamard, one cast back   qwen3.py:90-130
+  * the simulated flash attention call                            qwen3.py:144-166
+``post_rope_qk_transform`` is that excursion as one HIP pass per operand.
+``attention_core`` fuses it with the Q/K/V QDQ and runs the attention kernel:
+three prologue passes and one attention launch, with the same result as the
+reference's excursion followed by ``simulated_flash_attention_forward``.
+Module attributes are the reference's (``faquant_qk_smooth_scale``,
+``faquant_qk_smooth_delta``, ``faquant_qk_key_offset``, ``faquant_qk_rotation``,
+``faquant_qk_rotation_block_size`` plus the simulator's).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _ops
+from .hif4 import HIF4_ATTN_OPERAND_SCALE_LEVELS
+from .simulated_flash_attention import _hif4_group, count_tiles, simulated_flash_attention_forward
+
+
+def _block(rotation: bool, rotation_block_size: Optional[int], head_dim: int) -> int:
+    if not rotation:
+        return 0
+    if rotation_block_size is None or rotation_block_size == head_dim:
+        return head_dim
+    if rotation_block_size not in (64, 128):
+        raise NotImplementedError(f"Hadamard block {rotation_block_size} is not implemented on the MI355X")
+    return rotation_block_size
+
+
+def _smooth(smooth_scale, smooth_delta):
+    if smooth_delta is not None:
+        if smooth_scale is None:
+            raise RuntimeError("Smooth-QK delta requires a frozen base scale")
+        smooth_scale = smooth_scale * smooth_delta.float().exp()
+    return smooth_scale
+
+
+def post_rope_qk_transform(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    *,
+    smooth_scale: Optional[torch.Tensor] = None,
+    smooth_delta: Optional[torch.Tensor] = None,
+    key_offset: Optional[torch.Tensor] = None,
+    rotation: bool = False,
+    rotation_block_size: Optional[int] = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Q [B, Hq, L, 128] and K [B, Hkv, L, 128] after the qwen3.py:97-130 excursion."""
+    smooth_scale = _smooth(smooth_scale, smooth_delta)
+    if smooth_scale is None and key_offset is None and not rotation:
+        return query, key
+    block = _block(rotation, rotation_block_size, query.shape[-1])
+    out = []
+    for t, is_key in ((query, False), (key, True)):
+        y, rot = _ops.operand_prep(
+            t, levels=None, hadamard=block, key_offset=key_offset if is_key else None,
+            smooth=smooth_scale, smooth_divide=is_key, round_dtype=t.dtype,
+            want_rotated=t.dtype != torch.bfloat16,
+        )
+        out.append(y if rot is None else rot)
+    return out[0], out[1]
+
+
+def attention_core(
+    module: torch.nn.Module,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    scaling: Optional[float] = None,
+) -> torch.Tensor:
+    """Post-RoPE Q/K/V -> attention output [B, L, Hq, 128], fused on the GPU.
+
+    Equivalent to the reference's excursion followed by
+    ``simulated_flash_attention_forward(module, q, k, v, None, scaling=scaling)``
+    for mask-free causal prefill; other cases go through that drop-in.
+    """
+    smooth_scale = _smooth(getattr(module, "faquant_qk_smooth_scale", None),
+                           getattr(module, "faquant_qk_smooth_delta", None))
+    key_offset = getattr(module, "faquant_qk_key_offset", None)
+    rotation = bool(getattr(module, "faquant_qk_rotation", False))
+    block = _block(rotation, getattr(module, "faquant_qk_rotation_block_size", None), query.shape[-1])
+    qk_quant = bool(module.faquant_qk_matmul_quant)
+    pv_quant = bool(module.faquant_pv_matmul_quant)
+    if query.dtype != torch.bfloat16 or int(module.faquant_attention_key_chunk_size) != _ops.KEY_TILE:
+        q, k = post_rope_qk_transform(
+            query, key, smooth_scale=smooth_scale, key_offset=key_offset, rotation=rotation,
+            rotation_block_size=getattr(module, "faquant_qk_rotation_block_size", None),
+        )
+        return simulated_flash_attention_forward(module, q, k, value, None, scaling=scaling)[0]
+    quant_kwargs = module.faquant_matmul_quant_kwargs
+    qk_group = _hif4_group(getattr(module, "faquant_qk_matmul_quant_kwargs", quant_kwargs), "QK") if qk_quant else 64
+    pv_group = _hif4_group(getattr(module, "faquant_pv_matmul_quant_kwargs", quant_kwargs), "PV") if pv_quant else 64
+    levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
+    q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None, hadamard=block,
+                                smooth=smooth_scale, round_dtype=torch.bfloat16)
+    k_op, _ = _ops.operand_prep(key, levels=levels["k"] if qk_quant else None, hadamard=block,
+                                key_offset=key_offset, smooth=smooth_scale, smooth_divide=True,
+                                round_dtype=torch.bfloat16)
+    vt = _ops.operand_prep_vt(value, levels=levels["v"] if pv_quant else None)
+    B, Hq, Lq, D = query.shape
+    Lk = key.shape[2]
+    scale = float(scaling if scaling is not None else D**-0.5)
+    causal = bool(getattr(module, "is_causal", True))
+    out = torch.empty((B, Lq, Hq, D), device=query.device, dtype=query.dtype)
+    mode = getattr(module, "faquant_pv_normalizer_mode", "unquantized")
+    _ops.attention_fwd(q_op, k_op, vt, Lk, causal=causal, scale=scale, quant_p=pv_quant,
+                       p_levels=levels["p"], norm_same=mode == "quantized_same", out=out.transpose(1, 2))
+    count_tiles(
+        module.faquant_simulated_attention_stats, batch=B, query_heads=Hq, query_length=Lq, key_length=Lk,
+        head_dim=D, query_chunk=int(module.faquant_attention_query_chunk_size), key_chunk=_ops.KEY_TILE,
+        causal=causal, skip_fully_masked=bool(getattr(module, "faquant_skip_fully_masked_tiles", True)),
+        qk_quant=qk_quant, pv_quant=pv_quant, qk_group=qk_group, pv_group=pv_group,
+    )
+    return out

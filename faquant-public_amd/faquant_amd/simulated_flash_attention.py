@@ -1,0 +1,248 @@
+"""HiF4 QK/PV flash attention on the MI355X: drop-in for faquant.simulated_flash_attention.
+
+``simulated_flash_attention_forward`` keeps the reference signature, module
+attributes, validation messages, stats counters and output layout
+(src/faquant/simulated_flash_attention.py:457-909), and computes the same
+recurrence in two HIP launches: an operand prologue (HiF4 QDQ of Q, K and V;
+V is written transposed for the PV MFMA operand) and the attention kernel.
+
+Supported on the GPU: head_dim 128, key tiles of 128 (the reference default),
+the HiF4 format with groups of 64 (or no quantization), causal (bottom-right)
+or full attention, attention_mask None or an all-valid 2-D mask, bf16 or fp32
+inputs.  Everything else the reference accepts (padding ranks, sliding window,
+softcap, 4-D masks, int/MXFP8 formats, the PV-normalizer probe) raises
+NotImplementedError: there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _ops
+from .config import PV_NORMALIZER_MODES
+from .hif4 import HIF4_ATTN_OPERAND_SCALE_LEVELS, HIF4_BLOCK_SIZE
+
+SIMULATED_ATTENTION_IMPLEMENTATION = "faquant_simulated"
+
+_QUANTIZED_OPERANDS = ("q", "k", "p", "v")
+
+PV_MASS_RATIO_BIN_EDGES = (0.5, 0.7, 0.8, 0.9, 0.95, 0.99, 1.0, 1.01, 1.05, 1.1, 1.3)
+
+
+def new_simulated_attention_stats() -> dict[str, int]:
+    """Zeroed counters of one attention runtime (sfa:18-33)."""
+    stats = {"calls": 0, "qk_tiles": 0, "pv_tiles": 0, "qk_quantized_tiles": 0, "pv_quantized_tiles": 0}
+    for operand in _QUANTIZED_OPERANDS:
+        for field in ("quant_calls", "quantized_values", "quant_blocks", "quant_padding_values"):
+            stats[f"{operand}_{field}"] = 0
+    return stats
+
+
+def register_simulated_attention_backend() -> None:
+    """Register this attention with the transformers attention/mask registries (sfa:214-228)."""
+    from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, flash_attention_mask
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    ALL_ATTENTION_FUNCTIONS.register(SIMULATED_ATTENTION_IMPLEMENTATION, simulated_flash_attention_forward)
+    ALL_MASK_ATTENTION_FUNCTIONS.register(SIMULATED_ATTENTION_IMPLEMENTATION, flash_attention_mask)
+
+
+def _record(stats: dict, operand: str, width: int, numel: int, group_size: int, repeats: int) -> None:
+    """Logical and padded geometry of one operand QDQ (sfa:187-211)."""
+    g = width if group_size == -1 else group_size
+    groups = math.ceil(width / g)
+    vectors = numel // width
+    stats[f"{operand}_quant_calls"] += repeats
+    stats[f"{operand}_quantized_values"] += numel * repeats
+    stats[f"{operand}_quant_blocks"] += vectors * groups * repeats
+    stats[f"{operand}_quant_padding_values"] += vectors * (groups * g - width) * repeats
+
+
+def count_tiles(
+    stats: dict,
+    *,
+    batch: int,
+    query_heads: int,
+    query_length: int,
+    key_length: int,
+    head_dim: int,
+    query_chunk: int,
+    key_chunk: int,
+    causal: bool,
+    skip_fully_masked: bool,
+    qk_quant: bool,
+    pv_quant: bool,
+    qk_group: int,
+    pv_group: int,
+) -> None:
+    """The simulator's counters in closed form: its query-tile / key-tile schedule
+    (sfa:623-697, 886-908) replayed without computing anything."""
+    passes = []
+    full = query_length // query_chunk
+    if full:
+        passes.append((0, query_chunk, full))
+    tail = full * query_chunk
+    if tail < query_length:
+        passes.append((tail, query_length - tail, 1))
+    tiles_done = 0
+    for q0, rows, tiles in passes:
+        if qk_quant:
+            _record(stats, "q", head_dim, batch * query_heads * rows * head_dim, qk_group, tiles)
+        for k0 in range(0, key_length, key_chunk):
+            kw = min(k0 + key_chunk, key_length) - k0
+            first = 0
+            if skip_fully_masked and causal:
+                first = max(0, min(tiles, (k0 - (key_length - query_length) - q0) // rows))
+            active = tiles - first
+            if active == 0:
+                continue
+            if qk_quant:
+                _record(stats, "k", head_dim, batch * query_heads * kw * head_dim, qk_group, active)
+            if pv_quant:
+                _record(stats, "p", kw, batch * query_heads * rows * kw, pv_group, active)
+                _record(stats, "v", head_dim, batch * query_heads * kw * head_dim, pv_group, active)
+            tiles_done += active
+    stats["calls"] += 1
+    stats["qk_tiles"] += tiles_done
+    stats["pv_tiles"] += tiles_done
+    if qk_quant:
+        stats["qk_quantized_tiles"] += tiles_done
+    if pv_quant:
+        stats["pv_quantized_tiles"] += tiles_done
+
+
+def _hif4_group(kwargs: dict, what: str) -> int:
+    """Validate matmul quant kwargs for the HIP path; return the group size."""
+    fmt = kwargs.get("quant_format", "int")
+    if fmt != "hif4":
+        raise NotImplementedError(f"{what} quantization with quant_format={fmt!r} is not implemented on the MI355X")
+    if kwargs.get("bits", 4) != 4:
+        raise ValueError("HiF4 requires bits=4")
+    group = kwargs.get("group_size", -1)
+    if group not in (-1, HIF4_BLOCK_SIZE):
+        raise ValueError("HiF4 requires group_size=64 (or -1 for direct use)")
+    if not kwargs.get("symmetric", True):
+        raise ValueError("HiF4 does not support asymmetric quantization")
+    if kwargs.get("clip_ratio", 1.0) != 1.0:
+        raise ValueError("HiF4 direct-cast does not support clipping")
+    return HIF4_BLOCK_SIZE if group == -1 else group
+
+
+def simulated_flash_attention_forward(
+    module: torch.nn.Module,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    attention_mask: Optional[torch.Tensor],
+    dropout: float = 0.0,
+    scaling: Optional[float] = None,
+    sliding_window: Optional[int] = None,
+    softcap: Optional[float] = None,
+    **kwargs: object,
+) -> tuple[torch.Tensor, None]:
+    """Tiled HiF4 flash attention (reference sfa:457-909) on the MI355X."""
+    if dropout:
+        raise ValueError("simulated FlashAttention only supports dropout=0 inference")
+    if softcap is not None and softcap < 0:
+        raise ValueError("softcap must be non-negative")
+    if sliding_window is not None and sliding_window <= 0:
+        raise ValueError("sliding_window must be positive")
+    if kwargs.get("output_attentions", False):
+        raise ValueError("simulated FlashAttention does not materialize attention weights")
+    if query.ndim != 4 or key.ndim != 4 or value.ndim != 4:
+        raise ValueError("simulated FlashAttention expects rank-4 Q/K/V tensors")
+    if key.shape != value.shape:
+        raise ValueError("simulated FlashAttention requires matching K/V shapes")
+    if query.shape[0] != key.shape[0] or query.shape[-1] != key.shape[-1]:
+        raise ValueError("simulated FlashAttention received incompatible Q/K shapes")
+    if any(kwargs.get(n) is not None for n in ("cu_seq_lens_q", "cu_seq_lens_k", "max_length_q", "max_length_k")):
+        raise NotImplementedError("packed cu_seqlens are not supported by the simulator")
+    position_ids = kwargs.get("position_ids")
+    if attention_mask is None and isinstance(position_ids, torch.Tensor) and position_ids.shape[-1] > 1:
+        if torch.any(position_ids[..., 1:] <= position_ids[..., :-1]):
+            raise NotImplementedError("packed/reset position_ids are not supported")
+
+    valid_key_length = key.shape[-2]
+    if attention_mask is not None:
+        valid_key_length = min(valid_key_length, attention_mask.shape[-1])
+    cache_position = kwargs.get("cache_position")
+    if isinstance(cache_position, torch.Tensor) and cache_position.numel():
+        valid_key_length = min(valid_key_length, int(cache_position.max().item()) + 1)
+    if valid_key_length < key.shape[-2]:
+        key = key[:, :, :valid_key_length]
+        value = value[:, :, :valid_key_length]
+
+    batch, query_heads, query_length, head_dim = query.shape
+    _, kv_heads, key_length, _ = key.shape
+    if query_heads % kv_heads:
+        raise ValueError("query heads must be divisible by key/value heads")
+    if any(size == 0 for size in query.shape) or key_length == 0:
+        raise ValueError("simulated FlashAttention does not support zero dimensions")
+
+    scale = float(scaling if scaling is not None else head_dim**-0.5)
+    query_chunk = int(module.faquant_attention_query_chunk_size)
+    key_chunk = int(module.faquant_attention_key_chunk_size)
+    quant_kwargs = module.faquant_matmul_quant_kwargs
+    qk_quant_kwargs = getattr(module, "faquant_qk_matmul_quant_kwargs", quant_kwargs)
+    pv_quant_kwargs = getattr(module, "faquant_pv_matmul_quant_kwargs", quant_kwargs)
+    qk_quant = bool(module.faquant_qk_matmul_quant)
+    pv_quant = bool(module.faquant_pv_matmul_quant)
+    mode = getattr(module, "faquant_pv_normalizer_mode", "unquantized")
+    if mode not in PV_NORMALIZER_MODES:
+        raise ValueError(f"unsupported pv_normalizer_mode {mode!r}; expected one of {PV_NORMALIZER_MODES}")
+    requested_causal = kwargs.get("is_causal")
+    is_causal = bool(getattr(module, "is_causal", True) if requested_causal is None else requested_causal)
+    skip = bool(getattr(module, "faquant_skip_fully_masked_tiles", True))
+
+    if attention_mask is not None:
+        if attention_mask.ndim == 2:
+            if not bool(torch.all(attention_mask[:, -key_length:]).item()):
+                raise NotImplementedError("padding masks (rank-based causal alignment) are not implemented on the MI355X")
+            attention_mask = None  # an all-valid mask is the mask-free bottom-right case
+        elif attention_mask.ndim in (3, 4):
+            raise NotImplementedError("3-D/4-D attention masks are not implemented on the MI355X")
+        else:
+            raise ValueError("attention mask must be rank 2, 3, or 4")
+    if sliding_window is not None:
+        raise NotImplementedError("sliding-window attention is not implemented on the MI355X")
+    if softcap:
+        raise NotImplementedError("logit softcap is not implemented on the MI355X")
+    if key_chunk != _ops.KEY_TILE:
+        raise NotImplementedError(f"the HIP kernel uses key tiles of {_ops.KEY_TILE}, got {key_chunk}")
+    if query_chunk <= 0:
+        raise ValueError("attention query chunk size must be positive")
+    if head_dim != _ops.HEAD_DIM:
+        raise NotImplementedError(f"the HIP kernel supports head_dim {_ops.HEAD_DIM}, got {head_dim}")
+    for t in (query, key, value):
+        if t.dtype not in (torch.float32, torch.bfloat16):
+            raise NotImplementedError(f"the HIP attention path takes bf16 or fp32 operands, got {t.dtype}")
+    qk_group = _hif4_group(qk_quant_kwargs, "QK") if qk_quant else 64
+    pv_group = _hif4_group(pv_quant_kwargs, "PV") if pv_quant else 64
+    if pv_quant and isinstance(getattr(module, "faquant_pv_normalizer_diagnostics", None), dict):
+        raise NotImplementedError("the PV normalizer probe is not implemented on the MI355X")
+
+    levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
+    q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None)
+    k_op, _ = _ops.operand_prep(key, levels=levels["k"] if qk_quant else None)
+    vt = _ops.operand_prep_vt(value, levels=levels["v"] if pv_quant else None)
+    # The reference caches K/V QDQ values for decode (sfa:243-289); the HIP path keeps
+    # the quantized operands under the same names (V as a [B, Hkv, L, 128] view).
+    module.faquant_k_matmul_qdq_cache = k_op if qk_quant else None
+    module.faquant_v_matmul_qdq_cache = vt.transpose(-1, -2)[..., :key_length, :] if pv_quant else None
+
+    output = torch.empty((batch, query_length, query_heads, head_dim), device=query.device, dtype=query.dtype)
+    _ops.attention_fwd(
+        q_op, k_op, vt, key_length,
+        causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
+        norm_same=mode == "quantized_same", out=output.transpose(1, 2),
+    )
+    count_tiles(
+        module.faquant_simulated_attention_stats,
+        batch=batch, query_heads=query_heads, query_length=query_length, key_length=key_length,
+        head_dim=head_dim, query_chunk=query_chunk, key_chunk=key_chunk, causal=is_causal,
+        skip_fully_masked=skip, qk_quant=qk_quant, pv_quant=pv_quant, qk_group=qk_group, pv_group=pv_group,
+    )
+    return output, None

@@ -1,0 +1,132 @@
+/*
+ * faquant_amd.h -- C ABI of the MI355X (gfx950) HiF4 attention path.
+ *
+ * Every entry point takes raw device pointers, sizes and element strides, writes into
+ * caller-allocated outputs, enqueues its kernels on the given HIP stream and returns 0
+ * or a negative status (FAQ_E*).  faq_last_error() returns a thread-local message for
+ * the last failure on the calling thread.  No entry point allocates or keeps device
+ * memory and none synchronizes the stream.  Pointers to float data must be 16-byte
+ * aligned and rows must have a unit last-dimension stride.
+ *
+ * dtype codes: FAQ_F32 = 0, FAQ_BF16 = 1, FAQ_F16 = 2.
+ * HiF4 levels: 123 (E6M2 per 64 + 1-bit exponents per 8 and per 4), 12, 13.
+ *
+ * Reference interfaces replaced (paths in MingZwhy/FAQUANT-Public):
+ *   faq_hif4_qdq_rows     src/faquant/hif4.py:143-219 fit_hif4_compact_parameters,
+ *                         hif4.py:377-390 fake_quantize_hif4,
+ *                         src/faquant/quantization.py:30-57 fake_quantize(quant_format="hif4"),
+ *                         src/faquant/wan22_attention.py:97-102 qdq_rows_128
+ *   faq_hadamard_rows     src/faquant/rotation.py:14-29 hadamard_transform,
+ *                         rotation.py:117-135 chunked_block_hadamard_transform,
+ *                         src/faquant/wan22_attention.py:186-192 rotate_heads
+ *   faq_operand_prep      src/faquant/qwen3.py:97-136 (post-RoPE fp32 excursion: key offset,
+ *                         Smooth-QK, Hadamard, one cast) and the Q/K QDQ of
+ *                         src/faquant/simulated_flash_attention.py:592-619
+ *   faq_operand_prep_vt   the V QDQ of simulated_flash_attention.py:600-611
+ *                         (written transposed for the PV operand)
+ *   faq_attention_fwd     src/faquant/simulated_flash_attention.py:457-909
+ *                         simulated_flash_attention_forward (key tiles of 128, masks: none /
+ *                         bottom-right causal) and src/faquant/wan22_attention.py:165-183
+ *                         hif4_attention
+ */
+#ifndef FAQUANT_AMD_H
+#define FAQUANT_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FAQ_OK 0
+#define FAQ_EINVAL (-1)  /* invalid argument */
+#define FAQ_EUNSUP (-2)  /* valid in the reference but not implemented by this library */
+#define FAQ_ELAUNCH (-3) /* HIP launch error */
+
+#define FAQ_F32 0
+#define FAQ_BF16 1
+#define FAQ_F16 2
+
+typedef void* faq_stream_t; /* hipStream_t */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* faq_last_error(void);
+
+/* Library version string. */
+const char* faq_version(void);
+
+/*
+ * HiF4 fake quantization of `rows` rows of `cols` values (row stride = cols), along
+ * the row in groups of 64 with zero padding of a short last group; y has x's dtype
+ * (FAQ_F32 / FAQ_BF16 / FAQ_F16) and may alias x.  Optional outputs (NULL to skip),
+ * with groups = ceil(cols / 64):
+ *   scale, rec      fp32 [rows, groups]   E6M2 scale and bf16 reciprocal
+ *   lv2             int8 [rows, groups, 8]   level-2 exponents (per 8 values)
+ *   lv3             int8 [rows, groups, 16]  level-3 exponents (per 4 values)
+ *   codes           uint8 [rows, cols / 2]   4-bit codes, value 2i in the low nibble
+ *                   (bit 3 sign, bits 0-2 magnitude); requires cols % 64 == 0
+ *   scale_byte      uint8 [rows, groups]  ((e + 48) << 2) | m with scale = 2^e (1 + m/4)
+ *   lv2_bits        uint8 [rows, groups]  bit i = lv2 of 8-group i
+ *   lv3_bits        uint16 [rows, groups] bit i = lv3 of 4-group i
+ */
+int faq_hif4_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, int levels,
+                      float* scale, float* rec, int8_t* lv2, int8_t* lv3, uint8_t* codes,
+                      uint8_t* scale_byte, uint8_t* lv2_bits, uint16_t* lv3_bits, faq_stream_t stream);
+
+/*
+ * Normalized Walsh-Hadamard transform (Sylvester order, fp32 butterflies, true division
+ * by fp32(sqrt(block))) applied independently to each `block`-wide slice of each row;
+ * rows of `cols` values, cols % block == 0 and cols % 8 == 0, block a power of two in
+ * [2, 512].  Input dtype in_dtype is converted to fp32, the result is rounded once to
+ * out_dtype (the reference's chunked transform and rotate_heads).
+ */
+int faq_hadamard_rows(const void* x, void* y, int64_t rows, int64_t cols, int block, int in_dtype,
+                      int out_dtype, faq_stream_t stream);
+
+/*
+ * Attention operand prologue for Q or K, head_dim 128: x [B, H, L, 128] with element
+ * strides (sb, sh, sl).  In fp32: subtract key_offset[h * off_sh + d] (if non-NULL),
+ * multiply (smooth_divide = 0) or divide (= 1) by smooth[h * smooth_sh + d] (if
+ * non-NULL), apply the block Hadamard of size `hadamard` (0 = none, 64 or 128), round
+ * once to round_dtype; optionally store that rotated tensor to `rotated` (round_dtype,
+ * contiguous [B, H, L, 128]); then HiF4 QDQ with `levels` (0 = no quantization) and
+ * store bf16 to y with element strides (yb, yh, yl).
+ */
+int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
+                     const float* key_offset, int64_t off_sh, const float* smooth, int64_t smooth_sh,
+                     int smooth_divide, int hadamard, int round_dtype, void* rotated, void* y, int64_t yb,
+                     int64_t yh, int64_t yl, int levels, faq_stream_t stream);
+
+/*
+ * V operand: x [B, H, L, 128] (strides sb, sh, sl), HiF4 QDQ with `levels` (0 = none),
+ * written transposed as bf16 vt [B, H, 128, Lpad] (contiguous), Lpad = multiple of 128
+ * >= L, keys >= L zero-filled.
+ */
+int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
+                        int Lpad, uint16_t* vt, int levels, faq_stream_t stream);
+
+/*
+ * HiF4 QK/PV flash attention forward, head_dim 128, key tiles of 128 in ascending
+ * order from key 0.
+ *   q   bf16 [B, Hq, Lq, 128]  strides (q_sb, q_sh, q_sl)   (quantized or not by caller)
+ *   k   bf16 [B, Hkv, Lk, 128] strides (k_sb, k_sh, k_sl)
+ *   vt  bf16 [B, Hkv, 128, Lpad] strides (v_sb, v_sh, v_sd) from faq_operand_prep_vt
+ *   o   [B, Hq, Lq, 128] via strides (o_sb, o_sh, o_sl), o_dtype FAQ_F32 or FAQ_BF16
+ *   Hq % Hkv == 0 (query head h reads KV head h / (Hq / Hkv)).
+ *   causal      1: bottom-right causal mask (row p sees keys <= p + Lk - Lq)
+ *   scale       softmax scale (e.g. 128^-0.5)
+ *   quant_p     1: HiF4-quantize P along keys in 64-groups with p_levels
+ *   norm_same   1: denominator sums the quantized P (P-Reordering, "quantized_same")
+ *   row_den     optional fp32 [B, Hq, Lq]: the final softmax denominator of each row
+ */
+int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
+                      int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
+                      int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                      int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels,
+                      int norm_same, float* row_den, faq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAQUANT_AMD_H */

@@ -35,3 +35,22 @@ def golden_hadamard():
 @pytest.fixture(scope="session")
 def golden_attention():
     return load_golden("attention.npz")
+
+
+def gpu_available() -> bool:
+    try:
+        import torch
+
+        return torch.cuda.is_available()
+    except Exception:  # pragma: no cover
+        return False
+
+
+@pytest.fixture(scope="session")
+def dev():
+    """The MI355X device; GPU tests skip cleanly where there is none."""
+    if not gpu_available():
+        pytest.skip("needs a ROCm GPU")
+    import torch
+
+    return torch.device("cuda:0")

@@ -1,0 +1,167 @@
+"""The C ABI boundary and the host-side mirror, without a GPU.
+
+* libfaquant_amd.so loads and exports every entry point include/faquant_amd.h declares;
+* argument validation returns the documented status before any device work;
+* the drop-in Python functions raise the reference's exception types and
+  messages for invalid arguments, and refuse CPU tensors (no CPU fallback).
+"""
+
+import ctypes
+import os
+import re
+from types import SimpleNamespace
+
+import pytest
+
+from tests.conftest import REPO
+
+torch = pytest.importorskip("torch")
+
+HEADER = os.path.join(REPO, "include", "faquant_amd.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(faq_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from faquant_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("HIP library not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_lists_the_entry_points():
+    names = declared()
+    assert names == sorted(
+        ["faq_last_error", "faq_version", "faq_hif4_qdq_rows", "faq_hadamard_rows", "faq_operand_prep",
+         "faq_operand_prep_vt", "faq_attention_fwd"]
+    )
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from faquant_amd import _lib
+
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert set(declared()) == set(_lib.EXPORTED)
+    assert lib.faq_version().decode().startswith("faquant_amd")
+
+
+def test_validation_statuses_without_device_work(lib):
+    from faquant_amd import _lib
+
+    assert lib.faq_hif4_qdq_rows(None, None, 1, 64, 0, 123, *([None] * 8), None) == _lib.EINVAL
+    assert "null" in lib.faq_last_error().decode()
+    buf = ctypes.create_string_buffer(1024)
+    p = ctypes.addressof(buf)
+    p16 = (p + 15) // 16 * 16
+    assert lib.faq_hif4_qdq_rows(p16, p16, 1, 64, 0, 7, *([None] * 8), None) == _lib.EINVAL
+    assert "123, 12 or 13" in lib.faq_last_error().decode()
+    assert lib.faq_hadamard_rows(p16, p16, 1, 24, 3, 0, 0, None) == _lib.EINVAL
+    assert "power of two" in lib.faq_last_error().decode()
+    assert lib.faq_operand_prep(p16, 1, 128, 128, 128, 1, 1, 1, None, 0, None, 0, 0, 96, 1, None, p16, 128, 128, 128,
+                                123, None) == _lib.EUNSUP
+    rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
+                               1, 3, 2, 1, 1, 1, 0.1, 1, 123, 1, None, None)
+    assert rc == _lib.EINVAL and "divisible" in lib.faq_last_error().decode()
+    rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 100, p16, 1, 0, 0, 0,
+                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, None)
+    assert rc == _lib.EINVAL and "Lpad" in lib.faq_last_error().decode()
+
+
+def test_status_maps_to_reference_exception_types(lib):
+    from faquant_amd import _lib
+
+    lib.faq_hadamard_rows(None, None, 1, 8, 8, 0, 0, None)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.EINVAL)
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.EUNSUP)
+
+
+def _module():
+    from faquant_amd.simulated_flash_attention import new_simulated_attention_stats
+
+    return SimpleNamespace(
+        is_causal=True, training=False, faquant_attention_query_chunk_size=256,
+        faquant_attention_key_chunk_size=128, faquant_qk_matmul_quant=True, faquant_pv_matmul_quant=True,
+        faquant_pv_normalizer_mode="quantized_same",
+        faquant_matmul_quant_kwargs={"quant_format": "hif4", "bits": 4, "group_size": 64, "symmetric": True,
+                                     "clip_ratio": 1.0},
+        faquant_simulated_attention_stats=new_simulated_attention_stats(),
+    )
+
+
+def test_drop_in_validation_messages_match_reference():
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward as f
+
+    q = torch.zeros(1, 2, 3, 128)
+    k = torch.zeros(1, 1, 3, 128)
+    with pytest.raises(ValueError, match="dropout=0"):
+        f(_module(), q, k, k, None, dropout=0.1)
+    with pytest.raises(ValueError, match="rank-4"):
+        f(_module(), q[0], k, k, None)
+    with pytest.raises(ValueError, match="matching K/V"):
+        f(_module(), q, k, torch.zeros(1, 1, 4, 128), None)
+    with pytest.raises(ValueError, match="divisible"):
+        f(_module(), torch.zeros(1, 3, 3, 128), torch.zeros(1, 2, 3, 128), torch.zeros(1, 2, 3, 128), None)
+    with pytest.raises(NotImplementedError, match="packed cu_seqlens"):
+        f(_module(), q, k, k, None, cu_seq_lens_q=torch.tensor([0, 3]))
+    with pytest.raises(ValueError, match="sliding_window must be positive"):
+        f(_module(), q, k, k, None, sliding_window=0)
+    mod = _module()
+    mod.faquant_pv_normalizer_mode = "quantized"
+    with pytest.raises(ValueError, match="pv_normalizer_mode"):
+        f(mod, q, k, k, None)
+
+
+def test_cpu_tensors_are_refused_not_computed(lib):
+    from faquant_amd.hif4 import fake_quantize_hif4
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward as f
+
+    with pytest.raises(ValueError, match="ROCm device"):
+        fake_quantize_hif4(torch.zeros(4, 64))
+    with pytest.raises(ValueError, match="ROCm device"):
+        f(_module(), torch.zeros(1, 2, 3, 128), torch.zeros(1, 1, 3, 128), torch.zeros(1, 1, 3, 128), None)
+
+
+def test_quantizer_argument_errors():
+    from faquant_amd.hif4 import fake_quantize_hif4, fit_hif4_compact_parameters
+    from faquant_amd.quantization import fake_quantize
+
+    with pytest.raises(TypeError, match="floating-point"):
+        fake_quantize_hif4(torch.zeros(4, 64, dtype=torch.int32))
+    with pytest.raises(ValueError, match="at least one dimension"):
+        fit_hif4_compact_parameters(torch.tensor(1.0))
+    with pytest.raises(ValueError, match="final dimension of 64"):
+        fit_hif4_compact_parameters(torch.zeros(2, 32))
+    with pytest.raises(ValueError, match="bits=4"):
+        fake_quantize(torch.zeros(2, 64), quant_format="hif4", bits=8)
+    with pytest.raises(ValueError, match="group_size=64"):
+        fake_quantize(torch.zeros(2, 64), quant_format="hif4", group_size=32)
+    with pytest.raises(NotImplementedError):
+        fake_quantize(torch.zeros(2, 64), quant_format="int", bits=4, group_size=4)
+
+
+def test_stats_closed_form_matches_oracle_counters():
+    """count_tiles replays the simulator schedule: compare with the oracle's counters."""
+    import numpy as np
+
+    from faquant_amd.simulated_flash_attention import count_tiles, new_simulated_attention_stats
+    from oracle import attention as OA
+
+    for (B, Hq, Hkv, Lq, Lk, qc, causal) in ((1, 4, 2, 300, 300, 256, True), (2, 2, 1, 130, 400, 64, True),
+                                              (1, 2, 2, 200, 200, 256, False), (1, 2, 1, 9, 3, 4, True)):
+        q = np.zeros((B, Hq, Lq, 128), np.float32)
+        k = np.zeros((B, Hkv, Lk, 128), np.float32)
+        so = OA.new_stats()
+        OA.simulated_flash_attention(q, k, k, OA.SimConfig(query_chunk=qc), is_causal=causal, stats=so)
+        sg = new_simulated_attention_stats()
+        count_tiles(sg, batch=B, query_heads=Hq, query_length=Lq, key_length=Lk, head_dim=128, query_chunk=qc,
+                    key_chunk=128, causal=causal, skip_fully_masked=True, qk_quant=True, pv_quant=True,
+                    qk_group=64, pv_group=64)
+        assert sg == so
