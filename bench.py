@@ -133,6 +133,8 @@ def main():
     ap.add_argument("--config", default="qwen8b_32k", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 256 MiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus})",
@@ -142,6 +144,16 @@ def main():
     import torch
 
     from faquant_amd import _ops
+
+    if args.calibrate_copy:
+        src = torch.empty(64 << 20, device="cuda:0", dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4,
+                          "launches": 3}), flush=True)
+        return
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")

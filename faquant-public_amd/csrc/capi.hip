@@ -229,6 +229,10 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   if (o_dtype == FAQ_BF16 ? ((o_sb | o_sh | o_sl) & 3) : ((o_sb | o_sh | o_sl) & 3))
     return fail(FAQ_EINVAL, "faq_attention_fwd: output strides must be multiples of 4 elements");
   if (v_sd < Lpad) return fail(FAQ_EINVAL, "faq_attention_fwd: v_sd must be >= Lpad");
+  // the kernel addresses one head's K and V^T with 32-bit byte offsets
+  if (k_sl > (int64_t(1) << 22) || v_sd > (int64_t(1) << 22) ||
+      (static_cast<int64_t>(Lk) * k_sl + 128) * 2 >= (int64_t(1) << 32) || 128 * v_sd * 2 >= (int64_t(1) << 32))
+    return fail(FAQ_EUNSUP, "faq_attention_fwd: one head's K or V^T spans more than 4 GiB of addresses");
   if (B == 0 || Lq == 0) return FAQ_OK;
   const int G = Hq / Hkv;
   const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;

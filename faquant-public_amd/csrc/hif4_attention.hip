@@ -14,7 +14,14 @@
 //
 // Work decomposition: a 256-thread workgroup owns 128 query rows that share one KV
 // head (GQA: up to 4 query heads x 32 positions), so each K/V tile staged in LDS is
-// reused by every row of the group.  Each wave owns 32 rows.
+// reused by every row of the group.  Each wave owns 32 rows; two workgroups share a
+// CU (two waves per SIMD), so one workgroup's softmax overlaps the other's MFMAs.
+//
+// Tile pipeline (per workgroup, LDS holds one K tile and one V tile, 64 KiB):
+//   QK(t) reads K(t) | barrier | DMA K(t+1) | softmax(t) | PV(t) reads V(t) | barrier |
+//   DMA V(t+1) | ...
+// The K/V tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging), so
+// K(t+1) lands during softmax+PV(t) and V(t+1) during QK(t+1)+softmax(t+1).
 //
 // MFMA layout (v_mfma_f32_32x32x16_bf16; lane l, m = l % 32, half = l / 32):
 //   QK computes S^T = K Q^T.  The B operand is the wave's Q fragment (lane holds
@@ -25,10 +32,26 @@
 //   group of its row, in key order, so all group maxima are lane-local.
 //   PV computes O^T = V^T P^T.  For k-chunk c the B operand slots 8 half + t are keys
 //   64 half + 8 c + t, i.e. this lane's own P values (8c .. 8c+7), and the A operand is
-//   the matching 16-byte run of the transposed V tile.  The row sum of P^ (P-Reordering)
-//   is one more MFMA against an all-ones A operand.
-// LDS tiles are 128 rows x 256 bytes with the 16-byte pieces XOR-swizzled per row so
-// that the MFMA operand reads of 16 consecutive lanes hit distinct banks.
+//   the matching 16-byte run of the transposed V tile.
+// LDS tiles are 128 rows x 256 bytes; the 16-byte piece p of row r is stored at
+// position p ^ swz(r), so the operand reads of 16 consecutive lanes hit 16 distinct
+// bank groups.
+//
+// P quantization in registers (levels 123 shown; 12 and 13 differ only in the micro
+// exponent rule).  Per lane and tile: the group maximum m1 is exp2 of the lane's largest
+// scaled score (the same fma and exp2 as that element), giving the E6M2 scale s and
+// rec = bf16(1/s).  Per 4-key group with maximum m3, the micro exponent k in {0,1,2}
+// (hif4.py:200-213) is read off K = 2^k = med3(floor2(m3 rec), 2^e2, 4), where
+// floor2(x) = 2^floor(log2 x) is a mask of the exponent bits (the comparisons
+// m3 rec >= 2, >= 4 of the reference are exactly floor2 comparisons).  The code is then
+// one fused multiply-add against the magic constant M_K = 2^(23+k):
+//   z = fma(p, 4 rec, M_K)  ->  z = M_K + K * rint(p * 4 rec / K)
+// (M_K has unit-in-last-place K), clamped at M_K + 7K (the bit pattern of M_K plus 7),
+// and dequantized exactly by y = fma(z, s/4, -M_K s/4) = K * code * s/4 = code * ds / 4.
+// This equals the reference's floor(fp32(p * qm) * 4 + 0.5) except on the measure-zero
+// sets where p * qm * 4 rounds onto, or is exactly, a half-integer (ties round to even
+// here); P itself already differs from torch.exp by a few ulp, so P^ is compared within
+// the attention tolerance, while the standalone quantizers stay bit-exact.
 #include "hif4_device.h"
 
 namespace faq {
@@ -54,15 +77,49 @@ struct AttnArgs {
   float* row_den;  // optional fp32 [B, Hq, Lq]: final denominator l
 };
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Stored position of piece p of K-tile row r is p ^ k_swz(r); of V^T-tile row r, p ^ (r & 15).
 __device__ __forceinline__ int k_swz(int r) { return (r & 15) ^ (((r >> 6) & 1) << 3); }
-__device__ __forceinline__ int v_swz(int d) { return d & 15; }
 
 __device__ __forceinline__ floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ bf16x8 lds_read16(const uint16_t* base, int row, int piece) {
-  return *reinterpret_cast<const bf16x8*>(base + row * kDim + piece * 8);
+__device__ __forceinline__ bf16x8 lds_read16(const uint16_t* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// One 16-byte-per-lane DMA from global memory into LDS: lane l reads 16 bytes at byte
+// offset soff + voff of the buffer `rs` and writes them to bytes [16 l, 16 l + 16) of the
+// 1 KiB LDS block at `dst` (wave-uniform).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff, uint16_t* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst), 16, voff, soff, 0, 0);
+}
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// Wait until every memory operation this wave issued has completed (LDS DMA included):
+// the workgroup barrier alone does not order another wave's DMA writes into LDS.
+__device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// v_permlane32_swap of a register with itself yields {x of lane l % 32, x of lane
+// 32 + l % 32} in every lane l, so these give the same value in lanes l and l ^ 32.
+__device__ __forceinline__ float halves_max(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float halves_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Pack 8 fp32 values as bf16; `exact` values are bf16-representable (truncation is exact).
@@ -83,11 +140,68 @@ __device__ __forceinline__ bf16x8 pack8(const float* v) {
   return r;
 }
 
+__device__ __forceinline__ float floor2(float x) { return __uint_as_float(__float_as_uint(x) & 0xFF800000u); }
+
+// Per-lane constants of the HiF4 QDQ of one 64-key P group (p >= 0) with maximum m1.
+struct PQuant {
+  float rec4;   // 4 rec
+  float rec23;  // rec 2^23: floor2(m3 rec23) = 2^(23 + floor(log2 (m3 rec)))
+  float s4;     // s / 4
+  float ns4;    // -s / 4
+};
+
+template <int LV>
+__device__ __forceinline__ PQuant pquant_setup(float m1) {
+  float sc, rec;
+  hif4_scale<LV>(m1, sc, rec);
+  PQuant q;
+  q.rec4 = rec * 4.0f;
+  q.rec23 = rec * 8388608.0f;
+  q.s4 = sc * 0.25f;
+  q.ns4 = -q.s4;
+  return q;
+}
+
+// HiF4 QDQ in place of one 8-key group g[0..7] (two 4-key groups) of a lane's P group.
+template <int LV>
+__device__ __forceinline__ void pquant8(float* g, const PQuant& q) {
+  const float m3a = fmaxf(fmaxf(g[0], g[1]), fmaxf(g[2], g[3]));
+  const float m3b = fmaxf(fmaxf(g[4], g[5]), fmaxf(g[6], g[7]));
+  const float xa = floor2(m3a * q.rec23);
+  const float xb = floor2(m3b * q.rec23);
+  float mka, mkb;
+  if (LV == 123) {
+    // e2 = [max(t3a, t3b) >= 4]; K = med3(floor2(t3), 2^e2, 4), all scaled by 2^23
+    const float e2 = fmaxf(xa, xb) >= 33554432.0f ? 16777216.0f : 8388608.0f;
+    mka = __builtin_amdgcn_fmed3f(xa, e2, 33554432.0f);
+    mkb = __builtin_amdgcn_fmed3f(xb, e2, 33554432.0f);
+  } else if (LV == 12) {
+    // e2 = [max(t3a, t3b) >= 2], e3 = 0
+    mka = fmaxf(xa, xb) >= 16777216.0f ? 16777216.0f : 8388608.0f;
+    mkb = mka;
+  } else {
+    // e2 = 0, e3 = [t3 >= 2]
+    mka = __builtin_amdgcn_fmed3f(xa, 8388608.0f, 16777216.0f);
+    mkb = __builtin_amdgcn_fmed3f(xb, 8388608.0f, 16777216.0f);
+  }
+  const float cka = __uint_as_float(__float_as_uint(mka) + 7u);
+  const float ckb = __uint_as_float(__float_as_uint(mkb) + 7u);
+  const float nka = mka * q.ns4;
+  const float nkb = mkb * q.ns4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float za = fminf(__builtin_fmaf(g[j], q.rec4, mka), cka);
+    g[j] = __builtin_fmaf(za, q.s4, nka);
+    const float zb = fminf(__builtin_fmaf(g[4 + j], q.rec4, mkb), ckb);
+    g[4 + j] = __builtin_fmaf(zb, q.s4, nkb);
+  }
+}
+
 template <int LV, bool kQuantP, bool kSame>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[kKeyTile * kDim];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[kDim * kKeyTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks[kKeyTile * kDim];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs[kDim * kKeyTile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -131,62 +245,98 @@ void attn_fwd_kernel(AttnArgs a) {
   floatx16 acc[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) acc[mb] = floatx16{};
-  floatx16 accl = floatx16{};
   float m_run = -INFINITY;
   float l_run = 0.0f;
-  bf16x8 ones;
+  bf16x2_t ones2;
   {
     const uint32_t one2 = 0x3F803F80u;
-    uint32_t w4[4] = {one2, one2, one2, one2};
-    __builtin_memcpy(&ones, w4, 16);
+    __builtin_memcpy(&ones2, &one2, 4);
   }
 
   const uint16_t* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
   const uint16_t* vbase = a.vt + b * a.v_sb + kvh * a.v_sh;
-  // Tile loads: thread (row r = tid/16 + 16 i, piece tid%16) moves one 16-byte piece of
-  // the K tile (key rows) and of the transposed V tile (dim rows) into LDS.  Offsets
-  // inside a tile are 32-bit; the tile base is wave-uniform.
-  const int ld_row = tid >> 4;
-  const int ld_piece = tid & 15;
-  const int k_off0 = ld_row * static_cast<int>(a.k_sl) + ld_piece * 8;
-  const int v_off0 = ld_row * static_cast<int>(a.v_sd) + ld_piece * 8;
-  const int k_step = 16 * static_cast<int>(a.k_sl);
-  const int v_step = 16 * static_cast<int>(a.v_sd);
-  const int st_k_lo = ld_row * kDim + ((ld_piece ^ ld_row) * 8);       // rows r < 64: piece ^ (r & 15)
-  const int st_k_hi = ld_row * kDim + ((ld_piece ^ ld_row ^ 8) * 8);   // rows r >= 64: piece ^ (r & 15) ^ 8
+
+  // DMA assignment: wave w, instruction j fills LDS rows 32 w + 4 j + lane / 16 (1 KiB per
+  // instruction); lane writes stored position lane % 16 of its row, i.e. logical piece
+  // (lane % 16) ^ swz(row).  The swizzle of rows 32 w + 4 j + lane / 16 depends on j % 4
+  // only, so instructions j and j + 4 share a lane offset and differ by 16 rows.
+  const int ws = __builtin_amdgcn_readfirstlane(w);
+  uint32_t kvo[4], vvo[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 32 * ws + 4 * j + (lane >> 4);
+    kvo[j] = static_cast<uint32_t>(r * static_cast<int>(a.k_sl) + 8 * ((lane & 15) ^ k_swz(r))) * 2u;
+    vvo[j] = static_cast<uint32_t>(r * static_cast<int>(a.v_sd) + 8 * ((lane & 15) ^ (r & 15))) * 2u;
+  }
+  const uint32_t k16 = static_cast<uint32_t>(16 * a.k_sl) * 2u;
+  const uint32_t v16 = static_cast<uint32_t>(16 * a.v_sd) * 2u;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, a.Lk > 0 ? static_cast<uint32_t>(((a.Lk - 1) * a.k_sl + kDim) * 2) : 0u);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, static_cast<uint32_t>((127 * a.v_sd + a.v_sd) * 2));
+  uint16_t* const ks_w = ks + ws * (8 * 512);
+  uint16_t* const vs_w = vs + ws * (8 * 512);
+
+  auto load_k = [&](int t) {
+    const int key0 = t * kKeyTile;
+    const uint32_t soff = static_cast<uint32_t>(key0 * a.k_sl) * 2u;
+    if (key0 + kKeyTile <= a.Lk) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dma16(krs, kvo[j & 3], soff + (j >> 2) * k16, ks_w + j * 512);
+    } else {
+      // ragged last tile: rows past the last key re-read the last key (their scores are
+      // masked to -inf before use)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = 32 * ws + 4 * j + (lane >> 4);
+        const int rr = min(r, a.Lk - 1 - key0);
+        const uint32_t vo = static_cast<uint32_t>(rr * static_cast<int>(a.k_sl) + 8 * ((lane & 15) ^ k_swz(r))) * 2u;
+        dma16(krs, vo, soff, ks_w + j * 512);
+      }
+    }
+  };
+  auto load_v = [&](int t) {
+    const uint32_t soff = static_cast<uint32_t>(t * kKeyTile) * 2u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma16(vrs, vvo[j & 3], soff + (j >> 2) * v16, vs_w + j * 512);
+  };
+
+  // LDS operand addresses (element offsets).  QK: key row pi(0, n) + 16 kb, piece 2c + half.
+  const int krow0 = 64 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+  const int ksw = k_swz(krow0);
+  int kaddr[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) kaddr[c] = krow0 * kDim + (((2 * c + half) ^ ksw) * 8);
+  // PV: V^T row 32 mb + n, piece 8 half + c.
+  int vaddr[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) vaddr[c] = n * kDim + (((8 * half + c) ^ (n & 15)) * 8);
+
+  if (ntiles > 0) {
+    load_k(0);
+    load_v(0);
+  }
+  wait_all_memory();
+  __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
     const int key0 = t * kKeyTile;
-    const uint16_t* ktile = kbase + static_cast<int64_t>(key0) * a.k_sl;
-    const uint16_t* vtile = vbase + key0;
-    const int krows = a.Lk - key0;  // valid key rows in this tile (> 0)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = ld_row + 16 * i;
-      // rows past the last key read the last valid row and are replaced by zeros
-      const int koff = r < krows ? k_off0 + i * k_step : (krows - 1) * static_cast<int>(a.k_sl) + ld_piece * 8;
-      uint4 kv = *reinterpret_cast<const uint4*>(ktile + koff);
-      if (r >= krows) kv = make_uint4(0, 0, 0, 0);
-      const uint4 vv = *reinterpret_cast<const uint4*>(vtile + v_off0 + i * v_step);
-      // K rows >= 64 (i >= 4) flip bit 3 of the piece swizzle (k_swz); V uses d & 15 (v_swz)
-      *reinterpret_cast<uint4*>(ks + (i < 4 ? st_k_lo : st_k_hi) + 16 * i * kDim) = kv;
-      *reinterpret_cast<uint4*>(vs + st_k_lo + 16 * i * kDim) = vv;
-    }
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-
-    if (key0 < kend_w) {
+    const bool active = key0 < kend_w;
+    floatx16 s[4];
+    if (active) {
       // ---- S^T = K Q^T
-      floatx16 s[4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         s[kb] = floatx16{};
-        const int krow = 64 * ((n >> 2) & 1) + 16 * kb + 4 * (n >> 3) + (n & 3);
-        const int sw = k_swz(krow);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) s[kb] = mfma32(lds_read16(ks, krow, (2 * c + half) ^ sw), qf[c], s[kb]);
+        for (int c = 0; c < 8; ++c) s[kb] = mfma32(lds_read16(ks + kaddr[c] + kb * 16 * kDim), qf[c], s[kb]);
       }
-      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // K(t) consumed by every wave; V(t) has landed
+    wait_all_memory();
+    __syncthreads();
+    if (t + 1 < ntiles) load_k(t + 1);
+
+    if (active) {
       // ---- masks (ragged key tail, causal diagonal)
       const bool need_mask = (key0 + kKeyTile > a.Lk) || (a.causal && key0 + kKeyTile - 1 > p0w + off);
       if (need_mask) {
@@ -203,87 +353,84 @@ void attn_fwd_kernel(AttnArgs a) {
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx * a.c1);
+      const float mx_row = halves_max(mx);
+      const float m_new = fmaxf(m_run, mx_row * a.c1);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float nm = -m_use;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       m_run = m_new;
-      float p[64];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) p[16 * kb + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], a.c1, -m_use));
-
       if (__ballot(alpha != 1.0f) != 0) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
-        accl[0] *= alpha;
         l_run *= alpha;
       }
-
-      float rowsum = 0.0f;
-      if (!(kQuantP && kSame)) {
-        // the normalizer sums P (unquantized mode, or no P quantization)
-#pragma unroll
-        for (int i = 0; i < 64; ++i) rowsum += p[i];
-      }
-
+      // ---- P, its HiF4 QDQ and the row sum, one 8-key chunk at a time; chunk c of this lane
+      // is keys 64 half + 8c .. 8c+7, the B operand of PV k-chunk c.
+      PQuant pq;
       if (kQuantP) {
-        float m3[16];
-#pragma unroll
-        for (int g = 0; g < 16; ++g) m3[g] = fmaxf(fmaxf(p[4 * g], p[4 * g + 1]), fmaxf(p[4 * g + 2], p[4 * g + 3]));
-        float m1 = m3[0];
-#pragma unroll
-        for (int g = 1; g < 16; ++g) m1 = fmaxf(m1, m3[g]);
-        float sc, rec;
-        hif4_scale<LV>(m1, sc, rec);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          int ka, kb2;
-          hif4_micro<LV>(m3[2 * c], m3[2 * c + 1], rec, ka, kb2);
-          float qa, da, qb, db;
-          hif4_group_mults(sc, rec, ka, qa, da);
-          hif4_group_mults(sc, rec, kb2, qb, db);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) p[8 * c + j] = hif4_element(p[8 * c + j], j < 4 ? qa : qb, j < 4 ? da : db);
-        }
+        // group maximum = P of the lane's largest score (same fma and exp2)
+        pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
       }
-
-      // ---- O^T += V^T P^T (and the P^ row sum)
+      float rowsum = 0.0f;
+      bf16x8 pbv[8];
+      bf16x8 plo[kQuantP ? 1 : 8];
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const bf16x8 pb = pack8<kQuantP>(&p[8 * c]);
-        // Unquantized P is not exact in bf16: it goes in as hi + lo bf16 parts
-        // (16 significant bits) so PV keeps the fp32-operand accuracy of the reference.
-        bf16x8 plo;
-        if (!kQuantP) {
+        float pc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
+        if (!(kQuantP && kSame)) {
+          // the normalizer sums P (unquantized mode, or no P quantization)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) rowsum += pc[j];
+        }
+        if (kQuantP) {
+          pquant8<LV>(pc, pq);
+          pbv[c] = pack8<true>(pc);
+          if (kSame) {
+            uint32_t wv[4];
+            __builtin_memcpy(wv, &pbv[c], 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              bf16x2_t pr;
+              __builtin_memcpy(&pr, &wv[i], 4);
+              rowsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, rowsum, false);
+            }
+          }
+        } else {
+          // Unquantized P is not exact in bf16: it goes in as hi + lo bf16 parts
+          // (16 significant bits) so PV keeps the fp32-operand accuracy of the reference.
           float r[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) r[j] = p[8 * c + j] - bf16_rne(p[8 * c + j]);
-          plo = pack8<false>(r);
+          for (int j = 0; j < 8; ++j) r[j] = pc[j] - bf16_rne(pc[j]);
+          pbv[c] = pack8<false>(pc);
+          plo[kQuantP ? 0 : c] = pack8<false>(r);
         }
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const int d = 32 * mb + n;
-          const bf16x8 va = lds_read16(vs, d, (8 * half + c) ^ v_swz(d));
-          acc[mb] = mfma32(va, pb, acc[mb]);
-          if (!kQuantP) acc[mb] = mfma32(va, plo, acc[mb]);
-        }
-        if (kQuantP && kSame) accl = mfma32(ones, pb, accl);
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (!(kQuantP && kSame)) {
-        rowsum += __shfl_xor(rowsum, 32, 64);
-        l_run += rowsum;
+
+      // ---- O^T += V^T P^T
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const bf16x8 va = lds_read16(vs + vaddr[c] + mb * 32 * kDim);
+          acc[mb] = mfma32(va, pbv[c], acc[mb]);
+          if (!kQuantP) acc[mb] = mfma32(va, plo[kQuantP ? 0 : c], acc[mb]);
+        }
       }
+      l_run += halves_sum(rowsum);
     }
+    // V(t) consumed by every wave; K(t+1) has landed
+    wait_all_memory();
     __syncthreads();
+    if (t + 1 < ntiles) load_v(t + 1);
   }
 
   if (!row_live) return;
-  const float l = (kQuantP && kSame) ? accl[0] : l_run;
+  const float l = l_run;
   const float inv_guard = fmaxf(l, 1.17549435e-38f);
   if (a.row_den && half == 0) a.row_den[(static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos] = l;
   char* obase = static_cast<char*>(a.o);
