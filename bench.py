@@ -30,6 +30,13 @@ for _p in (REPO, os.path.join(REPO, "faquant-public_amd")):
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBPS = 8000.0
 
+# HBM bytes per attention launch, measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and
+# scaled by the same counters on a 256 MiB device copy (bench.py --calibrate-copy):
+# profiles/attn_fwd_<config>_counters.md.  None where no counter run was made.
+MEASURED_TRAFFIC_BYTES = {
+    "qwen8b_32k": 2.648e9,
+}
+
 CONFIGS = {
     # name: B, Hq, Hkv, L, causal, hadamard block, levels, key distribution, per-head scale
     "qwen8b_32k": dict(B=1, Hq=32, Hkv=8, L=32768, causal=True, hadamard=64, levels="123", keys="normal",
@@ -228,7 +235,7 @@ def main():
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC_BYTES.get(args.config),
         },
     }
     if not args.no_cpu_baseline:

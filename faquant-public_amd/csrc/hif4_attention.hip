@@ -142,6 +142,11 @@ __device__ __forceinline__ bf16x8 pack8(const float* v) {
 
 __device__ __forceinline__ float floor2(float x) { return __uint_as_float(__float_as_uint(x) & 0xFF800000u); }
 
+// max of two non-negative floats as an integer max of their bit patterns
+__device__ __forceinline__ float fmax_nonneg(float a, float b) {
+  return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+
 // Per-lane constants of the HiF4 QDQ of one 64-key P group (p >= 0) with maximum m1.
 struct PQuant {
   float rec4;   // 4 rec
@@ -150,10 +155,25 @@ struct PQuant {
   float ns4;    // -s / 4
 };
 
+// fp32 -> bf16 (round to nearest even, the hardware conversion) -> fp32.
+__device__ __forceinline__ float bf16_round_hw(float x) {
+  const __bf16 h = static_cast<__bf16>(x);
+  uint16_t u;
+  __builtin_memcpy(&u, &h, 2);
+  return __uint_as_float(static_cast<uint32_t>(u) << 16);
+}
+
+// Same values as hif4_scale (hif4.py:91-115) for m1 >= 0: s0 = bf16(m1 bf16(1/div)),
+// clamped to [2^-48, 49152] (integer clamp of the non-negative bit pattern), E6M2
+// round-half-even on the bits, and rec = bf16(1/s): 1/s = 2^-e / (1 + m/4) lies far from
+// every bf16 rounding boundary, so the 1-ulp hardware reciprocal rounds to the same bf16.
 template <int LV>
 __device__ __forceinline__ PQuant pquant_setup(float m1) {
-  float sc, rec;
-  hif4_scale<LV>(m1, sc, rec);
+  const float s0 = bf16_round_hw(m1 * divisor_reciprocal<LV>());
+  uint32_t b = min(max(__float_as_uint(s0), 0x27800000u), 0x47400000u);
+  b = (b + 0x000FFFFFu + ((b >> 21) & 1u)) & 0xFFE00000u;
+  const float sc = __uint_as_float(b);
+  const float rec = bf16_round_hw(__builtin_amdgcn_rcpf(sc));
   PQuant q;
   q.rec4 = rec * 4.0f;
   q.rec23 = rec * 8388608.0f;
@@ -172,12 +192,12 @@ __device__ __forceinline__ void pquant8(float* g, const PQuant& q) {
   float mka, mkb;
   if (LV == 123) {
     // e2 = [max(t3a, t3b) >= 4]; K = med3(floor2(t3), 2^e2, 4), all scaled by 2^23
-    const float e2 = fmaxf(xa, xb) >= 33554432.0f ? 16777216.0f : 8388608.0f;
+    const float e2 = fmax_nonneg(xa, xb) >= 33554432.0f ? 16777216.0f : 8388608.0f;
     mka = __builtin_amdgcn_fmed3f(xa, e2, 33554432.0f);
     mkb = __builtin_amdgcn_fmed3f(xb, e2, 33554432.0f);
   } else if (LV == 12) {
     // e2 = [max(t3a, t3b) >= 2], e3 = 0
-    mka = fmaxf(xa, xb) >= 16777216.0f ? 16777216.0f : 8388608.0f;
+    mka = fmax_nonneg(xa, xb) >= 16777216.0f ? 16777216.0f : 8388608.0f;
     mkb = mka;
   } else {
     // e2 = 0, e3 = [t3 >= 2]
@@ -323,12 +343,29 @@ void attn_fwd_kernel(AttnArgs a) {
     floatx16 s[4];
     if (active) {
       // ---- S^T = K Q^T
+      // c-major: four independent accumulation chains; the K fragments of step c + 1 are
+      // read while the MFMAs of step c run
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        s[kb] = floatx16{};
+      for (int kb = 0; kb < 4; ++kb) s[kb] = floatx16{};
+      bf16x8 kf[2][4];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) s[kb] = mfma32(lds_read16(ks + kaddr[c] + kb * 16 * kDim), qf[c], s[kb]);
+      for (int kb = 0; kb < 4; ++kb) kf[0][kb] = lds_read16(ks + kaddr[0] + kb * 16 * kDim);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        if (c + 1 < 8) {
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) kf[(c + 1) & 1][kb] = lds_read16(ks + kaddr[c + 1] + kb * 16 * kDim);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) s[kb] = mfma32(kf[c & 1][kb], qf[c], s[kb]);
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+      for (int c = 0; c < 7; ++c) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
     // K(t) consumed by every wave; V(t) has landed
@@ -374,10 +411,12 @@ void attn_fwd_kernel(AttnArgs a) {
         pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
       }
       float rowsum = 0.0f;
-      bf16x8 pbv[8];
-      bf16x8 plo[kQuantP ? 1 : 8];
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
+        // V^T fragments of this chunk first: their LDS latency hides under the chunk's VALU work
+        bf16x8 va[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) va[mb] = lds_read16(vs + vaddr[c] + mb * 32 * kDim);
         float pc[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
@@ -386,12 +425,13 @@ void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) rowsum += pc[j];
         }
+        bf16x8 pbc, plo;
         if (kQuantP) {
           pquant8<LV>(pc, pq);
-          pbv[c] = pack8<true>(pc);
+          pbc = pack8<true>(pc);
           if (kSame) {
             uint32_t wv[4];
-            __builtin_memcpy(wv, &pbv[c], 16);
+            __builtin_memcpy(wv, &pbc, 16);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               bf16x2_t pr;
@@ -405,21 +445,20 @@ void attn_fwd_kernel(AttnArgs a) {
           float r[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) r[j] = pc[j] - bf16_rne(pc[j]);
-          pbv[c] = pack8<false>(pc);
-          plo[kQuantP ? 0 : c] = pack8<false>(r);
+          pbc = pack8<false>(pc);
+          plo = pack8<false>(r);
         }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-
-      // ---- O^T += V^T P^T
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
+        // ---- O^T += V^T P^T for this chunk; the MFMAs run while the next chunk's VALU issues
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-          const bf16x8 va = lds_read16(vs + vaddr[c] + mb * 32 * kDim);
-          acc[mb] = mfma32(va, pbv[c], acc[mb]);
-          if (!kQuantP) acc[mb] = mfma32(va, plo[kQuantP ? 0 : c], acc[mb]);
+          acc[mb] = mfma32(va[mb], pbc, acc[mb]);
+          if (!kQuantP) acc[mb] = mfma32(va[mb], plo, acc[mb]);
         }
+        // order inside the chunk: the 4 LDS reads, then the VALU work, then the MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kQuantP ? 4 : 8, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
       l_run += halves_sum(rowsum);
     }
