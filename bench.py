@@ -34,7 +34,7 @@ HBM_PEAK_GBPS = 8000.0
 # scaled by the same counters on a 256 MiB device copy (bench.py --calibrate-copy):
 # profiles/attn_fwd_<config>_counters.md.  None where no counter run was made.
 MEASURED_TRAFFIC_BYTES = {
-    "qwen8b_32k": 2.705e9,
+    "qwen8b_32k": 1.674e9,
 }
 
 CONFIGS = {

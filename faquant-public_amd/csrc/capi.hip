@@ -80,9 +80,9 @@ void launch_prep_vt(const faq::OperandPrepVtArgs& a, int levels, dim3 grid, hipS
 
 template <int LV>
 void launch_attn_lv(const faq::AttnArgs& a, int quant_p, int same, dim3 grid, hipStream_t st) {
-  if (quant_p && same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true>), grid, dim3(256), 0, st, a);
-  else if (quant_p) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, false, false>), grid, dim3(256), 0, st, a);
+  if (quant_p && same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true>), grid, dim3(512), 0, st, a);
+  else if (quant_p) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false>), grid, dim3(512), 0, st, a);
+  else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, false, false>), grid, dim3(512), 0, st, a);
 }
 
 }  // namespace
@@ -235,8 +235,9 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
     return fail(FAQ_EUNSUP, "faq_attention_fwd: one head's K or V^T spans more than 4 GiB of addresses");
   if (B == 0 || Lq == 0) return FAQ_OK;
   const int G = Hq / Hkv;
-  const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
-  const int pos_per_wg = 32 * (4 / hpw);
+  // eight waves of 32 query rows per workgroup; hpw query heads of one KV head share it
+  const int hpw = (G % 8 == 0) ? 8 : (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+  const int pos_per_wg = 32 * (8 / hpw);
   faq::AttnArgs a{};
   a.q = q;
   a.q_sb = q_sb;

@@ -72,7 +72,7 @@ struct AttnArgs {
   int B, Hq, Hkv, Lq, Lk;
   int causal;
   float c1;  // softmax scale * log2(e)
-  int hpw;        // query heads per workgroup: 1, 2 or 4
+  int hpw;        // query heads per workgroup: 1, 2, 4 or 8
   int n_pblocks;  // position blocks per head group
   float* row_den;  // optional fp32 [B, Hq, Lq]: final denominator l
 };
@@ -80,11 +80,6 @@ struct AttnArgs {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Stored position of piece p of K-tile row r is p ^ k_swz(r); of V^T-tile row r, p ^ (r & 15).
-// gfx950 services ds_read_b128 in four passes of 16 lanes, pass = (lane bit 5, parity of lane
-// bits 2..4); a pass is conflict-free when its lanes hit 16 distinct 16-byte bank groups.
-// With these swizzles every QK and PV operand read of the 32x32x16 layout is conflict-free.
-__device__ __forceinline__ int k_swz(int r) { return r & 15; }
 
 __device__ __forceinline__ floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -194,37 +189,59 @@ __device__ __forceinline__ void pquant8(float* g, const PQuant& q) {
   const float xb = floor2(m3b * q.rec23);
   float mka, mkb;
   if (LV == 123) {
-    // e2 = [max(t3a, t3b) >= 4]; K = med3(floor2(t3), 2^e2, 4), all scaled by 2^23
-    const float e2 = fmax_nonneg(xa, xb) >= 33554432.0f ? 16777216.0f : 8388608.0f;
+    // e2 = [max(t3a, t3b) >= 4]; K = med3(floor2(t3), 2^e2, 4), all scaled by 2^23.
+    // 2^e2 2^23 = med3(max(xa, xb) / 2, 2^23, 2^24); the halving is an exponent decrement
+    // (xa, xb are 0 or normal powers of two; 0 becomes -inf, which med3 clamps).
+    const float hm = __uint_as_float(max(__float_as_uint(xa), __float_as_uint(xb)) - 0x00800000u);
+    const float e2 = __builtin_amdgcn_fmed3f(hm, 8388608.0f, 16777216.0f);
     mka = __builtin_amdgcn_fmed3f(xa, e2, 33554432.0f);
     mkb = __builtin_amdgcn_fmed3f(xb, e2, 33554432.0f);
   } else if (LV == 12) {
-    // e2 = [max(t3a, t3b) >= 2], e3 = 0
-    mka = fmax_nonneg(xa, xb) >= 16777216.0f ? 16777216.0f : 8388608.0f;
+    // e2 = [max(t3a, t3b) >= 2], e3 = 0: 2^e2 2^23 = med3(max(xa, xb), 2^23, 2^24)
+    mka = __builtin_amdgcn_fmed3f(fmax_nonneg(xa, xb), 8388608.0f, 16777216.0f);
     mkb = mka;
   } else {
     // e2 = 0, e3 = [t3 >= 2]
     mka = __builtin_amdgcn_fmed3f(xa, 8388608.0f, 16777216.0f);
     mkb = __builtin_amdgcn_fmed3f(xb, 8388608.0f, 16777216.0f);
   }
-  const float cka = __uint_as_float(__float_as_uint(mka) + 7u);
-  const float ckb = __uint_as_float(__float_as_uint(mkb) + 7u);
+  // code clamp at 7: z = M_K + code ulp, compared as integers (z > 0)
+  const uint32_t cka = __float_as_uint(mka) + 7u;
+  const uint32_t ckb = __float_as_uint(mkb) + 7u;
   const float nka = mka * q.ns4;
   const float nkb = mkb * q.ns4;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float za = fminf(__builtin_fmaf(g[j], q.rec4, mka), cka);
+    const float za = __uint_as_float(min(__float_as_uint(__builtin_fmaf(g[j], q.rec4, mka)), cka));
     g[j] = __builtin_fmaf(za, q.s4, nka);
-    const float zb = fminf(__builtin_fmaf(g[4 + j], q.rec4, mkb), ckb);
+    const float zb = __uint_as_float(min(__float_as_uint(__builtin_fmaf(g[4 + j], q.rec4, mkb)), ckb));
     g[4 + j] = __builtin_fmaf(zb, q.s4, nkb);
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Attention forward: one 512-thread workgroup per CU (eight waves of 32 query rows, two
+// waves per SIMD), K and V^T tiles double-buffered in LDS so the DMA of tile t + 1 is issued
+// a whole tile ahead, and one barrier per tile.  gfx950 services a ds_read_b128 in four
+// passes of 16 lanes (lane bit 5, parity of lane bits 2..4); a pass is conflict-free when
+// its 16 lanes hit 16 distinct 16-byte bank groups.  LDS rows are padded to 17 16-byte units (272 B): unit u of a tile
+// holds piece u % 17 of row u / 17 (piece 16 is padding), so every operand read is a base
+// register plus a constant offset, and under the ds_read_b128 pass structure (lane bit 5,
+// parity of lane bits 2..4) the QK reads (rows pi(kb, n), one piece) and the PV reads
+// (rows n, one piece) of a pass hit 16 distinct bank groups: (17 r + p) mod 16 = (r + p)
+// mod 16 with 16 distinct r mod 16 per pass.
+constexpr int kRowUnits = 17;
+constexpr int kTileBytes = kKeyTile * kRowUnits * 16;  // 34816
+constexpr int kStageBytes = 2 * kTileBytes;             // K tile, then V^T tile
+
+__device__ __forceinline__ bf16x8 lds_read_at(const uint8_t* base, int byte_off) {
+  return *reinterpret_cast<const bf16x8*>(base + byte_off);
+}
+
 template <int LV, bool kQuantP, bool kSame>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t ks[kKeyTile * kDim];
-  __shared__ __attribute__((aligned(1024))) uint16_t vs[kDim * kKeyTile];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -239,7 +256,7 @@ void attn_fwd_kernel(AttnArgs a) {
   const int kvh = (bx / hgroups) % a.Hkv;
   const int b = bx / (hgroups * a.Hkv);
   const int pb = a.causal ? (a.n_pblocks - 1 - static_cast<int>(blockIdx.y)) : static_cast<int>(blockIdx.y);
-  const int pos_per_wg = 32 * (4 / a.hpw);
+  const int pos_per_wg = 32 * (8 / a.hpw);
   const int hq = kvh * G + hg * a.hpw + (w % a.hpw);
   const int p0w = pb * pos_per_wg + (w / a.hpw) * 32;
   const int off = a.Lk - a.Lq;  // bottom-right alignment: row p sees keys <= p + off
@@ -279,85 +296,85 @@ void attn_fwd_kernel(AttnArgs a) {
   const uint16_t* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
   const uint16_t* vbase = a.vt + b * a.v_sb + kvh * a.v_sh;
 
-  // DMA assignment: wave w, instruction j fills LDS rows 32 w + 4 j + lane / 16 (1 KiB per
-  // instruction); lane writes stored position lane % 16 of its row, i.e. logical piece
-  // (lane % 16) ^ swz(row).  The swizzle of rows 32 w + 4 j + lane / 16 depends on j % 4
-  // only, so instructions j and j + 4 share a lane offset and differ by 16 rows.
+  // DMA assignment: instruction j (0..3) of wave w fills tile units 512 j + 64 w + lane;
+  // waves 0 and 1 also fill units 2048 + 64 w + lane (j = 4).  Unit u is piece u % 17 of
+  // row u / 17; the padding piece re-reads piece 15 of its row.
   const int ws = __builtin_amdgcn_readfirstlane(w);
-  uint32_t kvo[4], vvo[4];
+  const int nj = ws < 2 ? 5 : 4;
+  uint32_t kvo[5], vvo[5];
+  int krow[5];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 32 * ws + 4 * j + (lane >> 4);
-    kvo[j] = static_cast<uint32_t>(r * static_cast<int>(a.k_sl) + 8 * ((lane & 15) ^ k_swz(r))) * 2u;
-    vvo[j] = static_cast<uint32_t>(r * static_cast<int>(a.v_sd) + 8 * ((lane & 15) ^ (r & 15))) * 2u;
+  for (int j = 0; j < 5; ++j) {
+    const int u = (j < 4 ? 512 * j : 2048) + 64 * ws + lane;
+    const int r = u / kRowUnits;
+    const int p = min(u - r * kRowUnits, 15);
+    krow[j] = r;
+    kvo[j] = static_cast<uint32_t>(r * static_cast<int>(a.k_sl) + 8 * p) * 2u;
+    vvo[j] = static_cast<uint32_t>(r * static_cast<int>(a.v_sd) + 8 * p) * 2u;
   }
-  const uint32_t k16 = static_cast<uint32_t>(16 * a.k_sl) * 2u;
-  const uint32_t v16 = static_cast<uint32_t>(16 * a.v_sd) * 2u;
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, a.Lk > 0 ? static_cast<uint32_t>(((a.Lk - 1) * a.k_sl + kDim) * 2) : 0u);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, static_cast<uint32_t>((127 * a.v_sd + a.v_sd) * 2));
-  uint16_t* const ks_w = ks + ws * (8 * 512);
-  uint16_t* const vs_w = vs + ws * (8 * 512);
 
-  auto load_k = [&](int t) {
+  auto load_tile = [&](int t) {
+    uint8_t* const st = lds + (t & 1) * kStageBytes;
     const int key0 = t * kKeyTile;
-    const uint32_t soff = static_cast<uint32_t>(key0 * a.k_sl) * 2u;
+    const uint32_t ksoff = static_cast<uint32_t>(key0 * a.k_sl) * 2u;
+    const uint32_t vsoff = static_cast<uint32_t>(key0) * 2u;
     if (key0 + kKeyTile <= a.Lk) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dma16(krs, kvo[j & 3], soff + (j >> 2) * k16, ks_w + j * 512);
+      for (int j = 0; j < 5; ++j)
+        if (j < nj) dma16(krs, kvo[j], ksoff, reinterpret_cast<uint16_t*>(st + ((j < 4 ? 512 * j : 2048) + 64 * ws) * 16));
     } else {
       // ragged last tile: rows past the last key re-read the last key (their scores are
       // masked to -inf before use)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int r = 32 * ws + 4 * j + (lane >> 4);
-        const int rr = min(r, a.Lk - 1 - key0);
-        const uint32_t vo = static_cast<uint32_t>(rr * static_cast<int>(a.k_sl) + 8 * ((lane & 15) ^ k_swz(r))) * 2u;
-        dma16(krs, vo, soff, ks_w + j * 512);
+      for (int j = 0; j < 5; ++j) {
+        if (j < nj) {
+          const int rr = min(krow[j], a.Lk - 1 - key0);
+          const uint32_t vo = kvo[j] - static_cast<uint32_t>((krow[j] - rr) * static_cast<int>(a.k_sl)) * 2u;
+          dma16(krs, vo, ksoff, reinterpret_cast<uint16_t*>(st + ((j < 4 ? 512 * j : 2048) + 64 * ws) * 16));
+        }
       }
     }
-  };
-  auto load_v = [&](int t) {
-    const uint32_t soff = static_cast<uint32_t>(t * kKeyTile) * 2u;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dma16(vrs, vvo[j & 3], soff + (j >> 2) * v16, vs_w + j * 512);
+    for (int j = 0; j < 5; ++j)
+      if (j < nj) dma16(vrs, vvo[j], vsoff, reinterpret_cast<uint16_t*>(st + kTileBytes + ((j < 4 ? 512 * j : 2048) + 64 * ws) * 16));
   };
 
-  // LDS operand addresses (element offsets).  QK: key row pi(0, n) + 16 kb, piece 2c + half.
+  // LDS operand offsets (bytes).  QK: key row pi(0, n) + 16 kb, piece 2c + half.
   const int krow0 = 64 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
-  const int ksw = k_swz(krow0);
-  int kaddr[8];
-#pragma unroll
-  for (int c = 0; c < 8; ++c) kaddr[c] = krow0 * kDim + (((2 * c + half) ^ ksw) * 8);
+  const int kbyte = krow0 * (kRowUnits * 16) + half * 16;
   // PV: V^T row 32 mb + n, piece 8 half + c.
-  int vaddr[8];
-#pragma unroll
-  for (int c = 0; c < 8; ++c) vaddr[c] = n * kDim + (((8 * half + c) ^ (n & 15)) * 8);
+  const int vbyte = kTileBytes + n * (kRowUnits * 16) + half * 128;
 
-  if (ntiles > 0) {
-    load_k(0);
-    load_v(0);
-  }
-  wait_all_memory();
-  __syncthreads();
+  if (ntiles > 0) load_tile(0);
 
   for (int t = 0; t < ntiles; ++t) {
+    // tile t has landed for every wave; every wave is done with tile t - 1, whose stage
+    // the DMA of tile t + 1 overwrites
+    wait_all_memory();
+    __syncthreads();
+    if (t + 1 < ntiles) load_tile(t + 1);
+    const uint8_t* const st = lds + (t & 1) * kStageBytes;
+    const uint8_t* const kp = st + kbyte;
+    const uint8_t* const vp = st + vbyte;
+
     const int key0 = t * kKeyTile;
-    const bool active = key0 < kend_w;
+    if (key0 >= kend_w) continue;
     floatx16 s[4];
-    if (active) {
-      // ---- S^T = K Q^T
-      // c-major: four independent accumulation chains; the K fragments of step c + 1 are
-      // read while the MFMAs of step c run
+    {
+      // ---- S^T = K Q^T, c-major (four independent accumulation chains); the K fragments
+      // of step c + 1 are read while the MFMAs of step c run
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) s[kb] = floatx16{};
       bf16x8 kf[2][4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) kf[0][kb] = lds_read16(ks + kaddr[0] + kb * 16 * kDim);
+      for (int kb = 0; kb < 4; ++kb) kf[0][kb] = lds_read_at(kp, kb * 16 * kRowUnits * 16);
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         if (c + 1 < 8) {
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) kf[(c + 1) & 1][kb] = lds_read16(ks + kaddr[c + 1] + kb * 16 * kDim);
+          for (int kb = 0; kb < 4; ++kb) kf[(c + 1) & 1][kb] = lds_read_at(kp, kb * 16 * kRowUnits * 16 + (c + 1) * 32);
         }
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) s[kb] = mfma32(kf[c & 1][kb], qf[c], s[kb]);
@@ -371,125 +388,115 @@ void attn_fwd_kernel(AttnArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // K(t) consumed by every wave; V(t) has landed
-    wait_all_memory();
-    __syncthreads();
-    if (t + 1 < ntiles) load_k(t + 1);
 
-    if (active) {
-      // ---- masks (ragged key tail, causal diagonal)
-      const bool need_mask = (key0 + kKeyTile > a.Lk) || (a.causal && key0 + kKeyTile - 1 > p0w + off);
-      if (need_mask) {
-        const int lim = a.causal ? min(a.Lk - 1, pos + off) : a.Lk - 1;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (key0 + 64 * half + 16 * kb + i > lim) s[kb][i] = -INFINITY;
-      }
-      // ---- online softmax in the log2 domain
-      float mx = -INFINITY;
+    // ---- masks (ragged key tail, causal diagonal)
+    const bool need_mask = (key0 + kKeyTile > a.Lk) || (a.causal && key0 + kKeyTile - 1 > p0w + off);
+    if (need_mask) {
+      const int lim = a.causal ? min(a.Lk - 1, pos + off) : a.Lk - 1;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-      const float mx_row = halves_max(mx);
-      const float m_new = fmaxf(m_run, mx_row * a.c1);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float nm = -m_use;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      m_run = m_new;
-      if (__ballot(alpha != 1.0f) != 0) {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
-        l_run *= alpha;
-      }
-      // ---- P, its HiF4 QDQ and the row sum, one 8-key chunk at a time; chunk c of this lane
-      // is keys 64 half + 8c .. 8c+7, the B operand of PV k-chunk c.
-      PQuant pq;
-      if (kQuantP) {
-        // group maximum = P of the lane's largest score (same fma and exp2)
-        pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
-      }
-      float rowsum = 0.0f;
-      // Software pipeline over the eight 8-key chunks: iteration c computes chunk c's P^
-      // (VALU) while the MFMAs of chunk c - 1 issue one at a time between those VALU
-      // instructions, so each MFMA executes under VALU work of the same wave.
-      bf16x8 pprev, plprev;
-#pragma unroll
-      for (int c = 0; c <= 8; ++c) {
-        bf16x8 va[4];
-        if (c >= 1) {
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) va[mb] = lds_read16(vs + vaddr[c - 1] + mb * 32 * kDim);
-        }
-        bf16x8 pcur, plcur;
-        if (c < 8) {
-          float pc[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
-          if (!(kQuantP && kSame)) {
-            // the normalizer sums P (unquantized mode, or no P quantization)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) rowsum += pc[j];
-          }
-          if (kQuantP) {
-            pquant8<LV>(pc, pq);
-            pcur = pack8<true>(pc);
-            if (kSame) {
-              uint32_t wv[4];
-              __builtin_memcpy(wv, &pcur, 16);
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                bf16x2_t pr;
-                __builtin_memcpy(&pr, &wv[i], 4);
-                rowsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, rowsum, false);
-              }
-            }
-          } else {
-            // Unquantized P is not exact in bf16: it goes in as hi + lo bf16 parts
-            // (16 significant bits) so PV keeps the fp32-operand accuracy of the reference.
-            float r[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) r[j] = pc[j] - bf16_rne(pc[j]);
-            pcur = pack8<false>(pc);
-            plcur = pack8<false>(r);
-          }
-        }
-        if (c >= 1) {
-          // ---- O^T += V^T P^T for chunk c - 1
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
-            acc[mb] = mfma32(va[mb], pprev, acc[mb]);
-            if (!kQuantP) acc[mb] = mfma32(va[mb], plprev, acc[mb]);
-          }
-          // issue order: the four LDS reads, ~20 VALU (read latency), then one MFMA per
-          // ~12 VALU instructions
-          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-          if (c < 8) {
-            __builtin_amdgcn_sched_group_barrier(0x002, 20, 0);
-#pragma unroll
-            for (int i = 0; i < (kQuantP ? 4 : 8); ++i) {
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-              __builtin_amdgcn_sched_group_barrier(0x002, kQuantP ? 12 : 6, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
-          } else {
-            __builtin_amdgcn_sched_group_barrier(0x008, kQuantP ? 4 : 8, 0);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        pprev = pcur;
-        plprev = plcur;
-      }
-      l_run += halves_sum(rowsum);
+        for (int i = 0; i < 16; ++i)
+          if (key0 + 64 * half + 16 * kb + i > lim) s[kb][i] = -INFINITY;
     }
-    // V(t) consumed by every wave; K(t+1) has landed
-    wait_all_memory();
-    __syncthreads();
-    if (t + 1 < ntiles) load_v(t + 1);
+    // ---- online softmax in the log2 domain
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+    const float mx_row = halves_max(mx);
+    const float m_new = fmaxf(m_run, mx_row * a.c1);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float nm = -m_use;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    if (__ballot(alpha != 1.0f) != 0) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
+      l_run *= alpha;
+    }
+    // ---- P, its HiF4 QDQ and the row sum, one 8-key chunk at a time; chunk c of this lane
+    // is keys 64 half + 8c .. 8c+7, the B operand of PV k-chunk c.
+    PQuant pq;
+    if (kQuantP) {
+      // group maximum = P of the lane's largest score (same fma and exp2)
+      pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
+    }
+    float rowsum = 0.0f;
+    // Software pipeline over the eight 8-key chunks: iteration c computes chunk c's P^
+    // (VALU) while the MFMAs of chunk c - 1 issue one at a time between those VALU
+    // instructions.
+    bf16x8 pprev, plprev;
+#pragma unroll
+    for (int c = 0; c <= 8; ++c) {
+      bf16x8 va[4];
+      if (c >= 1) {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) va[mb] = lds_read_at(vp, mb * 32 * kRowUnits * 16 + (c - 1) * 16);
+      }
+      bf16x8 pcur, plcur;
+      if (c < 8) {
+        float pc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
+        if (!(kQuantP && kSame)) {
+          // the normalizer sums P (unquantized mode, or no P quantization)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) rowsum += pc[j];
+        }
+        if (kQuantP) {
+          pquant8<LV>(pc, pq);
+          pcur = pack8<true>(pc);
+          if (kSame) {
+            uint32_t wv[4];
+            __builtin_memcpy(wv, &pcur, 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              bf16x2_t pr;
+              __builtin_memcpy(&pr, &wv[i], 4);
+              rowsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, rowsum, false);
+            }
+          }
+        } else {
+          // Unquantized P is not exact in bf16: it goes in as hi + lo bf16 parts
+          // (16 significant bits) so PV keeps the fp32-operand accuracy of the reference.
+          float r[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) r[j] = pc[j] - bf16_rne(pc[j]);
+          pcur = pack8<false>(pc);
+          plcur = pack8<false>(r);
+        }
+      }
+      if (c >= 1) {
+        // ---- O^T += V^T P^T for chunk c - 1
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          acc[mb] = mfma32(va[mb], pprev, acc[mb]);
+          if (!kQuantP) acc[mb] = mfma32(va[mb], plprev, acc[mb]);
+        }
+        // issue order: the four LDS reads, ~20 VALU (read latency), then one MFMA per
+        // ~12 VALU instructions
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        if (c < 8) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 20, 0);
+#pragma unroll
+          for (int i = 0; i < (kQuantP ? 4 : 8); ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, kQuantP ? 12 : 6, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x008, kQuantP ? 4 : 8, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      pprev = pcur;
+      plprev = plcur;
+    }
+    l_run += halves_sum(rowsum);
   }
 
   if (!row_live) return;
