@@ -22,7 +22,13 @@ import torch
 
 from . import _ops
 from .hif4 import HIF4_ATTN_OPERAND_SCALE_LEVELS
-from .simulated_flash_attention import _hif4_group, count_tiles, simulated_flash_attention_forward
+from .simulated_flash_attention import (
+    _hif4_group,
+    _key_operand,
+    _value_operand,
+    count_tiles,
+    simulated_flash_attention_forward,
+)
 
 
 def _block(rotation: bool, rotation_block_size: Optional[int], head_dim: int) -> int:
@@ -102,11 +108,12 @@ def attention_core(
     levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
     q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None, hadamard=block,
                                 smooth=smooth_scale, round_dtype=torch.bfloat16)
-    k_op, _ = _ops.operand_prep(key, levels=levels["k"] if qk_quant else None, hadamard=block,
-                                key_offset=key_offset, smooth=smooth_scale, smooth_divide=True,
-                                round_dtype=torch.bfloat16)
-    vt = _ops.operand_prep_vt(value, levels=levels["v"] if pv_quant else None)
     B, Hq, Lq, D = query.shape
+    # K and V through the decode QDQ cache of the module (sfa:243-289), K with the same
+    # post-RoPE prologue as Q
+    k_op = _key_operand(module, key, enabled=qk_quant, query_length=Lq, levels=levels["k"], hadamard=block,
+                        key_offset=key_offset, smooth=smooth_scale, smooth_divide=True, round_dtype=torch.bfloat16)
+    vt = _value_operand(module, value, enabled=pv_quant, query_length=Lq, levels=levels["v"])
     Lk = key.shape[2]
     scale = float(scaling if scaling is not None else D**-0.5)
     causal = bool(getattr(module, "is_causal", True))

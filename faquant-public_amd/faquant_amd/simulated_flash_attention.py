@@ -131,6 +131,91 @@ def _hif4_group(kwargs: dict, what: str) -> int:
     return HIF4_BLOCK_SIZE if group == -1 else group
 
 
+_KV_STATE = "_faquant_amd_kv_cache_state"
+_KV_GROWTH = 1024  # keys of headroom added when a decode cache buffer grows
+
+
+def _cache_capacity(length: int) -> int:
+    return _ops._pad_keys(length)
+
+
+def _append_allowed(module, name: str, state, tensor: torch.Tensor, query_length: int) -> bool:
+    """The reference's append condition (sfa:268-276): decode step, the cache this
+    module holds is ours and still attached, same device/dtype/leading shape/head_dim,
+    and exactly one new position."""
+    return (
+        query_length == 1
+        and state is not None
+        and getattr(module, name, None) is state["view"]
+        and state["device"] == tensor.device
+        and state["dtype"] == tensor.dtype
+        and state["lead"] == tuple(tensor.shape[:-2])
+        and state["length"] + 1 == tensor.shape[-2]
+    )
+
+
+def _key_operand(module, key: torch.Tensor, *, enabled: bool, query_length: int, levels: str, **prep) -> torch.Tensor:
+    """bf16 K operand [B, Hkv, Lk, 128]; with K quantization it doubles as the decode QDQ
+    cache ``faquant_k_matmul_qdq_cache`` (sfa:243-289): a decode step quantizes only the
+    appended position into a capacity-padded buffer.  K QDQ (and the optional Q/K
+    prologue ``prep`` of operand_prep) is token-local, so this is bitwise equal to
+    quantizing the whole cache again."""
+    name = "faquant_k_matmul_qdq_cache"
+    states = getattr(module, _KV_STATE, None) or {}
+    if not enabled:
+        setattr(module, name, None)
+        states.pop("k", None)
+        setattr(module, _KV_STATE, states)
+        return _ops.operand_prep(key, levels=None, **prep)[0]
+    B, H, L, D = key.shape
+    st = states.get("k")
+    if _append_allowed(module, name, st, key, query_length):
+        buf = st["buf"]
+        if L > buf.shape[2]:
+            grown = torch.empty((B, H, _cache_capacity(L + _KV_GROWTH), D), device=key.device, dtype=torch.bfloat16)
+            grown[:, :, : L - 1].copy_(buf[:, :, : L - 1])
+            buf = grown
+        _ops.operand_prep(key[:, :, L - 1 :], levels=levels, out=buf[:, :, L - 1 : L], **prep)
+    else:
+        buf = torch.empty((B, H, _cache_capacity(L), D), device=key.device, dtype=torch.bfloat16)
+        _ops.operand_prep(key, levels=levels, out=buf[:, :, :L], **prep)
+    view = buf[:, :, :L]
+    states["k"] = dict(buf=buf, view=view, length=L, device=key.device, dtype=key.dtype, lead=(B, H))
+    setattr(module, _KV_STATE, states)
+    setattr(module, name, view)
+    return view
+
+
+def _value_operand(module, value: torch.Tensor, *, enabled: bool, query_length: int, levels: str) -> torch.Tensor:
+    """Transposed bf16 V operand [B, Hkv, 128, Lpad] (keys >= Lk zero); with V quantization
+    ``faquant_v_matmul_qdq_cache`` is its [B, Hkv, Lk, 128] view and a decode step
+    quantizes only the appended position (sfa:243-289)."""
+    name = "faquant_v_matmul_qdq_cache"
+    states = getattr(module, _KV_STATE, None) or {}
+    if not enabled:
+        setattr(module, name, None)
+        states.pop("v", None)
+        setattr(module, _KV_STATE, states)
+        return _ops.operand_prep_vt(value, levels=None)
+    B, H, L, D = value.shape
+    st = states.get("v")
+    if _append_allowed(module, name, st, value, query_length):
+        vt = st["buf"]
+        if L > vt.shape[-1]:
+            grown = torch.zeros((B, H, D, _cache_capacity(L + _KV_GROWTH)), device=value.device, dtype=torch.bfloat16)
+            grown[..., : L - 1].copy_(vt[..., : L - 1])
+            vt = grown
+        tail = _ops.operand_prep_vt(value[:, :, L - 1 :], levels=levels)
+        vt[..., L - 1 : L].copy_(tail[..., :1])
+    else:
+        vt = _ops.operand_prep_vt(value, levels=levels)
+    view = vt.transpose(-1, -2)[..., :L, :]
+    states["v"] = dict(buf=vt, view=view, length=L, device=value.device, dtype=value.dtype, lead=(B, H))
+    setattr(module, _KV_STATE, states)
+    setattr(module, name, view)
+    return vt
+
+
 def simulated_flash_attention_forward(
     module: torch.nn.Module,
     query: torch.Tensor,
@@ -226,12 +311,8 @@ def simulated_flash_attention_forward(
 
     levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
     q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None)
-    k_op, _ = _ops.operand_prep(key, levels=levels["k"] if qk_quant else None)
-    vt = _ops.operand_prep_vt(value, levels=levels["v"] if pv_quant else None)
-    # The reference caches K/V QDQ values for decode (sfa:243-289); the HIP path keeps
-    # the quantized operands under the same names (V as a [B, Hkv, L, 128] view).
-    module.faquant_k_matmul_qdq_cache = k_op if qk_quant else None
-    module.faquant_v_matmul_qdq_cache = vt.transpose(-1, -2)[..., :key_length, :] if pv_quant else None
+    k_op = _key_operand(module, key, enabled=qk_quant, query_length=query_length, levels=levels["k"])
+    vt = _value_operand(module, value, enabled=pv_quant, query_length=query_length, levels=levels["v"])
 
     output = torch.empty((batch, query_length, query_heads, head_dim), device=query.device, dtype=query.dtype)
     _ops.attention_fwd(
