@@ -215,13 +215,15 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
                       int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh, int64_t v_sd,
                       int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq,
                       int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels, int norm_same,
-                      float* row_den, faq_stream_t stream) {
+                      float* row_den, int out_levels, faq_stream_t stream) {
   if (!q || !k || !vt || !o) return fail(FAQ_EINVAL, "faq_attention_fwd: null operand");
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "faq_attention_fwd: bad sizes");
   if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
   if (Lpad % 128 || Lpad < Lk) return fail(FAQ_EINVAL, "faq_attention_fwd: Lpad must be a multiple of 128 >= Lk");
   if (o_dtype != FAQ_F32 && o_dtype != FAQ_BF16) return fail(FAQ_EUNSUP, "faq_attention_fwd: output must be fp32 or bf16");
   if (quant_p && !valid_levels(p_levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", p_levels);
+  if (out_levels != 0 && !valid_levels(out_levels))
+    return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", out_levels);
   if (!aligned16(q) || !aligned16(k) || !aligned16(vt) || !aligned16(o))
     return fail(FAQ_EINVAL, "faq_attention_fwd: pointers must be 16-byte aligned");
   if ((q_sb | q_sh | q_sl | k_sb | k_sh | k_sl | v_sb | v_sh | v_sd) & 7)
@@ -266,6 +268,7 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
   a.hpw = hpw;
   a.n_pblocks = (Lq + pos_per_wg - 1) / pos_per_wg;
   a.row_den = row_den;
+  a.out_levels = out_levels;
   const dim3 grid(static_cast<unsigned>(B * Hkv * (G / hpw)), static_cast<unsigned>(a.n_pblocks));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int lv = quant_p ? p_levels : 123;

@@ -75,6 +75,7 @@ struct AttnArgs {
   int hpw;        // query heads per workgroup: 1, 2, 4 or 8
   int n_pblocks;  // position blocks per head group
   float* row_den;  // optional fp32 [B, Hq, Lq]: final denominator l
+  int out_levels;  // 0, or HiF4 levels of a QDQ of each 64-value half of an output row
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -216,6 +217,71 @@ __device__ __forceinline__ void pquant8(float* g, const PQuant& q) {
     g[j] = __builtin_fmaf(za, q.s4, nka);
     const float zb = __uint_as_float(min(__float_as_uint(__builtin_fmaf(g[4 + j], q.rec4, mkb)), ckb));
     g[4 + j] = __builtin_fmaf(zb, q.s4, nkb);
+  }
+}
+
+// Value of x in lane l ^ 32 (v_permlane32_swap of a register with itself gives the
+// lower-half lane's copy in result 0 and the upper-half lane's in result 1).
+__device__ __forceinline__ float partner32(float x, int half) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(half ? r[0] : r[1]);
+}
+
+// HiF4 QDQ (levels LV) of one output row held by lanes n and n + 32: val[mb][j][r] is dim
+// 32 mb + 8 j + 4 half + r, so each 4-value micro group is lane-local, an 8-value group
+// pairs this lane's 4 values with the partner's, and each 64-value group is mb in
+// {2g, 2g + 1} of both lanes.  Same arithmetic as the row quantizer (hif4.py:143-271):
+// group maximum of |x|, E6M2 scale, micro exponents, codes; a NaN anywhere in a 64-value
+// group makes the whole group NaN.
+template <int LV>
+__device__ __forceinline__ void qdq_out_row(float (&val)[4][4][4], int half) {
+  float m3[4][4], pm3[4][4];
+  uint32_t nan = 0;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float m = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        m = fmaxf(m, fabsf(val[mb][j][r]));
+        if (val[mb][j][r] != val[mb][j][r]) nan |= 1u << (mb >> 1);
+      }
+      m3[mb][j] = m;
+    }
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pm3[mb][j] = partner32(m3[mb][j], half);
+  nan |= __float_as_uint(partner32(__uint_as_float(nan), half));
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    float m1 = 0.0f;
+#pragma unroll
+    for (int mb = 2 * g; mb < 2 * g + 2; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m1 = fmaxf(m1, fmaxf(m3[mb][j], pm3[mb][j]));
+    float s, rec;
+    hif4_scale<LV>(m1, s, rec);
+#pragma unroll
+    for (int mb = 2 * g; mb < 2 * g + 2; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // the 8-value group's first 4-group lives in the lower-half lane
+        const float m3a = half ? pm3[mb][j] : m3[mb][j];
+        const float m3b = half ? m3[mb][j] : pm3[mb][j];
+        int ka, kb;
+        hif4_micro<LV>(m3a, m3b, rec, ka, kb);
+        float qm4, dq;
+        hif4_group_mults(s, rec, half ? kb : ka, qm4, dq);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = val[mb][j][r];
+          const float y = hif4_element(fabsf(x), qm4, dq);
+          val[mb][j][r] = ((nan >> g) & 1u) ? __builtin_nanf("") : (x < 0.0f ? -y : y);
+        }
+      }
   }
 }
 
@@ -505,6 +571,21 @@ void attn_fwd_kernel(AttnArgs a) {
   if (a.row_den && half == 0) a.row_den[(static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos] = l;
   char* obase = static_cast<char*>(a.o);
   const int64_t orow = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl;
+  // o = acc / l (0 for rows that saw no key), in the output dtype
+  float val[4][4][4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = l > 0.0f ? acc[mb][4 * j + r] / inv_guard : 0.0f;
+        val[mb][j][r] = a.o_f32 ? x : bf16_rne(x);
+      }
+  // the o_proj-input QDQ of the output row (qwen3.py:167-171), on the output-dtype values
+  if (a.out_levels == 123) qdq_out_row<123>(val, half);
+  else if (a.out_levels == 12) qdq_out_row<12>(val, half);
+  else if (a.out_levels == 13) qdq_out_row<13>(val, half);
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -512,7 +593,7 @@ void attn_fwd_kernel(AttnArgs a) {
       const int d = 32 * mb + 8 * j + 4 * half;
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = l > 0.0f ? acc[mb][4 * j + r] / inv_guard : 0.0f;
+      for (int r = 0; r < 4; ++r) v[r] = val[mb][j][r];
       if (a.o_f32) {
         *reinterpret_cast<float4*>(obase + (orow + d) * 4) = make_float4(v[0], v[1], v[2], v[3]);
       } else {

@@ -51,7 +51,7 @@ _SIGNATURES = {
             _vp, _c_i64, _c_i64, _c_i64,
             _vp, _c_i64, _c_i64, _c_i64, _c_int,
             _vp, _c_int, _c_i64, _c_i64, _c_i64,
-            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp, _vp,
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp, _c_int, _vp,
         ],
         _c_int,
     ),

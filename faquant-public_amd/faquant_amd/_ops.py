@@ -180,9 +180,12 @@ def attention_fwd(
     norm_same: bool,
     out: torch.Tensor,
     row_den: torch.Tensor | None = None,
+    out_levels: str | None = None,
 ) -> torch.Tensor:
     """Attention over bf16 operands q [B, Hq, Lq, 128], k [B, Hkv, Lk, 128] and
-    vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16)."""
+    vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16).
+    ``out_levels`` adds a HiF4 QDQ of each 64-value half of every output row, after its
+    rounding to the output dtype (the o_proj-input quantizer, qwen3.py:167-171)."""
     _lib.require_device(q, k, vt, out, row_den)
     lib = _lib.load()
     B, Hq, Lq, D = q.shape
@@ -204,7 +207,7 @@ def attention_fwd(
             out.data_ptr(), _lib.dtype_code(out.dtype), *os_,
             B, Hq, Hkv, Lq, int(key_length), int(bool(causal)), float(scale),
             int(bool(quant_p)), int(p_levels), int(bool(norm_same)), _lib.ptr(row_den),
-            _lib.stream_ptr(q.device),
+            int(out_levels) if out_levels else 0, _lib.stream_ptr(q.device),
         )
     )
     return out

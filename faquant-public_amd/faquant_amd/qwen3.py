@@ -21,7 +21,9 @@ from typing import Optional
 import torch
 
 from . import _ops
-from .hif4 import HIF4_ATTN_OPERAND_SCALE_LEVELS
+from .hif4 import HIF4_ACT_SCALE_LEVELS, HIF4_ATTN_OPERAND_SCALE_LEVELS
+from .hif4 import _resolve as resolve_hif4_levels
+from .quantization import check_hif4_arguments, fake_quantize
 from .simulated_flash_attention import (
     _hif4_group,
     _key_operand,
@@ -75,6 +77,24 @@ def post_rope_qk_transform(
     return out[0], out[1]
 
 
+def _output_quant_levels(module: torch.nn.Module) -> Optional[str]:
+    """HiF4 levels of the attention-output (o_proj input) QDQ of qwen3.py:167-171, or None.
+
+    Validates ``faquant_core_quant_kwargs`` like fake_quantize's HiF4 branch
+    (quantization.py:30-57); other formats raise NotImplementedError.
+    """
+    if not getattr(module, "faquant_attention_output_quant", False):
+        return None
+    if getattr(getattr(module, "o_proj", None), "faquant_quantizes_input", False):
+        return None
+    kwargs = dict(module.faquant_core_quant_kwargs)
+    if kwargs.get("quant_format", "int") != "hif4":
+        fake_quantize(torch.zeros(1, 64), **kwargs)  # raises for formats outside the HiF4 path
+        return None
+    check_hif4_arguments(**{k: kwargs[k] for k in ("bits", "group_size", "symmetric", "clip_ratio") if k in kwargs})
+    return resolve_hif4_levels(kwargs.get("hif4_levels"), HIF4_ACT_SCALE_LEVELS)
+
+
 def attention_core(
     module: torch.nn.Module,
     query: torch.Tensor,
@@ -87,7 +107,10 @@ def attention_core(
 
     Equivalent to the reference's excursion followed by
     ``simulated_flash_attention_forward(module, q, k, v, None, scaling=scaling)``
-    for mask-free causal prefill; other cases go through that drop-in.
+    for mask-free causal prefill; other cases go through that drop-in.  When the module
+    enables the attention-output quantizer (``faquant_attention_output_quant`` and o_proj
+    does not quantize its own input, qwen3.py:167-171), the HiF4 QDQ of the output rows
+    with ``faquant_core_quant_kwargs`` runs in the attention kernel's epilogue.
     """
     smooth_scale = _smooth(getattr(module, "faquant_qk_smooth_scale", None),
                            getattr(module, "faquant_qk_smooth_delta", None))
@@ -101,7 +124,10 @@ def attention_core(
             query, key, smooth_scale=smooth_scale, key_offset=key_offset, rotation=rotation,
             rotation_block_size=getattr(module, "faquant_qk_rotation_block_size", None),
         )
-        return simulated_flash_attention_forward(module, q, k, value, None, scaling=scaling)[0]
+        out = simulated_flash_attention_forward(module, q, k, value, None, scaling=scaling)[0]
+        if _output_quant_levels(module) is not None:
+            out = fake_quantize(out.reshape(*out.shape[:2], -1), **module.faquant_core_quant_kwargs).view(out.shape)
+        return out
     quant_kwargs = module.faquant_matmul_quant_kwargs
     qk_group = _hif4_group(getattr(module, "faquant_qk_matmul_quant_kwargs", quant_kwargs), "QK") if qk_quant else 64
     pv_group = _hif4_group(getattr(module, "faquant_pv_matmul_quant_kwargs", quant_kwargs), "PV") if pv_quant else 64
@@ -120,7 +146,8 @@ def attention_core(
     out = torch.empty((B, Lq, Hq, D), device=query.device, dtype=query.dtype)
     mode = getattr(module, "faquant_pv_normalizer_mode", "unquantized")
     _ops.attention_fwd(q_op, k_op, vt, Lk, causal=causal, scale=scale, quant_p=pv_quant,
-                       p_levels=levels["p"], norm_same=mode == "quantized_same", out=out.transpose(1, 2))
+                       p_levels=levels["p"], norm_same=mode == "quantized_same", out=out.transpose(1, 2),
+                       out_levels=_output_quant_levels(module))
     count_tiles(
         module.faquant_simulated_attention_stats, batch=B, query_heads=Hq, query_length=Lq, key_length=Lk,
         head_dim=D, query_chunk=int(module.faquant_attention_query_chunk_size), key_chunk=_ops.KEY_TILE,

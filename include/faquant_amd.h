@@ -118,12 +118,15 @@ int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int
  *   quant_p     1: HiF4-quantize P along keys in 64-groups with p_levels
  *   norm_same   1: denominator sums the quantized P (P-Reordering, "quantized_same")
  *   row_den     optional fp32 [B, Hq, Lq]: the final softmax denominator of each row
+ *   out_levels  0, or HiF4 levels (123 / 12 / 13) of a QDQ of every 64-value half of each
+ *               output row after its rounding to o_dtype: the o_proj-input activation
+ *               quantizer of src/faquant/qwen3.py:167-171, fused into the epilogue
  */
 int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
                       int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
                       int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                       int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels,
-                      int norm_same, float* row_den, faq_stream_t stream);
+                      int norm_same, float* row_den, int out_levels, faq_stream_t stream);
 
 #ifdef __cplusplus
 }

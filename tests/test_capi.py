@@ -66,11 +66,14 @@ def test_validation_statuses_without_device_work(lib):
     assert lib.faq_operand_prep(p16, 1, 128, 128, 128, 1, 1, 1, None, 0, None, 0, 0, 96, 1, None, p16, 128, 128, 128,
                                 123, None) == _lib.EUNSUP
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
-                               1, 3, 2, 1, 1, 1, 0.1, 1, 123, 1, None, None)
+                               1, 3, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, None)
     assert rc == _lib.EINVAL and "divisible" in lib.faq_last_error().decode()
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 100, p16, 1, 0, 0, 0,
-                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, None)
+                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, None)
     assert rc == _lib.EINVAL and "Lpad" in lib.faq_last_error().decode()
+    rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
+                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 45, None)
+    assert rc == _lib.EINVAL and "123, 12 or 13" in lib.faq_last_error().decode()
 
 
 def test_status_maps_to_reference_exception_types(lib):
