@@ -56,6 +56,14 @@ void launch_hadamard_in(const faq::HadamardRowsArgs& a, int out_dtype, int64_t t
   else launch_hadamard<Tin, __half>(a, threads, st);
 }
 
+template <typename T>
+void launch_act(const faq::ActQdqArgs& a, int levels, int64_t threads, hipStream_t st) {
+  const dim3 grid(grid_for(threads));
+  if (levels == 12) hipLaunchKernelGGL((faq::act_qdq_rows_kernel<T, 12>), grid, dim3(256), 0, st, a);
+  else if (levels == 13) hipLaunchKernelGGL((faq::act_qdq_rows_kernel<T, 13>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((faq::act_qdq_rows_kernel<T, 123>), grid, dim3(256), 0, st, a);
+}
+
 template <typename Tin, typename Tround>
 void launch_prep(const faq::OperandPrepArgs& a, int levels, int64_t threads, hipStream_t st) {
   const dim3 grid(grid_for(threads));
@@ -143,6 +151,34 @@ int faq_hadamard_rows(const void* x, void* y, int64_t rows, int64_t cols, int bl
   else if (in_dtype == FAQ_BF16) launch_hadamard_in<__hip_bfloat16>(a, out_dtype, threads, st);
   else launch_hadamard_in<__half>(a, out_dtype, threads, st);
   return check_launch("faq_hadamard_rows");
+}
+
+int faq_act_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const float* col_scale,
+                     int hadamard, int levels, faq_stream_t stream) {
+  if (!x || !y) return fail(FAQ_EINVAL, "faq_act_qdq_rows: null input or output");
+  if (rows < 0) return fail(FAQ_EINVAL, "faq_act_qdq_rows: negative size");
+  if (!valid_dtype(dtype)) return fail(FAQ_EINVAL, "faq_act_qdq_rows: bad dtype");
+  if (levels != 0 && !valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
+  if (hadamard != 0) {
+    if (hadamard < 2 || hadamard > 512 || (hadamard & (hadamard - 1)))
+      return fail(FAQ_EINVAL, "Hadamard dimension must be a power of two, got %d", hadamard);
+    if (cols <= 0 || cols % hadamard)
+      return fail(FAQ_EINVAL, "dimension %lld must be divisible by power-of-two block_size=%d",
+                  static_cast<long long>(cols), hadamard);
+    if (cols % 64) return fail(FAQ_EUNSUP, "faq_act_qdq_rows: a rotated row must be a multiple of 64 wide");
+  }
+  if (cols <= 0) return fail(FAQ_EINVAL, "HiF4 fake quantization does not support an empty axis");
+  if (cols % 8) return fail(FAQ_EUNSUP, "faq_act_qdq_rows: row width must be a multiple of 8");
+  if (!aligned16(x) || !aligned16(y)) return fail(FAQ_EINVAL, "faq_act_qdq_rows: pointers must be 16-byte aligned");
+  if (rows == 0) return FAQ_OK;
+  faq::ActQdqArgs a{x, y, rows, cols, col_scale, hadamard,
+                    static_cast<float>(std::sqrt(static_cast<double>(hadamard ? hadamard : 1))), levels != 0};
+  const int64_t threads = rows * ((cols + 63) / 64) * 8;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FAQ_F32) launch_act<float>(a, levels, threads, st);
+  else if (dtype == FAQ_BF16) launch_act<__hip_bfloat16>(a, levels, threads, st);
+  else launch_act<__half>(a, levels, threads, st);
+  return check_launch("faq_act_qdq_rows");
 }
 
 int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,

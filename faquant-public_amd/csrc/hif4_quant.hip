@@ -282,6 +282,57 @@ __global__ __launch_bounds__(256) void hadamard_rows_kernel(HadamardRowsArgs a) 
   if (live) Io<Tout>::store8(static_cast<Tout*>(a.y) + row * a.cols + c0, v);
 }
 
+// ------------------------------------------------------------------ activation prologue
+
+struct ActQdqArgs {
+  const void* x;          // [rows, cols] contiguous, dtype T
+  void* y;                // [rows, cols] contiguous, dtype T
+  int64_t rows;
+  int64_t cols;           // multiple of 8; of 64 and of n when n > 0
+  const float* col_scale; // optional per-column input scale, [cols]
+  int n;                  // 0, or the block Hadamard size (power of two in [2, 512])
+  float sqrt_n;
+  int quant;              // 1: HiF4 QDQ
+};
+
+// The activation path of a quantized Linear (quantization.py:204-276 without the
+// rotation, clamp and companding options): x * bf16(scale) in the input dtype, the
+// per-block fp32 Hadamard with one cast back (rotation.py:117-135), then the HiF4 QDQ
+// in the input dtype.  Lanes map like qdq_rows_kernel: 8 lanes per (row, 64-value
+// group), so a Hadamard block of n <= 512 values is n / 8 consecutive lanes.
+template <typename T, int LV>
+__global__ __launch_bounds__(256) void act_qdq_rows_kernel(ActQdqArgs a) {
+  const int64_t groups = (a.cols + 63) / 64;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t unit = tid >> 3;
+  const int part = threadIdx.x & 7;
+  const bool live = unit < a.rows * groups;
+  const int64_t row = live ? unit / groups : 0;
+  const int64_t g = live ? unit % groups : 0;
+  const int64_t c0 = g * 64 + part * 8;
+  const bool have = live && c0 < a.cols;
+  const T* x = static_cast<const T*>(a.x) + row * a.cols;
+  T* y = static_cast<T*>(a.y) + row * a.cols;
+  float v[8];
+  if (have) {
+    Io<T>::load8(x + c0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  }
+  if (a.col_scale && have) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(v[i] * Io<T>::round(a.col_scale[c0 + i]));
+  }
+  if (a.n) {
+    fwht8_lanes(v, a.n);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(v[i] / a.sqrt_n);
+  }
+  if (a.quant) qdq8<LV>(v);
+  if (have) Io<T>::store8(y + c0, v);
+}
+
 // ------------------------------------------------------------------ operand prologue
 
 struct OperandPrepArgs {

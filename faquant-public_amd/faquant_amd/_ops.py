@@ -92,6 +92,39 @@ def hadamard_rows(x: torch.Tensor, block: int, out_dtype: torch.dtype | None = N
     return y
 
 
+def act_qdq_rows(
+    x: torch.Tensor,
+    *,
+    levels: str | None,
+    hadamard: int = 0,
+    col_scale: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Activation prologue of a W4A4 Linear along the last axis of ``x`` (any leading
+    shape, fp32 / bf16 / fp16): x * dtype(col_scale), optional block Hadamard in fp32 with
+    one cast back, HiF4 QDQ with ``levels`` (None: none).  Output in x's dtype."""
+    _lib.require_device(x, col_scale)
+    lib = _lib.load()
+    if x.ndim == 0:
+        raise ValueError("HiF4 fake quantization requires at least one dimension")
+    cols = x.shape[-1]
+    xc = x.contiguous()
+    rows = xc.numel() // cols if cols else 0
+    y = torch.empty_like(xc) if out is None else out
+    sc = None
+    if col_scale is not None:
+        sc = col_scale.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
+        if sc.numel() != cols:
+            raise ValueError(f"input scale must hold {cols} values, got {sc.numel()}")
+    _lib.check(
+        lib.faq_act_qdq_rows(
+            xc.data_ptr(), y.data_ptr(), rows, cols, _lib.dtype_code(x.dtype), _lib.ptr(sc), int(hadamard),
+            int(levels) if levels else 0, _lib.stream_ptr(x.device),
+        )
+    )
+    return y.view(x.shape)
+
+
 def _bhld_strides(x: torch.Tensor) -> tuple[int, int, int]:
     if x.stride(-1) != 1:
         raise ValueError("operands need a unit stride along head_dim")

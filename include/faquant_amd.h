@@ -19,6 +19,9 @@
  *   faq_hadamard_rows     src/faquant/rotation.py:14-29 hadamard_transform,
  *                         rotation.py:117-135 chunked_block_hadamard_transform,
  *                         src/faquant/wan22_attention.py:186-192 rotate_heads
+ *   faq_act_qdq_rows      src/faquant/quantization.py:204-276 FakeQuantLinear.forward (input
+ *                         scale, online block Hadamard, HiF4 input QDQ) and
+ *                         src/faquant/wan22_hif4.py:81-92 HiF4Linear.forward (input QDQ)
  *   faq_operand_prep      src/faquant/qwen3.py:97-136 (post-RoPE fp32 excursion: key offset,
  *                         Smooth-QK, Hadamard, one cast) and the Q/K QDQ of
  *                         src/faquant/simulated_flash_attention.py:592-619
@@ -96,6 +99,18 @@ int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_
                      const float* key_offset, int64_t off_sh, const float* smooth, int64_t smooth_sh,
                      int smooth_divide, int hadamard, int round_dtype, void* rotated, void* y, int64_t yb,
                      int64_t yh, int64_t yl, int levels, faq_stream_t stream);
+
+/*
+ * Activation prologue of a W4A4 Linear over x [rows, cols] (contiguous, dtype for input and
+ * output): x * dtype(col_scale) in dtype (col_scale optional, fp32 [cols]), then an optional
+ * per-block fp32 Hadamard of size `hadamard` (power of two <= 512, 0 = none) cast back to
+ * dtype, then the HiF4 QDQ with `levels` (0 = none) in groups of 64.  Replaces the
+ * input_scale / online_hadamard / fake_quantize steps of FakeQuantLinear.forward
+ * (src/faquant/quantization.py:204-276) and the input QDQ of HiF4Linear
+ * (src/faquant/wan22_hif4.py:81-92).
+ */
+int faq_act_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const float* col_scale,
+                     int hadamard, int levels, faq_stream_t stream);
 
 /*
  * V operand: x [B, H, L, 128] (strides sb, sh, sl), HiF4 QDQ with `levels` (0 = none),

@@ -37,8 +37,8 @@ def lib():
 def test_header_lists_the_entry_points():
     names = declared()
     assert names == sorted(
-        ["faq_last_error", "faq_version", "faq_hif4_qdq_rows", "faq_hadamard_rows", "faq_operand_prep",
-         "faq_operand_prep_vt", "faq_attention_fwd"]
+        ["faq_last_error", "faq_version", "faq_hif4_qdq_rows", "faq_hadamard_rows", "faq_act_qdq_rows",
+         "faq_operand_prep", "faq_operand_prep_vt", "faq_attention_fwd"]
     )
 
 
@@ -63,6 +63,11 @@ def test_validation_statuses_without_device_work(lib):
     assert "123, 12 or 13" in lib.faq_last_error().decode()
     assert lib.faq_hadamard_rows(p16, p16, 1, 24, 3, 0, 0, None) == _lib.EINVAL
     assert "power of two" in lib.faq_last_error().decode()
+    assert lib.faq_act_qdq_rows(p16, p16, 1, 96, 1, None, 64, 123, None) == _lib.EINVAL
+    assert "divisible by power-of-two block_size=64" in lib.faq_last_error().decode()
+    assert lib.faq_act_qdq_rows(p16, p16, 1, 64, 1, None, 0, 99, None) == _lib.EINVAL
+    assert "123, 12 or 13" in lib.faq_last_error().decode()
+    assert lib.faq_act_qdq_rows(p16, p16, 1, 12, 1, None, 0, 123, None) == _lib.EUNSUP
     assert lib.faq_operand_prep(p16, 1, 128, 128, 128, 1, 1, 1, None, 0, None, 0, 0, 96, 1, None, p16, 128, 128, 128,
                                 123, None) == _lib.EUNSUP
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
