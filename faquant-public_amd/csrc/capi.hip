@@ -93,6 +93,17 @@ void launch_attn_lv(const faq::AttnArgs& a, int quant_p, int same, dim3 grid, hi
   else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, false, false>), grid, dim3(512), 0, st, a);
 }
 
+// fp32(sqrt(n)), its fp32 reciprocal and whether it is a power of two (n = 4^k)
+faq::SqrtDiv sqrt_div(int n) {
+  faq::SqrtDiv d{};
+  d.d = static_cast<float>(std::sqrt(static_cast<double>(n > 0 ? n : 1)));
+  d.r = 1.0f / d.d;
+  int k = 0;
+  while ((1 << k) < n) ++k;
+  d.pow2 = (n > 0 && (1 << k) == n && k % 2 == 0) ? 1 : 0;
+  return d;
+}
+
 }  // namespace
 
 extern "C" {
@@ -144,7 +155,7 @@ int faq_hadamard_rows(const void* x, void* y, int64_t rows, int64_t cols, int bl
   if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype)) return fail(FAQ_EINVAL, "faq_hadamard_rows: bad dtype");
   if (!aligned16(x) || !aligned16(y)) return fail(FAQ_EINVAL, "faq_hadamard_rows: pointers must be 16-byte aligned");
   if (rows == 0) return FAQ_OK;
-  faq::HadamardRowsArgs a{x, y, rows, cols, block, static_cast<float>(std::sqrt(static_cast<double>(block)))};
+  faq::HadamardRowsArgs a{x, y, rows, cols, block, sqrt_div(block)};
   const int64_t threads = rows * (cols / 8);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (in_dtype == FAQ_F32) launch_hadamard_in<float>(a, out_dtype, threads, st);
@@ -171,8 +182,7 @@ int faq_act_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dty
   if (cols % 8) return fail(FAQ_EUNSUP, "faq_act_qdq_rows: row width must be a multiple of 8");
   if (!aligned16(x) || !aligned16(y)) return fail(FAQ_EINVAL, "faq_act_qdq_rows: pointers must be 16-byte aligned");
   if (rows == 0) return FAQ_OK;
-  faq::ActQdqArgs a{x, y, rows, cols, col_scale, hadamard,
-                    static_cast<float>(std::sqrt(static_cast<double>(hadamard ? hadamard : 1))), levels != 0};
+  faq::ActQdqArgs a{x, y, rows, cols, col_scale, hadamard, sqrt_div(hadamard), levels != 0};
   const int64_t threads = rows * ((cols + 63) / 64) * 8;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == FAQ_F32) launch_act<float>(a, levels, threads, st);
@@ -211,7 +221,7 @@ int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_
   a.smooth_sh = smooth_sh;
   a.smooth_divide = smooth_divide;
   a.hadamard = hadamard;
-  a.sqrt_n = hadamard ? static_cast<float>(std::sqrt(static_cast<double>(hadamard))) : 1.0f;
+  a.div = sqrt_div(hadamard);
   a.rotated = rotated;
   a.y = y;
   a.yb = yb;

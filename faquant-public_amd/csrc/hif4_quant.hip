@@ -83,14 +83,51 @@ struct Io<__half> {
   }
 };
 
-__device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
+// Value of lane l ^ M, as VALU lane moves instead of LDS permutes: DPP quad_perm for
+// M = 1, 2; row_half_mirror (l ^ 7) then quad_perm [3,2,1,0] (l ^ 3) for M = 4;
+// row_mirror (l ^ 15) then row_half_mirror for M = 8; v_permlane16_swap /
+// v_permlane32_swap of a register with itself for M = 16, 32 (results 0 / 1 are the
+// lower / upper lane's copy).
+template <int M>
+__device__ __forceinline__ int lane_xor(int u) {
+  if constexpr (M == 1) {
+    return __builtin_amdgcn_mov_dpp(u, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (M == 2) {
+    return __builtin_amdgcn_mov_dpp(u, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (M == 4) {
+    const int h = __builtin_amdgcn_mov_dpp(u, 0x141, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(h, 0x1B, 0xF, 0xF, false);
+  } else if constexpr (M == 8) {
+    const int h = __builtin_amdgcn_mov_dpp(u, 0x140, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(h, 0x141, 0xF, 0xF, false);
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return (threadIdx.x & 16) ? static_cast<int>(r[0]) : static_cast<int>(r[1]);
+  } else {
+    static_assert(M == 32, "lane_xor: M must be a power of two <= 32");
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return (threadIdx.x & 32) ? static_cast<int>(r[0]) : static_cast<int>(r[1]);
+  }
+}
 
-// Block maximum over the 8 lanes holding one 64-value group.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  return __int_as_float(lane_xor<M>(__float_as_int(v)));
+}
+
+template <int M>
+struct LaneMask {
+  static constexpr int value = M;
+};
+
+// Block maximum over the 8 lanes holding one 64-value group of non-negative values
+// (integer max of the bit patterns: no float canonicalization of the lane moves).
 __device__ __forceinline__ float group_max8(float v) {
-  v = xor_max(v, 1);
-  v = xor_max(v, 2);
-  v = xor_max(v, 4);
-  return v;
+  int u = __float_as_int(v);
+  u = max(u, lane_xor<1>(u));
+  u = max(u, lane_xor<2>(u));
+  u = max(u, lane_xor<4>(u));
+  return __int_as_float(u);
 }
 
 // HiF4 QDQ of the 8 values a lane owns (signed, |x| based).  Lanes 8j..8j+7 must hold
@@ -104,9 +141,9 @@ __device__ __forceinline__ void qdq8(float* v, float* s_out = nullptr, float* re
   int nan = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) nan |= v[i] != v[i];
-  nan = __shfl_xor(nan, 1, 64) | nan;
-  nan = __shfl_xor(nan, 2, 64) | nan;
-  nan = __shfl_xor(nan, 4, 64) | nan;
+  nan = lane_xor<1>(nan) | nan;
+  nan = lane_xor<2>(nan) | nan;
+  nan = lane_xor<4>(nan) | nan;
   const float m1 = group_max8(fmaxf(m3a, m3b));
   float s, rec;
   hif4_scale<LV>(m1, s, rec);
@@ -204,12 +241,12 @@ __global__ __launch_bounds__(256) void qdq_rows_kernel(QdqRowsArgs a) {
     uint32_t b2 = static_cast<uint32_t>(e2) << part;
     uint32_t b3 = (static_cast<uint32_t>(e3a) | (static_cast<uint32_t>(e3b) << 1)) << (2 * part);
     // (reductions run on live lanes only; a group's 8 lanes are all live or all dead)
-    b2 |= __shfl_xor(b2, 1, 8);
-    b2 |= __shfl_xor(b2, 2, 8);
-    b2 |= __shfl_xor(b2, 4, 8);
-    b3 |= __shfl_xor(b3, 1, 8);
-    b3 |= __shfl_xor(b3, 2, 8);
-    b3 |= __shfl_xor(b3, 4, 8);
+    b2 |= static_cast<uint32_t>(lane_xor<1>(static_cast<int>(b2)));
+    b2 |= static_cast<uint32_t>(lane_xor<2>(static_cast<int>(b2)));
+    b2 |= static_cast<uint32_t>(lane_xor<4>(static_cast<int>(b2)));
+    b3 |= static_cast<uint32_t>(lane_xor<1>(static_cast<int>(b3)));
+    b3 |= static_cast<uint32_t>(lane_xor<2>(static_cast<int>(b3)));
+    b3 |= static_cast<uint32_t>(lane_xor<4>(static_cast<int>(b3)));
     if (part == 0) {
       if (a.lv2_bits) a.lv2_bits[gi] = static_cast<uint8_t>(b2);
       if (a.lv3_bits) a.lv3_bits[gi] = static_cast<uint16_t>(b3);
@@ -243,14 +280,60 @@ __device__ __forceinline__ void fwht8_lanes(float* v, int n) {
       }
     }
   }
-  for (int m = 1; m * 8 < n; m <<= 1) {
+  auto stage = [&](auto m_tag) {
+    constexpr int m = decltype(m_tag)::value;
+    if (m * 8 >= n) return;
     const bool upper = (threadIdx.x & m) != 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float other = __shfl_xor(v[i], m, 64);
+      const float other = lane_xor<m>(v[i]);
       v[i] = upper ? other - v[i] : v[i] + other;
     }
+  };
+  stage(LaneMask<1>{});
+  stage(LaneMask<2>{});
+  stage(LaneMask<4>{});
+  stage(LaneMask<8>{});
+  stage(LaneMask<16>{});
+  stage(LaneMask<32>{});
+}
+
+// Division by d = fp32(sqrt(n)) with the result of the IEEE division x / d (the reference
+// divides by math.sqrt(n), rotation.py:28).  For square n the divisor is a power of two
+// and x * (1/d) is exact.  Otherwise q = x r (r = fp32(1/d)), e = fma(-q, d, x) (the exact
+// remainder) and fma(e, r, q) equal x / d for every fp32 x whose exponent field lies in
+// [22, 254] (checked exhaustively for n = 2, 8, 32, 128, 512: tests/fp_div_check.c); a
+// lane holding a smaller magnitude (zeros included), an infinity or a NaN takes the IEEE
+// division for its 8 values.
+struct SqrtDiv {
+  float d;   // fp32(sqrt(n))
+  float r;   // fp32(1 / d)
+  int pow2;  // d is a power of two
+};
+
+__device__ __forceinline__ void div_sqrt_n(float* v, const SqrtDiv& s) {
+  if (s.pow2) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] * s.r;
+    return;
   }
+  float y[8];
+  float lo = fabsf(v[0]), hi = fabsf(v[0]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float q = v[i] * s.r;
+    const float e = __builtin_fmaf(-q, s.d, v[i]);
+    y[i] = __builtin_fmaf(e, s.r, q);
+    lo = fminf(lo, fabsf(v[i]));
+    hi = fmaxf(hi, fabsf(v[i]));
+  }
+  // exponent field >= 22 is |x| >= 2^-105; a NaN fails the comparisons
+  if (!(lo >= 0x1p-105f && hi <= 3.40282347e38f)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = v[i] / s.d;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = y[i];
 }
 
 struct HadamardRowsArgs {
@@ -259,7 +342,7 @@ struct HadamardRowsArgs {
   int64_t rows;
   int64_t cols;   // multiple of n and of 8
   int n;          // block size, power of two in [2, 512]
-  float sqrt_n;   // fp32(sqrt(n)); the transform divides by it (true division)
+  SqrtDiv div;    // division by fp32(sqrt(n))
 };
 
 template <typename Tin, typename Tout>
@@ -277,8 +360,7 @@ __global__ __launch_bounds__(256) void hadamard_rows_kernel(HadamardRowsArgs a) 
     for (int i = 0; i < 8; ++i) v[i] = 0.0f;
   }
   fwht8_lanes(v, a.n);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = v[i] / a.sqrt_n;
+  div_sqrt_n(v, a.div);
   if (live) Io<Tout>::store8(static_cast<Tout*>(a.y) + row * a.cols + c0, v);
 }
 
@@ -291,7 +373,7 @@ struct ActQdqArgs {
   int64_t cols;           // multiple of 8; of 64 and of n when n > 0
   const float* col_scale; // optional per-column input scale, [cols]
   int n;                  // 0, or the block Hadamard size (power of two in [2, 512])
-  float sqrt_n;
+  SqrtDiv div;            // division by fp32(sqrt(n))
   int quant;              // 1: HiF4 QDQ
 };
 
@@ -326,8 +408,9 @@ __global__ __launch_bounds__(256) void act_qdq_rows_kernel(ActQdqArgs a) {
   }
   if (a.n) {
     fwht8_lanes(v, a.n);
+    div_sqrt_n(v, a.div);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(v[i] / a.sqrt_n);
+    for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(v[i]);
   }
   if (a.quant) qdq8<LV>(v);
   if (have) Io<T>::store8(y + c0, v);
@@ -345,7 +428,7 @@ struct OperandPrepArgs {
   int64_t smooth_sh;
   int smooth_divide;             // 1 for keys (k / s), 0 for queries (q * s)
   int hadamard;                  // 0, 64 or 128
-  float sqrt_n;
+  SqrtDiv div;                   // division by fp32(sqrt(hadamard))
   void* rotated;                 // optional: the rotated operand in the round dtype, [B, H, L, 128] contiguous
   void* y;                       // bf16 output [B, H, L, 128] with strides below
   int64_t yb, yh, yl;
@@ -384,8 +467,7 @@ __global__ __launch_bounds__(256) void operand_prep_kernel(OperandPrepArgs a) {
   }
   if (a.hadamard) {
     fwht8_lanes(v, a.hadamard);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = v[i] / a.sqrt_n;
+    div_sqrt_n(v, a.div);
   }
   // the single cast back to the operand dtype (qwen3.py:129-130)
 #pragma unroll

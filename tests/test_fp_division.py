@@ -1,0 +1,36 @@
+"""The Hadamard kernels replace the reference's true division by sqrt(n) (rotation.py:28)
+with q = x r, e = fma(-q, d, x), fma(e, r, q) on the range where that is exact, and an
+IEEE division elsewhere.  tests/fp_div_check.c verifies the identity (sampled here over
+every binade; run it with a second argument for all 2^32 inputs)."""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def checker(tmp_path_factory):
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    exe = str(tmp_path_factory.mktemp("fpdiv") / "fp_div_check")
+    flags = ["-O2", "-ffp-contract=off"]
+    probe = subprocess.run(["gcc", "-fopenmp", "-x", "c", "-", "-o", os.devnull], input="int main(){return 0;}",
+                           capture_output=True, text=True)
+    if probe.returncode == 0:
+        flags.append("-fopenmp")
+    subprocess.run(["gcc", *flags, os.path.join(HERE, "fp_div_check.c"), "-o", exe, "-lm"], check=True)
+    return exe
+
+
+@pytest.mark.parametrize("n", [2, 8, 32, 128, 512])
+def test_fma_division_equals_ieee_division(checker, n):
+    out = subprocess.run([checker, str(n)], capture_output=True, text=True, timeout=600)
+    print(out.stdout.strip())
+    assert out.returncode == 0, out.stdout
+    assert "mismatches 0" in out.stdout
