@@ -164,6 +164,25 @@ int faq_hadamard_rows(const void* x, void* y, int64_t rows, int64_t cols, int bl
   return check_launch("faq_hadamard_rows");
 }
 
+int faq_hif4_unpack_rows(const uint8_t* codes, const uint8_t* scale_byte, const uint8_t* lv2_bits,
+                         const uint16_t* lv3_bits, int64_t rows, int64_t cols, int out_dtype, void* y,
+                         faq_stream_t stream) {
+  if (!codes || !scale_byte || !lv2_bits || !lv3_bits || !y) return fail(FAQ_EINVAL, "faq_hif4_unpack_rows: null pointer");
+  if (rows < 0) return fail(FAQ_EINVAL, "faq_hif4_unpack_rows: negative size");
+  if (cols <= 0 || cols % 64) return fail(FAQ_EINVAL, "HiF4 packing needs a last axis that is a multiple of 64");
+  if (!valid_dtype(out_dtype)) return fail(FAQ_EINVAL, "faq_hif4_unpack_rows: bad dtype");
+  if (!aligned16(y) || reinterpret_cast<uintptr_t>(codes) % 4)
+    return fail(FAQ_EINVAL, "faq_hif4_unpack_rows: misaligned codes or output");
+  if (rows == 0) return FAQ_OK;
+  faq::UnpackArgs a{codes, scale_byte, lv2_bits, lv3_bits, y, rows, cols};
+  const dim3 grid(grid_for(rows * (cols / 8)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (out_dtype == FAQ_F32) hipLaunchKernelGGL((faq::unpack_rows_kernel<float>), grid, dim3(256), 0, st, a);
+  else if (out_dtype == FAQ_BF16) hipLaunchKernelGGL((faq::unpack_rows_kernel<__hip_bfloat16>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((faq::unpack_rows_kernel<__half>), grid, dim3(256), 0, st, a);
+  return check_launch("faq_hif4_unpack_rows");
+}
+
 int faq_act_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const float* col_scale,
                      int hadamard, int levels, faq_stream_t stream) {
   if (!x || !y) return fail(FAQ_EINVAL, "faq_act_qdq_rows: null input or output");

@@ -260,6 +260,48 @@ __global__ __launch_bounds__(256) void qdq_rows_kernel(QdqRowsArgs a) {
 }
 
 
+// ------------------------------------------------------------------ packed decode
+
+struct UnpackArgs {
+  const uint8_t* codes;        // [rows, cols / 2]: value 2i in the low nibble of byte i
+  const uint8_t* scale_byte;   // [rows, groups]: ((e + 48) << 2) | m, scale 2^e (1 + m/4)
+  const uint8_t* lv2_bits;     // [rows, groups]: bit j = level-2 exponent of 8-group j
+  const uint16_t* lv3_bits;    // [rows, groups]: bit j = level-3 exponent of 4-group j
+  void* y;                     // [rows, cols]
+  int64_t rows;
+  int64_t cols;                // multiple of 64
+};
+
+// Values of the packed HiF4 storage view (hif4.py:67-79 content): a code c (bit 3 sign,
+// bits 0-2 magnitude) in 4-group j of 8-group i is +-(c & 7)/4 * s * 2^(lv2_i + lv3_j), exact
+// in fp32 as (c & 7)(4 + m) 2^(e + k - 4).  One lane per 8 values (one 8-group).
+template <typename T>
+__global__ __launch_bounds__(256) void unpack_rows_kernel(UnpackArgs a) {
+  const int64_t groups = a.cols / 64;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= a.rows * groups * 8) return;
+  const int64_t gi = tid >> 3;  // (row, group)
+  const int part = static_cast<int>(tid & 7);
+  const int64_t row = gi / groups;
+  const int64_t c0 = (gi % groups) * 64 + part * 8;
+  const uint32_t word = *reinterpret_cast<const uint32_t*>(a.codes + row * (a.cols / 2) + c0 / 2);
+  const uint32_t sb = a.scale_byte[gi];
+  const int e = static_cast<int>(sb >> 2) - 48;
+  const int m = static_cast<int>(sb & 3u);
+  const int lv2 = (a.lv2_bits[gi] >> part) & 1;
+  const int lv3a = (a.lv3_bits[gi] >> (2 * part)) & 1;
+  const int lv3b = (a.lv3_bits[gi] >> (2 * part + 1)) & 1;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t c = (word >> (4 * i)) & 0xFu;
+    const int k = lv2 + (i < 4 ? lv3a : lv3b);
+    const float mag = ldexpf(static_cast<float>((c & 7u) * static_cast<uint32_t>(4 + m)), e + k - 4);
+    v[i] = (c & 8u) ? -mag : mag;
+  }
+  Io<T>::store8(static_cast<T*>(a.y) + row * a.cols + c0, v);
+}
+
 // ------------------------------------------------------------------ Hadamard
 
 // In-register stages of stride 1, 2, 4 (8 consecutive values per lane), then

@@ -75,6 +75,25 @@ def qdq_rows(
     return y, extra
 
 
+def unpack_rows(codes, scale_byte, lv2_bits, lv3_bits, cols: int, dtype: torch.dtype) -> torch.Tensor:
+    """Packed HiF4 rows -> values [rows, cols] in ``dtype`` (exact)."""
+    _lib.require_device(codes, scale_byte, lv2_bits, lv3_bits)
+    lib = _lib.load()
+    if cols % 64:
+        raise ValueError("HiF4 packing needs a last axis that is a multiple of 64")
+    c = codes.contiguous()
+    rows = c.numel() // (cols // 2) if cols else 0
+    y = torch.empty((rows, cols), device=codes.device, dtype=dtype)
+    parts = [t.contiguous() for t in (scale_byte, lv2_bits, lv3_bits)]
+    _lib.check(
+        lib.faq_hif4_unpack_rows(
+            c.data_ptr(), parts[0].data_ptr(), parts[1].data_ptr(), parts[2].data_ptr(), rows, cols,
+            _lib.dtype_code(dtype), y.data_ptr(), _lib.stream_ptr(codes.device),
+        )
+    )
+    return y
+
+
 def hadamard_rows(x: torch.Tensor, block: int, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """Block Hadamard over the last axis in fp32, rounded once to ``out_dtype``."""
     _lib.require_device(x)

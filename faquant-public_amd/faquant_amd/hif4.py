@@ -164,21 +164,8 @@ def encode_hif4(x: torch.Tensor, *, levels: str | None = None) -> PackedHiF4:
 
 
 def decode_hif4(packed: PackedHiF4, dtype: torch.dtype = torch.float32) -> torch.Tensor:
-    """Values of a PackedHiF4 (exact), computed with tensor ops on the codes' device."""
+    """Values of a PackedHiF4 (exact): the HIP unpack kernel over its rows."""
     codes = packed.codes
-    lo = (codes & 0xF).to(torch.int32)
-    hi = (codes >> 4).to(torch.int32)
-    nib = torch.stack((lo, hi), dim=-1).reshape(*codes.shape[:-1], -1)
-    groups = nib.reshape(*nib.shape[:-1], -1, HIF4_BLOCK_SIZE)
-    sb = packed.scale_byte.to(torch.int32)
-    e = (sb >> 2) - 48
-    m = sb & 3
-    scale = torch.ldexp(1.0 + m.float() / 4.0, e.float())
-    bit8 = torch.arange(8, device=codes.device)
-    bit16 = torch.arange(16, device=codes.device)
-    lv2 = (packed.lv2_bits.to(torch.int32)[..., None] >> bit8) & 1
-    lv3 = (packed.lv3_bits.to(torch.int32)[..., None] >> bit16) & 1
-    k = lv2.repeat_interleave(8, dim=-1) + lv3.repeat_interleave(4, dim=-1)
-    mag = (groups & 7).float() / 4.0 * scale[..., None] * torch.exp2(k.float())
-    val = torch.where((groups >> 3) & 1 == 1, -mag, mag)
-    return val.reshape(nib.shape).to(dtype)
+    lead = tuple(codes.shape[:-1])
+    cols = codes.shape[-1] * 2
+    return _ops.unpack_rows(codes, packed.scale_byte, packed.lv2_bits, packed.lv3_bits, cols, dtype).view(*lead, cols)

@@ -19,6 +19,8 @@
  *   faq_hadamard_rows     src/faquant/rotation.py:14-29 hadamard_transform,
  *                         rotation.py:117-135 chunked_block_hadamard_transform,
  *                         src/faquant/wan22_attention.py:186-192 rotate_heads
+ *   faq_hif4_unpack_rows  src/faquant/hif4.py:222-271 expand_hif4_parameters +
+ *                         quantize_hif4_with_parameters, from the packed 4.5-bit view
  *   faq_act_qdq_rows      src/faquant/quantization.py:204-276 FakeQuantLinear.forward (input
  *                         scale, online block Hadamard, HiF4 input QDQ) and
  *                         src/faquant/wan22_hif4.py:81-92 HiF4Linear.forward (input QDQ)
@@ -99,6 +101,18 @@ int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_
                      const float* key_offset, int64_t off_sh, const float* smooth, int64_t smooth_sh,
                      int smooth_divide, int hadamard, int round_dtype, void* rotated, void* y, int64_t yb,
                      int64_t yh, int64_t yl, int levels, faq_stream_t stream);
+
+/*
+ * Values of the packed HiF4 storage view written by faq_hif4_qdq_rows (4-bit codes, low
+ * nibble = even element, bit 3 sign; one E6M2 byte ((e + 48) << 2) | m, 8 level-2 bits and
+ * 16 level-3 bits per 64 values: the content of CompactHiF4Parameters, hif4.py:67-79, and
+ * the per-value multipliers of expand_hif4_parameters, hif4.py:222-243).  Exact: decodes
+ * to the fake-quantized values.  cols must be a multiple of 64; y is [rows, cols] in
+ * out_dtype.
+ */
+int faq_hif4_unpack_rows(const uint8_t* codes, const uint8_t* scale_byte, const uint8_t* lv2_bits,
+                         const uint16_t* lv3_bits, int64_t rows, int64_t cols, int out_dtype, void* y,
+                         faq_stream_t stream);
 
 /*
  * Activation prologue of a W4A4 Linear over x [rows, cols] (contiguous, dtype for input and

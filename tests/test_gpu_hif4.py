@@ -122,6 +122,27 @@ def test_packed_encoding_matches_oracle(dev, levels):
     np.testing.assert_array_equal(bits(dec), bits(fake_quantize_hif4(to_dev(x, dev), levels=levels)))
 
 
+def test_packed_storage_round_trip_extremes_and_size(dev):
+    """Packed HiF4 (4.5 bits per value) decodes exactly, to fp32 and bf16, over the whole
+    E6M2 scale range.  (HiF4 QDQ is not idempotent: the group maximum of a quantized
+    group can round to another E6M2 scale, so a cache is packed from the source values.)"""
+    from faquant_amd.hif4 import decode_hif4, encode_hif4, fake_quantize_hif4
+
+    g = np.random.Generator(np.random.PCG64(10))
+    x = g.standard_normal((3, 5, 512)).astype(np.float32)
+    x *= np.exp2(g.integers(-60, 20, size=(3, 5, 8, 1)).astype(np.float32)).repeat(64, axis=-1).reshape(3, 5, 512)
+    x[0, 0, :64] = 0.0
+    xt = to_dev(x, dev)
+    packed = encode_hif4(xt, levels="123")
+    nbytes = sum(t.numel() * t.element_size() for t in (packed.codes, packed.scale_byte, packed.lv2_bits,
+                                                         packed.lv3_bits))
+    assert nbytes * 8 == 4.5 * x.size
+    q = fake_quantize_hif4(xt, levels="123")
+    np.testing.assert_array_equal(bits(decode_hif4(packed)), bits(q))
+    dec16 = decode_hif4(packed, torch.bfloat16)
+    assert dec16.dtype == torch.bfloat16 and torch.equal(dec16.float(), q)
+
+
 def test_qdq_rows_128_matches_oracle(dev):
     from faquant_amd.wan22_attention import qdq_rows_128
 
