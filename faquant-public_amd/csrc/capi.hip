@@ -1,6 +1,7 @@
 // C ABI of the HiF4 attention path (declarations and contracts: include/faquant_amd.h).
 // Validates arguments on the host, selects the kernel instantiation, launches it on the
 // caller's stream and reports errors through a thread-local message.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -102,6 +103,98 @@ faq::SqrtDiv sqrt_div(int n) {
   while ((1 << k) < n) ++k;
   d.pow2 = (n > 0 && (1 << k) == n && k % 2 == 0) ? 1 : 0;
   return d;
+}
+
+
+// Validation and kernel arguments shared by the one-pass and split-key entry points.
+// Returns FAQ_OK with `a`/`grid` filled, 1 when there is nothing to launch, or a status.
+int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
+                    int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
+                    int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl, int B,
+                    int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels,
+                    float* row_den, int out_levels, faq::AttnArgs& a, dim3& grid) {
+  if (!q || !k || !vt || !o) return fail(FAQ_EINVAL, "%s: null operand", who);
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "%s: bad sizes", who);
+  if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
+  if (Lpad % 128 || Lpad < Lk) return fail(FAQ_EINVAL, "%s: Lpad must be a multiple of 128 >= Lk", who);
+  if (o_dtype != FAQ_F32 && o_dtype != FAQ_BF16) return fail(FAQ_EUNSUP, "%s: output must be fp32 or bf16", who);
+  if (quant_p && !valid_levels(p_levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", p_levels);
+  if (out_levels != 0 && !valid_levels(out_levels))
+    return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", out_levels);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(vt) || !aligned16(o))
+    return fail(FAQ_EINVAL, "%s: pointers must be 16-byte aligned", who);
+  if ((q_sb | q_sh | q_sl | k_sb | k_sh | k_sl | v_sb | v_sh | v_sd) & 7)
+    return fail(FAQ_EINVAL, "%s: operand strides must be multiples of 8 elements", who);
+  if ((o_sb | o_sh | o_sl) & 3) return fail(FAQ_EINVAL, "%s: output strides must be multiples of 4 elements", who);
+  if (v_sd < Lpad) return fail(FAQ_EINVAL, "%s: v_sd must be >= Lpad", who);
+  // the kernel addresses one head's K and V^T with 32-bit byte offsets
+  if (k_sl > (int64_t(1) << 22) || v_sd > (int64_t(1) << 22) ||
+      (static_cast<int64_t>(Lk) * k_sl + 128) * 2 >= (int64_t(1) << 32) || 128 * v_sd * 2 >= (int64_t(1) << 32))
+    return fail(FAQ_EUNSUP, "%s: one head's K or V^T spans more than 4 GiB of addresses", who);
+  if (B == 0 || Lq == 0) return 1;
+  const int G = Hq / Hkv;
+  // eight waves of 32 query rows per workgroup; hpw query heads of one KV head share it
+  const int hpw = (G % 8 == 0) ? 8 : (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+  const int pos_per_wg = 32 * (8 / hpw);
+  a = faq::AttnArgs{};
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_sl = q_sl;
+  a.k = k;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_sl = k_sl;
+  a.vt = vt;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.v_sd = v_sd;
+  a.o = o;
+  a.o_sb = o_sb;
+  a.o_sh = o_sh;
+  a.o_sl = o_sl;
+  a.o_f32 = o_dtype == FAQ_F32;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.Lq = Lq;
+  a.Lk = Lk;
+  a.causal = causal != 0;
+  a.c1 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  a.hpw = hpw;
+  a.n_pblocks = (Lq + pos_per_wg - 1) / pos_per_wg;
+  a.row_den = row_den;
+  a.out_levels = out_levels;
+  a.rows_total = B * Hq * Lq;
+  grid = dim3(static_cast<unsigned>(B * Hkv * (G / hpw)), static_cast<unsigned>(a.n_pblocks));
+  return FAQ_OK;
+}
+
+void launch_attention(const faq::AttnArgs& a, int quant_p, int p_levels, int norm_same, dim3 grid, hipStream_t st) {
+  const int lv = quant_p ? p_levels : 123;
+  if (lv == 12) launch_attn_lv<12>(a, quant_p, norm_same, grid, st);
+  else if (lv == 13) launch_attn_lv<13>(a, quant_p, norm_same, grid, st);
+  else launch_attn_lv<123>(a, quant_p, norm_same, grid, st);
+}
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+struct SplitLayout {
+  int64_t mx, m_start, part_o, part_lm, total;  // byte offsets and size
+  int ntiles, tiles_per_split;
+};
+
+SplitLayout split_layout(int B, int Hq, int Lq, int Lk, int nsplit) {
+  SplitLayout s{};
+  const int64_t rows = static_cast<int64_t>(B) * Hq * Lq;
+  s.ntiles = (Lk + 127) / 128;
+  s.tiles_per_split = nsplit > 0 ? (s.ntiles + nsplit - 1) / nsplit : 0;
+  s.mx = 0;
+  s.m_start = align256(rows * std::max(s.ntiles, 1) * 4);
+  s.part_o = s.m_start + align256(rows * nsplit * 4);
+  s.part_lm = s.part_o + align256(rows * nsplit * 128 * 4);
+  s.total = s.part_lm + align256(rows * nsplit * 2 * 4);
+  return s;
 }
 
 }  // namespace
@@ -281,66 +374,63 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
                       int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq,
                       int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels, int norm_same,
                       float* row_den, int out_levels, faq_stream_t stream) {
-  if (!q || !k || !vt || !o) return fail(FAQ_EINVAL, "faq_attention_fwd: null operand");
-  if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "faq_attention_fwd: bad sizes");
-  if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
-  if (Lpad % 128 || Lpad < Lk) return fail(FAQ_EINVAL, "faq_attention_fwd: Lpad must be a multiple of 128 >= Lk");
-  if (o_dtype != FAQ_F32 && o_dtype != FAQ_BF16) return fail(FAQ_EUNSUP, "faq_attention_fwd: output must be fp32 or bf16");
-  if (quant_p && !valid_levels(p_levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", p_levels);
-  if (out_levels != 0 && !valid_levels(out_levels))
-    return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", out_levels);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(vt) || !aligned16(o))
-    return fail(FAQ_EINVAL, "faq_attention_fwd: pointers must be 16-byte aligned");
-  if ((q_sb | q_sh | q_sl | k_sb | k_sh | k_sl | v_sb | v_sh | v_sd) & 7)
-    return fail(FAQ_EINVAL, "faq_attention_fwd: operand strides must be multiples of 8 elements");
-  if (o_dtype == FAQ_BF16 ? ((o_sb | o_sh | o_sl) & 3) : ((o_sb | o_sh | o_sl) & 3))
-    return fail(FAQ_EINVAL, "faq_attention_fwd: output strides must be multiples of 4 elements");
-  if (v_sd < Lpad) return fail(FAQ_EINVAL, "faq_attention_fwd: v_sd must be >= Lpad");
-  // the kernel addresses one head's K and V^T with 32-bit byte offsets
-  if (k_sl > (int64_t(1) << 22) || v_sd > (int64_t(1) << 22) ||
-      (static_cast<int64_t>(Lk) * k_sl + 128) * 2 >= (int64_t(1) << 32) || 128 * v_sd * 2 >= (int64_t(1) << 32))
-    return fail(FAQ_EUNSUP, "faq_attention_fwd: one head's K or V^T spans more than 4 GiB of addresses");
-  if (B == 0 || Lq == 0) return FAQ_OK;
-  const int G = Hq / Hkv;
-  // eight waves of 32 query rows per workgroup; hpw query heads of one KV head share it
-  const int hpw = (G % 8 == 0) ? 8 : (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
-  const int pos_per_wg = 32 * (8 / hpw);
-  faq::AttnArgs a{};
-  a.q = q;
-  a.q_sb = q_sb;
-  a.q_sh = q_sh;
-  a.q_sl = q_sl;
-  a.k = k;
-  a.k_sb = k_sb;
-  a.k_sh = k_sh;
-  a.k_sl = k_sl;
-  a.vt = vt;
-  a.v_sb = v_sb;
-  a.v_sh = v_sh;
-  a.v_sd = v_sd;
-  a.o = o;
-  a.o_sb = o_sb;
-  a.o_sh = o_sh;
-  a.o_sl = o_sl;
-  a.o_f32 = o_dtype == FAQ_F32;
-  a.B = B;
-  a.Hq = Hq;
-  a.Hkv = Hkv;
-  a.Lq = Lq;
-  a.Lk = Lk;
-  a.causal = causal != 0;
-  a.c1 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
-  a.hpw = hpw;
-  a.n_pblocks = (Lq + pos_per_wg - 1) / pos_per_wg;
-  a.row_den = row_den;
-  a.out_levels = out_levels;
-  const dim3 grid(static_cast<unsigned>(B * Hkv * (G / hpw)), static_cast<unsigned>(a.n_pblocks));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int lv = quant_p ? p_levels : 123;
-  if (lv == 12) launch_attn_lv<12>(a, quant_p, norm_same, grid, st);
-  else if (lv == 13) launch_attn_lv<13>(a, quant_p, norm_same, grid, st);
-  else launch_attn_lv<123>(a, quant_p, norm_same, grid, st);
+  faq::AttnArgs a;
+  dim3 grid;
+  const int rc = attention_setup("faq_attention_fwd", q, q_sb, q_sh, q_sl, k, k_sb, k_sh, k_sl, vt, v_sb, v_sh, v_sd,
+                                 Lpad, o, o_dtype, o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p,
+                                 p_levels, row_den, out_levels, a, grid);
+  if (rc != FAQ_OK) return rc == 1 ? FAQ_OK : rc;
+  launch_attention(a, quant_p, p_levels, norm_same, grid, static_cast<hipStream_t>(stream));
   return check_launch("faq_attention_fwd");
+}
+
+int64_t faq_attention_split_workspace(int B, int Hq, int Lq, int Lk, int nsplit) {
+  if (B < 0 || Hq < 0 || Lq < 0 || Lk < 0 || nsplit < 1) return -1;
+  return split_layout(B, Hq, Lq, Lk, nsplit).total;
+}
+
+int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
+                            int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
+                            int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                            int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p,
+                            int p_levels, int norm_same, float* row_den, int nsplit, void* workspace,
+                            int64_t workspace_bytes, faq_stream_t stream) {
+  if (nsplit < 1 || nsplit > 4096) return fail(FAQ_EINVAL, "faq_attention_fwd_split: nsplit must be in [1, 4096]");
+  faq::AttnArgs a;
+  dim3 grid;
+  const int rc = attention_setup("faq_attention_fwd_split", q, q_sb, q_sh, q_sl, k, k_sb, k_sh, k_sl, vt, v_sb, v_sh,
+                                 v_sd, Lpad, o, o_dtype, o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p,
+                                 p_levels, row_den, 0, a, grid);
+  if (rc != FAQ_OK) return rc == 1 ? FAQ_OK : rc;
+  const SplitLayout L = split_layout(B, Hq, Lq, Lk, nsplit);
+  if (!workspace || !aligned16(workspace)) return fail(FAQ_EINVAL, "faq_attention_fwd_split: null or misaligned workspace");
+  if (workspace_bytes < L.total)
+    return fail(FAQ_EINVAL, "faq_attention_fwd_split: workspace of %lld bytes, need %lld",
+                static_cast<long long>(workspace_bytes), static_cast<long long>(L.total));
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  grid.z = static_cast<unsigned>(nsplit);
+  a.tiles_per_split = L.tiles_per_split;
+  // 1. c1-scaled tile maxima of every row
+  faq::AttnArgs am = a;
+  am.mx_out = reinterpret_cast<float*>(ws + L.mx);
+  am.mx_stride = std::max(L.ntiles, 1);
+  launch_attention(am, quant_p, p_levels, norm_same, grid, st);
+  // 2. running maximum before each split
+  faq::SplitScanArgs sa{am.mx_out, am.mx_stride, reinterpret_cast<float*>(ws + L.m_start), a.rows_total, nsplit,
+                        L.tiles_per_split, Lq, Lk, causal != 0};
+  const int64_t scan_threads = static_cast<int64_t>(a.rows_total) * nsplit;
+  hipLaunchKernelGGL(faq::split_scan_kernel, dim3(grid_for(scan_threads)), dim3(256), 0, st, sa);
+  // 3. per-split recurrences from those maxima
+  faq::AttnArgs ap = a;
+  ap.m_start = sa.m_start;
+  ap.part_o = reinterpret_cast<float*>(ws + L.part_o);
+  ap.part_lm = reinterpret_cast<float*>(ws + L.part_lm);
+  launch_attention(ap, quant_p, p_levels, norm_same, grid, st);
+  // 4. combine
+  faq::SplitCombineArgs ca{ap.part_o, ap.part_lm, a.rows_total, nsplit, Hq, Lq, o, o_sb, o_sh, o_sl, a.o_f32, row_den};
+  hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(128), 0, st, ca);
+  return check_launch("faq_attention_fwd_split");
 }
 
 }  // extern "C"

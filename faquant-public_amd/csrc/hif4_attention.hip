@@ -76,6 +76,15 @@ struct AttnArgs {
   int n_pblocks;  // position blocks per head group
   float* row_den;  // optional fp32 [B, Hq, Lq]: final denominator l
   int out_levels;  // 0, or HiF4 levels of a QDQ of each 64-value half of an output row
+  // Split-key passes (key tiles divided among blockIdx.z; 0: one pass over all tiles).
+  // Row r = (b Hq + hq) Lq + pos; rows_total = B Hq Lq.
+  int tiles_per_split;
+  int rows_total;
+  float* mx_out;          // maxima pass: c1-scaled row maximum of each key tile, [rows_total, mx_stride]
+  int mx_stride;
+  const float* m_start;   // partial pass: running maximum before the split, [nsplit, rows_total]
+  float* part_o;          // partial pass: unnormalized O, [nsplit, rows_total, 128]
+  float* part_lm;         // partial pass: (l, running maximum) after the split, [nsplit, rows_total, 2]
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -335,6 +344,10 @@ void attn_fwd_kernel(AttnArgs a) {
 
   const int pos = p0w + n;
   const bool row_live = pos < a.Lq;
+  const int64_t row = (static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos;
+  const int split = static_cast<int>(blockIdx.z);
+  const int t_lo = a.tiles_per_split ? min(ntiles, split * a.tiles_per_split) : 0;
+  const int t_hi = a.tiles_per_split ? min(ntiles, t_lo + a.tiles_per_split) : ntiles;
   bf16x8 qf[8];
   {
     const uint16_t* qp = a.q + b * a.q_sb + hq * a.q_sh + static_cast<int64_t>(row_live ? pos : 0) * a.q_sl + 8 * half;
@@ -351,7 +364,9 @@ void attn_fwd_kernel(AttnArgs a) {
   floatx16 acc[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) acc[mb] = floatx16{};
-  float m_run = -INFINITY;
+  // a partial pass continues the reference's recurrence from the running maximum of the
+  // tiles before its split (sfa:788-806: P of tile t depends on the maximum after tile t)
+  float m_run = (a.m_start && row_live) ? a.m_start[static_cast<int64_t>(split) * a.rows_total + row] : -INFINITY;
   float l_run = 0.0f;
   bf16x2_t ones2;
   {
@@ -413,14 +428,14 @@ void attn_fwd_kernel(AttnArgs a) {
   // PV: V^T row 32 mb + n, piece 8 half + c.
   const int vbyte = kTileBytes + n * (kRowUnits * 16) + half * 128;
 
-  if (ntiles > 0) load_tile(0);
+  if (t_lo < t_hi) load_tile(t_lo);
 
-  for (int t = 0; t < ntiles; ++t) {
+  for (int t = t_lo; t < t_hi; ++t) {
     // tile t has landed for every wave; every wave is done with tile t - 1, whose stage
     // the DMA of tile t + 1 overwrites
     wait_all_memory();
     __syncthreads();
-    if (t + 1 < ntiles) load_tile(t + 1);
+    if (t + 1 < t_hi) load_tile(t + 1);
     const uint8_t* const st = lds + (t & 1) * kStageBytes;
     const uint8_t* const kp = st + kbyte;
     const uint8_t* const vp = st + vbyte;
@@ -472,6 +487,11 @@ void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
     const float mx_row = halves_max(mx);
+    if (a.mx_out) {
+      // maxima pass: the tile's c1-scaled row maximum only
+      if (row_live && half == 0) a.mx_out[row * a.mx_stride + t] = mx_row * a.c1;
+      continue;
+    }
     const float m_new = fmaxf(m_run, mx_row * a.c1);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float nm = -m_use;
@@ -565,7 +585,23 @@ void attn_fwd_kernel(AttnArgs a) {
     l_run += halves_sum(rowsum);
   }
 
-  if (!row_live) return;
+  if (!row_live || a.mx_out) return;
+  if (a.part_o) {
+    // partial pass: unnormalized O^T column of this row, its l and running maximum
+    float* po = a.part_o + (static_cast<int64_t>(split) * a.rows_total + row) * kDim;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<float4*>(po + 32 * mb + 8 * j + 4 * half) =
+            make_float4(acc[mb][4 * j], acc[mb][4 * j + 1], acc[mb][4 * j + 2], acc[mb][4 * j + 3]);
+    if (half == 0) {
+      float* lm = a.part_lm + (static_cast<int64_t>(split) * a.rows_total + row) * 2;
+      lm[0] = l_run;
+      lm[1] = m_run;
+    }
+    return;
+  }
   const float l = l_run;
   const float inv_guard = fmaxf(l, 1.17549435e-38f);
   if (a.row_den && half == 0) a.row_den[(static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos] = l;
@@ -605,6 +641,75 @@ void attn_fwd_kernel(AttnArgs a) {
       }
     }
   }
+}
+
+
+// ---------------------------------------------------------------------------------------
+// Split-key attention (decode and other short grids): after the maxima pass, the running
+// maximum before split j of row r is the maximum of the c1-scaled tile maxima of its first
+// t_lo(j) tiles (-inf if none), restricted to the tiles the row sees.
+struct SplitScanArgs {
+  const float* mx;     // [rows_total, mx_stride]
+  int mx_stride;
+  float* m_start;      // [nsplit, rows_total]
+  int rows_total;
+  int nsplit;
+  int tiles_per_split;
+  int Lq, Lk, causal;
+};
+
+__global__ __launch_bounds__(256) void split_scan_kernel(SplitScanArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<int64_t>(a.rows_total) * a.nsplit) return;
+  const int row = static_cast<int>(i % a.rows_total);
+  const int split = static_cast<int>(i / a.rows_total);
+  const int pos = row % a.Lq;
+  const int kend = a.causal ? min(a.Lk, max(0, pos + a.Lk - a.Lq + 1)) : a.Lk;
+  const int tiles_row = (kend + kKeyTile - 1) / kKeyTile;
+  const int upto = min(tiles_row, split * a.tiles_per_split);
+  float m = -INFINITY;
+  for (int t = 0; t < upto; ++t) m = fmaxf(m, a.mx[static_cast<int64_t>(row) * a.mx_stride + t]);
+  a.m_start[i] = m;
+}
+
+// O = sum_j 2^(m_j - M) O_j / sum_j 2^(m_j - M) l_j with M the row's final running maximum;
+// the per-split recurrences already used the reference's maxima, so only the fp32 order of
+// the O and l sums differs from one pass.
+struct SplitCombineArgs {
+  const float* part_o;   // [nsplit, rows_total, 128]
+  const float* part_lm;  // [nsplit, rows_total, 2]
+  int rows_total, nsplit;
+  int Hq, Lq;
+  void* o;               // [B, Hq, Lq, 128] via strides
+  int64_t o_sb, o_sh, o_sl;
+  int o_f32;
+  float* row_den;        // optional [rows_total]
+};
+
+__global__ __launch_bounds__(128) void split_combine_kernel(SplitCombineArgs a) {
+  const int row = blockIdx.x;
+  const int d = threadIdx.x;
+  float mmax = -INFINITY;
+  for (int j = 0; j < a.nsplit; ++j) mmax = fmaxf(mmax, a.part_lm[(static_cast<int64_t>(j) * a.rows_total + row) * 2 + 1]);
+  float l = 0.0f, acc = 0.0f;
+  if (mmax != -INFINITY) {
+    for (int j = 0; j < a.nsplit; ++j) {
+      const int64_t r = static_cast<int64_t>(j) * a.rows_total + row;
+      const float lj = a.part_lm[r * 2];
+      if (lj == 0.0f) continue;
+      const float w = __builtin_amdgcn_exp2f(a.part_lm[r * 2 + 1] - mmax);
+      l = __builtin_fmaf(w, lj, l);
+      acc = __builtin_fmaf(w, a.part_o[r * kDim + d], acc);
+    }
+  }
+  const int pos = row % a.Lq;
+  const int hq = (row / a.Lq) % a.Hq;
+  const int b = row / (a.Lq * a.Hq);
+  if (a.row_den && d == 0) a.row_den[row] = l;
+  const float v = l > 0.0f ? acc / fmaxf(l, 1.17549435e-38f) : 0.0f;
+  const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + d;
+  if (a.o_f32) static_cast<float*>(a.o)[off] = v;
+  else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
 }
 
 }  // namespace faq

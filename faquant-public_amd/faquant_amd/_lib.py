@@ -47,6 +47,18 @@ _SIGNATURES = {
         [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_int, _vp],
         _c_int,
     ),
+    "faq_attention_split_workspace": ([_c_int, _c_int, _c_int, _c_int, _c_int], _c_i64),
+    "faq_attention_fwd_split": (
+        [
+            _vp, _c_i64, _c_i64, _c_i64,
+            _vp, _c_i64, _c_i64, _c_i64,
+            _vp, _c_i64, _c_i64, _c_i64, _c_int,
+            _vp, _c_int, _c_i64, _c_i64, _c_i64,
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp,
+            _c_int, _vp, _c_i64, _vp,
+        ],
+        _c_int,
+    ),
     "faq_attention_fwd": (
         [
             _vp, _c_i64, _c_i64, _c_i64,

@@ -233,6 +233,7 @@ def attention_fwd(
     out: torch.Tensor,
     row_den: torch.Tensor | None = None,
     out_levels: str | None = None,
+    split: int | None = None,
 ) -> torch.Tensor:
     """Attention over bf16 operands q [B, Hq, Lq, 128], k [B, Hkv, Lk, 128] and
     vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16).
@@ -253,6 +254,20 @@ def attention_fwd(
     os_ = (out.stride(0), out.stride(1), out.stride(2))
     if out.stride(3) != 1:
         raise ValueError("attention output needs a unit stride along head_dim")
+    nsplit = _split_count(B, Hq, Hkv, Lq, int(key_length)) if split is None else int(split)
+    if nsplit > 1 and not out_levels:
+        ws_bytes = lib.faq_attention_split_workspace(B, Hq, Lq, int(key_length), nsplit)
+        ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
+        _lib.check(
+            lib.faq_attention_fwd_split(
+                q.data_ptr(), *qs, k.data_ptr(), *ks_, vt.data_ptr(), *vs, vt.shape[-1],
+                out.data_ptr(), _lib.dtype_code(out.dtype), *os_,
+                B, Hq, Hkv, Lq, int(key_length), int(bool(causal)), float(scale),
+                int(bool(quant_p)), int(p_levels), int(bool(norm_same)), _lib.ptr(row_den),
+                nsplit, ws.data_ptr(), ws.numel(), _lib.stream_ptr(q.device),
+            )
+        )
+        return out
     _lib.check(
         lib.faq_attention_fwd(
             q.data_ptr(), *qs, k.data_ptr(), *ks_, vt.data_ptr(), *vs, vt.shape[-1],
@@ -263,6 +278,20 @@ def attention_fwd(
         )
     )
     return out
+
+
+def _split_count(B: int, Hq: int, Hkv: int, Lq: int, Lk: int) -> int:
+    """Key ranges for decode-sized queries (Lq <= 64) whose grid cannot fill 256 CUs: the
+    one-pass kernel runs one 256-row workgroup per (KV head group, 256/hpw positions).
+    Longer query blocks keep the one-pass kernel, so a prefill fed in chunks stays
+    bitwise equal to one pass."""
+    G = Hq // Hkv
+    hpw = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
+    wgs = B * Hkv * (G // hpw) * -(-Lq // (256 // hpw))
+    ntiles = -(-Lk // KEY_TILE)
+    if Lq > 64 or wgs >= 128 or ntiles < 4:
+        return 1
+    return min(ntiles // 2, max(2, -(-512 // wgs)))
 
 
 def attention_pairs(query_length: int, key_length: int, causal: bool) -> int:

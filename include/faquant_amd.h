@@ -33,6 +33,10 @@
  *                         simulated_flash_attention_forward (key tiles of 128, masks: none /
  *                         bottom-right causal) and src/faquant/wan22_attention.py:165-183
  *                         hif4_attention
+ *   faq_attention_fwd_split  the same recurrence divided over key ranges (decode, where
+ *                         the reference appends one position to its QDQ cache,
+ *                         simulated_flash_attention.py:243-289, and runs the tile loop)
+ *   faq_attention_split_workspace  workspace size of faq_attention_fwd_split
  */
 #ifndef FAQUANT_AMD_H
 #define FAQUANT_AMD_H
@@ -156,6 +160,25 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
                       int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                       int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels,
                       int norm_same, float* row_den, int out_levels, faq_stream_t stream);
+
+/*
+ * Split-key form of faq_attention_fwd for grids that cannot fill the GPU (decode steps,
+ * short prompts).  Same arguments and results (up to the fp32 order of the final O and l
+ * sums; every P-hat code is the same); out_levels is not available.  Key tiles are divided
+ * into nsplit ranges: a first pass records each row's c1-scaled maximum of every key
+ * tile, a scan gives each range the running maximum of the tiles before it (the maximum
+ * the reference's sequential recurrence holds there, sfa:788-806), each range then runs
+ * the recurrence from it, and a combine rescales and sums the ranges.  `workspace` is
+ * device memory of at least faq_attention_split_workspace(B, Hq, Lq, Lk, nsplit) bytes,
+ * 16-byte aligned.
+ */
+int64_t faq_attention_split_workspace(int B, int Hq, int Lq, int Lk, int nsplit);
+int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
+                            int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
+                            int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                            int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p,
+                            int p_levels, int norm_same, float* row_den, int nsplit, void* workspace,
+                            int64_t workspace_bytes, faq_stream_t stream);
 
 #ifdef __cplusplus
 }
