@@ -1,6 +1,6 @@
 """GPU parity of the HiF4 QK/PV attention kernel against the oracle and the reference goldens.
 
-Tolerance (fp32 math, stated here and in DESIGN.md): the kernel computes P with a
+Tolerance (fp32 math): the kernel computes P with a
 hardware exp2 on log2-scaled scores and sums in MFMA order, the oracle with
 numpy exp and BLAS order, so a few P codes flip at rounding boundaries.  The
 bar is a relative Frobenius error <= 2e-3 and a max abs error <= 2e-2 of the
