@@ -87,11 +87,11 @@ void launch_prep_vt(const faq::OperandPrepVtArgs& a, int levels, dim3 grid, hipS
   else hipLaunchKernelGGL((faq::operand_prep_vt_kernel<Tin, 123>), grid, dim3(256), 0, st, a);
 }
 
-template <int LV>
+template <int LV, int kMask>
 void launch_attn_lv(const faq::AttnArgs& a, int quant_p, int same, dim3 grid, hipStream_t st) {
-  if (quant_p && same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true>), grid, dim3(512), 0, st, a);
-  else if (quant_p) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false>), grid, dim3(512), 0, st, a);
-  else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, false, false>), grid, dim3(512), 0, st, a);
+  if (quant_p && same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true, kMask>), grid, dim3(512), 0, st, a);
+  else if (quant_p) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false, kMask>), grid, dim3(512), 0, st, a);
+  else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, false, false, kMask>), grid, dim3(512), 0, st, a);
 }
 
 // fp32(sqrt(n)), its fp32 reciprocal and whether it is a power of two (n = 4^k)
@@ -112,8 +112,19 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
                     int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
                     int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl, int B,
                     int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels,
-                    float* row_den, int out_levels, faq::AttnArgs& a, dim3& grid) {
+                    float* row_den, int out_levels, const faq_attn_opts* opts, faq::AttnArgs& a, dim3& grid) {
   if (!q || !k || !vt || !o) return fail(FAQ_EINVAL, "%s: null operand", who);
+  if (opts) {
+    const bool any = opts->row_lo || opts->row_hi || opts->key_bits;
+    if (any && !(opts->row_lo && opts->row_hi && opts->key_bits))
+      return fail(FAQ_EINVAL, "%s: row_lo, row_hi and key_bits go together", who);
+    if (any && opts->key_words < 4 * ((static_cast<int64_t>(Lk) + 127) / 128))
+      return fail(FAQ_EINVAL, "%s: key_words must be >= 4 * ceil(Lk / 128)", who);
+    if (!(opts->softcap >= 0.0f) || opts->softcap == INFINITY)
+      return fail(FAQ_EINVAL, "softcap must be non-negative");
+    if (opts->softcap > 0.0f && !any)
+      return fail(FAQ_EINVAL, "%s: the softcap needs key ranges (faq_attention_mask_bounds)", who);
+  }
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "%s: bad sizes", who);
   if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
   if (Lpad % 128 || Lpad < Lk) return fail(FAQ_EINVAL, "%s: Lpad must be a multiple of 128 >= Lk", who);
@@ -160,7 +171,17 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
   a.Lq = Lq;
   a.Lk = Lk;
   a.causal = causal != 0;
-  a.c1 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  a.scale = scale;
+  if (opts) {
+    a.row_lo = opts->row_lo;
+    a.row_hi = opts->row_hi;
+    a.key_bits = opts->key_bits;
+    a.key_words = opts->key_words;
+    a.softcap = opts->softcap;
+    a.softcap_rec = opts->softcap > 0.0f ? static_cast<float>(1.0 / static_cast<double>(opts->softcap)) : 0.0f;
+  }
+  // the softcap path scales inside the tanh, so its scores enter the exponent unscaled
+  a.c1 = static_cast<float>(static_cast<double>(a.softcap > 0.0f ? 1.0f : scale) * 1.4426950408889634);
   a.hpw = hpw;
   a.n_pblocks = (Lq + pos_per_wg - 1) / pos_per_wg;
   a.row_den = row_den;
@@ -170,11 +191,19 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
   return FAQ_OK;
 }
 
-void launch_attention(const faq::AttnArgs& a, int quant_p, int p_levels, int norm_same, dim3 grid, hipStream_t st) {
+template <int kMask>
+void launch_attention_m(const faq::AttnArgs& a, int quant_p, int p_levels, int norm_same, dim3 grid,
+                         hipStream_t st) {
   const int lv = quant_p ? p_levels : 123;
-  if (lv == 12) launch_attn_lv<12>(a, quant_p, norm_same, grid, st);
-  else if (lv == 13) launch_attn_lv<13>(a, quant_p, norm_same, grid, st);
-  else launch_attn_lv<123>(a, quant_p, norm_same, grid, st);
+  if (lv == 12) launch_attn_lv<12, kMask>(a, quant_p, norm_same, grid, st);
+  else if (lv == 13) launch_attn_lv<13, kMask>(a, quant_p, norm_same, grid, st);
+  else launch_attn_lv<123, kMask>(a, quant_p, norm_same, grid, st);
+}
+
+void launch_attention(const faq::AttnArgs& a, int quant_p, int p_levels, int norm_same, dim3 grid, hipStream_t st) {
+  if (a.softcap > 0.0f) launch_attention_m<2>(a, quant_p, p_levels, norm_same, grid, st);
+  else if (a.row_lo) launch_attention_m<1>(a, quant_p, p_levels, norm_same, grid, st);
+  else launch_attention_m<0>(a, quant_p, p_levels, norm_same, grid, st);
 }
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -373,15 +402,33 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
                       int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh, int64_t v_sd,
                       int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq,
                       int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels, int norm_same,
-                      float* row_den, int out_levels, faq_stream_t stream) {
+                      float* row_den, int out_levels, const faq_attn_opts* opts, faq_stream_t stream) {
   faq::AttnArgs a;
   dim3 grid;
   const int rc = attention_setup("faq_attention_fwd", q, q_sb, q_sh, q_sl, k, k_sb, k_sh, k_sl, vt, v_sb, v_sh, v_sd,
                                  Lpad, o, o_dtype, o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p,
-                                 p_levels, row_den, out_levels, a, grid);
+                                 p_levels, row_den, out_levels, opts, a, grid);
   if (rc != FAQ_OK) return rc == 1 ? FAQ_OK : rc;
   launch_attention(a, quant_p, p_levels, norm_same, grid, static_cast<hipStream_t>(stream));
   return check_launch("faq_attention_fwd");
+}
+
+int faq_attention_mask_bounds(const uint8_t* mask, int64_t mask_sb, int B, int Lq, int Lk, int causal, int window,
+                              int32_t* row_lo, int32_t* row_hi, uint32_t* key_bits, int64_t key_words,
+                              faq_stream_t stream) {
+  if (!row_lo || !row_hi) return fail(FAQ_EINVAL, "faq_attention_mask_bounds: null output");
+  if (B < 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "faq_attention_mask_bounds: bad sizes");
+  if (window < 0) return fail(FAQ_EINVAL, "sliding_window must be positive");
+  if (Lk > 32 * faq::kMaskMaxWords)
+    return fail(FAQ_EUNSUP, "faq_attention_mask_bounds: at most %d keys", 32 * faq::kMaskMaxWords);
+  if (key_bits && key_words < 4 * ((static_cast<int64_t>(Lk) + 127) / 128))
+    return fail(FAQ_EINVAL, "faq_attention_mask_bounds: key_words must be >= 4 * ceil(Lk / 128)");
+  if (mask && mask_sb < Lk) return fail(FAQ_EINVAL, "faq_attention_mask_bounds: mask row stride < Lk");
+  if (B == 0 || (Lq == 0 && !key_bits)) return FAQ_OK;
+  faq::MaskBoundsArgs a{mask, mask_sb, Lq, Lk, causal != 0, window, row_lo, row_hi, key_bits, key_words};
+  hipLaunchKernelGGL(faq::mask_bounds_kernel, dim3(static_cast<unsigned>(B)), dim3(faq::kMaskThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("faq_attention_mask_bounds");
 }
 
 int64_t faq_attention_split_workspace(int B, int Hq, int Lq, int Lk, int nsplit) {
@@ -394,13 +441,13 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                             int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                             int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p,
                             int p_levels, int norm_same, float* row_den, int nsplit, void* workspace,
-                            int64_t workspace_bytes, faq_stream_t stream) {
+                            int64_t workspace_bytes, const faq_attn_opts* opts, faq_stream_t stream) {
   if (nsplit < 1 || nsplit > 4096) return fail(FAQ_EINVAL, "faq_attention_fwd_split: nsplit must be in [1, 4096]");
   faq::AttnArgs a;
   dim3 grid;
   const int rc = attention_setup("faq_attention_fwd_split", q, q_sb, q_sh, q_sl, k, k_sb, k_sh, k_sl, vt, v_sb, v_sh,
                                  v_sd, Lpad, o, o_dtype, o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p,
-                                 p_levels, row_den, 0, a, grid);
+                                 p_levels, row_den, 0, opts, a, grid);
   if (rc != FAQ_OK) return rc == 1 ? FAQ_OK : rc;
   const SplitLayout L = split_layout(B, Hq, Lq, Lk, nsplit);
   if (!workspace || !aligned16(workspace)) return fail(FAQ_EINVAL, "faq_attention_fwd_split: null or misaligned workspace");
@@ -418,7 +465,7 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   launch_attention(am, quant_p, p_levels, norm_same, grid, st);
   // 2. running maximum before each split
   faq::SplitScanArgs sa{am.mx_out, am.mx_stride, reinterpret_cast<float*>(ws + L.m_start), a.rows_total, nsplit,
-                        L.tiles_per_split, Lq, Lk, causal != 0};
+                        L.tiles_per_split, Hq, Lq, Lk, causal != 0, a.row_lo, a.row_hi};
   const int64_t scan_threads = static_cast<int64_t>(a.rows_total) * nsplit;
   hipLaunchKernelGGL(faq::split_scan_kernel, dim3(grid_for(scan_threads)), dim3(256), 0, st, sa);
   // 3. per-split recurrences from those maxima

@@ -12,16 +12,18 @@
 // and O = acc / l (0 where l == 0).  HiF4-quantized Q/K/V/P values carry at most six
 // significant bits, so they are exact bf16 MFMA operands.
 //
-// Work decomposition: a 256-thread workgroup owns 128 query rows that share one KV
-// head (GQA: up to 4 query heads x 32 positions), so each K/V tile staged in LDS is
-// reused by every row of the group.  Each wave owns 32 rows; two workgroups share a
-// CU (two waves per SIMD), so one workgroup's softmax overlaps the other's MFMAs.
+// Work decomposition: a 512-thread workgroup (eight waves of 32 query rows, one
+// workgroup per CU, two waves per SIMD) owns 256 query rows that share one KV head (GQA:
+// hpw query heads x 256 / hpw positions), so each K/V tile staged in LDS serves 256 rows.
+// K and V^T tiles are double-buffered in LDS and move HBM -> LDS by buffer loads that
+// write LDS directly (no VGPR staging); the DMA of tile t + 1 is issued at the top of
+// tile t, behind the tile's single barrier.
 //
-// Tile pipeline (per workgroup, LDS holds one K tile and one V tile, 64 KiB):
-//   QK(t) reads K(t) | barrier | DMA K(t+1) | softmax(t) | PV(t) reads V(t) | barrier |
-//   DMA V(t+1) | ...
-// The K/V tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging), so
-// K(t+1) lands during softmax+PV(t) and V(t+1) during QK(t+1)+softmax(t+1).
+// Masks: bottom-right causal from the shapes, or per-row key ranges [row_lo, row_hi]
+// plus a key-validity bitmap (2-D padding masks in the unpadded-rank form of sfa:371-427,
+// sliding windows); keys outside become -inf before the row maximum, and key tiles no
+// row of a wave sees are skipped (bitwise the same as processing an all -inf tile).
+// An optional logit softcap replaces s by softcap tanh(scale s / softcap) (sfa:725-727).
 //
 // MFMA layout (v_mfma_f32_32x32x16_bf16; lane l, m = l % 32, half = l / 32):
 //   QK computes S^T = K Q^T.  The B operand is the wave's Q fragment (lane holds
@@ -33,9 +35,8 @@
 //   PV computes O^T = V^T P^T.  For k-chunk c the B operand slots 8 half + t are keys
 //   64 half + 8 c + t, i.e. this lane's own P values (8c .. 8c+7), and the A operand is
 //   the matching 16-byte run of the transposed V tile.
-// LDS tiles are 128 rows x 256 bytes; the 16-byte piece p of row r is stored at
-// position p ^ swz(r), so the operand reads of 16 consecutive lanes hit 16 distinct
-// bank groups.
+// LDS rows are padded to 17 16-byte units (see kRowUnits below), which makes both the
+// QK and the PV operand reads conflict-free.
 //
 // P quantization in registers (levels 123 shown; 12 and 13 differ only in the micro
 // exponent rule).  Per lane and tile: the group maximum m1 is exp2 of the lane's largest
@@ -85,6 +86,17 @@ struct AttnArgs {
   const float* m_start;   // partial pass: running maximum before the split, [nsplit, rows_total]
   float* part_o;          // partial pass: unnormalized O, [nsplit, rows_total, 128]
   float* part_lm;         // partial pass: (l, running maximum) after the split, [nsplit, rows_total, 2]
+  // Key-range masks (kMask >= 1; otherwise the causal flag decides).  Query position p of
+  // batch b sees the keys k in [row_lo[b Lq + p], row_hi[b Lq + p]] whose bit in
+  // key_bits[b key_words + k / 32] is set; bounds lie in [0, Lk - 1] or describe an empty
+  // range (lo > hi), and key_words covers every key tile, 4 words per tile, zero past Lk.
+  const int* row_lo;
+  const int* row_hi;
+  const uint32_t* key_bits;
+  int64_t key_words;
+  float scale;    // softmax scale (the softcap path applies it before the tanh)
+  float softcap;  // > 0 (kMask 2): s -> softcap tanh(scale s / softcap)
+  float softcap_rec;  // fp32(1 / softcap)
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -128,6 +140,45 @@ __device__ __forceinline__ float halves_sum(float x) {
   const uint32_t u = __float_as_uint(x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Minimum / maximum over the 64 lanes, returned as wave-uniform scalars (once per kernel).
+__device__ __forceinline__ int wave_min_i32(int x) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x = min(x, __shfl_xor(x, m, 64));
+  return __builtin_amdgcn_readfirstlane(x);
+}
+__device__ __forceinline__ int wave_max_i32(int x) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x = max(x, __shfl_xor(x, m, 64));
+  return __builtin_amdgcn_readfirstlane(x);
+}
+
+// tanh for the logit softcap, branch-free: |u| < 0.625 takes u + u^3 q(u^2) with a degree-4
+// polynomial fitted (weighted least squares on Chebyshev nodes) to (tanh(x)/x - 1)/x^2;
+// larger |u| takes 1 - 2 / (exp(2|u|) + 1).  Error <= 3 ulp against a float64 tanh over
+// the whole float range (tests/tanh_check.c restates it on the host); exp2 overflow
+// gives 1 and NaN stays NaN.
+__device__ __forceinline__ float softcap_tanh(float u) {
+  const float x = fabsf(u);
+  const float t = x * x;
+  float p = __builtin_fmaf(t, -0.005705005954951048f, 0.020639128983020782f);
+  p = __builtin_fmaf(t, p, -0.05373973771929741f);
+  p = __builtin_fmaf(t, p, 0.13331443071365356f);
+  p = __builtin_fmaf(t, p, -0.3333328068256378f);
+  const float small = __builtin_fmaf(x * t, p, x);
+  const float r = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(x * 2.8853900817779268f) + 1.0f);
+  const float big = 1.0f - (r + r);
+  return __builtin_copysignf(x < 0.625f ? small : big, u);
+}
+
+// Bits [lo, hi] (inclusive, clipped to [0, 31]) of a 32-bit word; 0 when lo > hi.
+__device__ __forceinline__ uint32_t bit_range32(int lo, int hi) {
+  const int a = min(max(lo, 0), 32);
+  const int e = min(max(hi + 1, 0), 32);  // one past the last bit
+  const uint32_t below_e = e >= 32 ? ~0u : ((1u << e) - 1u);
+  const uint32_t below_a = a >= 32 ? ~0u : ((1u << a) - 1u);
+  return below_e & ~below_a;
 }
 
 // Pack 8 fp32 values as bf16; `exact` values are bf16-representable (truncation is exact).
@@ -313,10 +364,16 @@ __device__ __forceinline__ bf16x8 lds_read_at(const uint8_t* base, int byte_off)
   return *reinterpret_cast<const bf16x8*>(base + byte_off);
 }
 
-template <int LV, bool kQuantP, bool kSame>
+// kMask 0: masks from the shapes (none, bottom-right causal, ragged tail); 1: key ranges
+// and valid-key bits (a.row_lo, a.row_hi, a.key_bits); 2: key ranges and the logit
+// softcap.  One masking form per instantiation keeps each hot loop within its register
+// budget.
+template <int LV, bool kQuantP, bool kSame, int kMask>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
+  // one LDS object: two K/V stages, then (key-range mode) the waves' key bounds
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes + (kMask ? 16 * 4 : 0)];
+  int* const wg_keys = reinterpret_cast<int*>(lds + 2 * kStageBytes);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -336,18 +393,52 @@ void attn_fwd_kernel(AttnArgs a) {
   const int p0w = pb * pos_per_wg + (w / a.hpw) * 32;
   const int off = a.Lk - a.Lq;  // bottom-right alignment: row p sees keys <= p + off
 
-  int kend_wg = a.Lk;
-  if (a.causal) kend_wg = min(a.Lk, min(pb * pos_per_wg + pos_per_wg, a.Lq) - 1 + off + 1);
-  const int ntiles = kend_wg > 0 ? (kend_wg + kKeyTile - 1) / kKeyTile : 0;
-  int kend_w = p0w < a.Lq ? a.Lk : 0;
-  if (a.causal && p0w < a.Lq) kend_w = max(0, min(a.Lk, min(p0w + 31, a.Lq - 1) + off + 1));
-
   const int pos = p0w + n;
   const bool row_live = pos < a.Lq;
   const int64_t row = (static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos;
+
+  // Keys [kbeg, kend) seen by some row of this wave / workgroup.
+  int kbeg_w = 0, kbeg_wg = 0;
+  int kend_wg = a.Lk;
+  int kend_w = p0w < a.Lq ? a.Lk : 0;
+  // Key-range mode: a tile needs no per-key mask when every row of the wave sees all of
+  // it (lo_max <= key0 and key0 + 127 <= hi_min).
+  int lo_max = 0, hi_min = a.Lk - 1;
+  int rlo = a.Lk, rhi = -1;  // this row's key range
+  if (kMask) {
+    if (row_live) {
+      rlo = a.row_lo[static_cast<int64_t>(b) * a.Lq + pos];
+      rhi = a.row_hi[static_cast<int64_t>(b) * a.Lq + pos];
+    }
+    const bool any = rlo <= rhi;
+    kbeg_w = wave_min_i32(any ? rlo : a.Lk);
+    kend_w = wave_max_i32(any ? rhi + 1 : 0);
+    lo_max = wave_max_i32(any ? rlo : a.Lk);
+    hi_min = wave_min_i32(any ? rhi : -1);
+    if (lane == 0) {
+      wg_keys[w] = kbeg_w;
+      wg_keys[8 + w] = kend_w;
+    }
+    __syncthreads();
+    kbeg_wg = wg_keys[0];
+    kend_wg = wg_keys[8];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      kbeg_wg = min(kbeg_wg, wg_keys[i]);
+      kend_wg = max(kend_wg, wg_keys[8 + i]);
+    }
+    kbeg_wg = __builtin_amdgcn_readfirstlane(kbeg_wg);
+    kend_wg = __builtin_amdgcn_readfirstlane(kend_wg);
+  } else if (a.causal) {
+    kend_wg = min(a.Lk, min(pb * pos_per_wg + pos_per_wg, a.Lq) - 1 + off + 1);
+    if (p0w < a.Lq) kend_w = max(0, min(a.Lk, min(p0w + 31, a.Lq - 1) + off + 1));
+  }
+  const int ntiles = kend_wg > 0 ? (kend_wg + kKeyTile - 1) / kKeyTile : 0;
+  const int t_first = kbeg_wg < kend_wg ? kbeg_wg / kKeyTile : ntiles;
+
   const int split = static_cast<int>(blockIdx.z);
-  const int t_lo = a.tiles_per_split ? min(ntiles, split * a.tiles_per_split) : 0;
-  const int t_hi = a.tiles_per_split ? min(ntiles, t_lo + a.tiles_per_split) : ntiles;
+  const int t_lo = a.tiles_per_split ? max(t_first, min(ntiles, split * a.tiles_per_split)) : t_first;
+  const int t_hi = a.tiles_per_split ? min(ntiles, split * a.tiles_per_split + a.tiles_per_split) : ntiles;
   bf16x8 qf[8];
   {
     const uint16_t* qp = a.q + b * a.q_sb + hq * a.q_sh + static_cast<int64_t>(row_live ? pos : 0) * a.q_sl + 8 * half;
@@ -441,7 +532,7 @@ void attn_fwd_kernel(AttnArgs a) {
     const uint8_t* const vp = st + vbyte;
 
     const int key0 = t * kKeyTile;
-    if (key0 >= kend_w) continue;
+    if (key0 >= kend_w || key0 + kKeyTile <= kbeg_w) continue;
     floatx16 s[4];
     {
       // ---- S^T = K Q^T, c-major (four independent accumulation chains); the K fragments
@@ -470,9 +561,44 @@ void attn_fwd_kernel(AttnArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- masks (ragged key tail, causal diagonal)
-    const bool need_mask = (key0 + kKeyTile > a.Lk) || (a.causal && key0 + kKeyTile - 1 > p0w + off);
-    if (need_mask) {
+    if (kMask == 2) {
+      // sfa:725-727: scores * scale, then softcap * tanh(scores / softcap)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          // scale, then the quotient by softcap: q = t rc corrected by one fma step
+          const float t = s[kb][i] * a.scale;
+          const float q0 = t * a.softcap_rec;
+          const float q = __builtin_fmaf(__builtin_fmaf(-q0, a.softcap, t), a.softcap_rec, q0);
+          s[kb][i] = softcap_tanh(q) * a.softcap;
+        }
+    }
+    // ---- masks (ragged key tail, causal diagonal, key ranges and invalid keys)
+    if (kMask) {
+      // the tile's four valid-key words, loaded as scalars (wave-uniform address): no wait
+      // on the vector-memory counter, which the in-flight DMA of the next tile also holds
+      // (the constant address space: this kernel never writes key_bits)
+      typedef const __attribute__((address_space(4))) uint32_t const_u32;
+      const_u32* kw = (const_u32*)(a.key_bits + b * a.key_words + (key0 >> 5));
+      const uint32_t kw0 = kw[0], kw1 = kw[1], kw2 = kw[2], kw3 = kw[3];
+      if (!(lo_max <= key0 && key0 + kKeyTile - 1 <= hi_min) || (kw0 & kw1 & kw2 & kw3) != ~0u) {
+        const bool hi_half = half != 0;
+        const int base = key0 + (hi_half ? 64 : 0);
+        const uint32_t m0 = bit_range32(rlo - base, rhi - base) & (hi_half ? kw2 : kw0);
+        const uint32_t m1 = bit_range32(rlo - base - 32, rhi - base - 32) & (hi_half ? kw3 : kw1);
+        // keep = all ones for an allowed key (sign-extended bit), else -inf: bfe + bfi
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int j = 16 * kb + i;
+            const uint32_t keep = static_cast<uint32_t>(
+                __builtin_amdgcn_sbfe(static_cast<int>(j < 32 ? m0 : m1), static_cast<uint32_t>(j & 31), 1u));
+            s[kb][i] = __uint_as_float((__float_as_uint(s[kb][i]) & keep) | (0xFF800000u & ~keep));
+          }
+      }
+    } else if ((key0 + kKeyTile > a.Lk) || (a.causal && key0 + kKeyTile - 1 > p0w + off)) {
       const int lim = a.causal ? min(a.Lk - 1, pos + off) : a.Lk - 1;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -655,7 +781,9 @@ struct SplitScanArgs {
   int rows_total;
   int nsplit;
   int tiles_per_split;
-  int Lq, Lk, causal;
+  int Hq, Lq, Lk, causal;
+  const int* row_lo;  // key-range mode: the row's key range (the attention kernel's bounds)
+  const int* row_hi;
 };
 
 __global__ __launch_bounds__(256) void split_scan_kernel(SplitScanArgs a) {
@@ -664,11 +792,20 @@ __global__ __launch_bounds__(256) void split_scan_kernel(SplitScanArgs a) {
   const int row = static_cast<int>(i % a.rows_total);
   const int split = static_cast<int>(i / a.rows_total);
   const int pos = row % a.Lq;
-  const int kend = a.causal ? min(a.Lk, max(0, pos + a.Lk - a.Lq + 1)) : a.Lk;
-  const int tiles_row = (kend + kKeyTile - 1) / kKeyTile;
-  const int upto = min(tiles_row, split * a.tiles_per_split);
+  // key tiles [t0, t1) of this row; the maxima pass wrote every one of them
+  int t0 = 0, t1;
+  if (a.row_lo) {
+    const int64_t br = static_cast<int64_t>(row / (a.Hq * a.Lq)) * a.Lq + pos;
+    const int lo = a.row_lo[br], hi = a.row_hi[br];
+    t0 = lo <= hi ? lo / kKeyTile : 0;
+    t1 = lo <= hi ? hi / kKeyTile + 1 : 0;
+  } else {
+    const int kend = a.causal ? min(a.Lk, max(0, pos + a.Lk - a.Lq + 1)) : a.Lk;
+    t1 = (kend + kKeyTile - 1) / kKeyTile;
+  }
+  const int upto = min(t1, split * a.tiles_per_split);
   float m = -INFINITY;
-  for (int t = 0; t < upto; ++t) m = fmaxf(m, a.mx[static_cast<int64_t>(row) * a.mx_stride + t]);
+  for (int t = t0; t < upto; ++t) m = fmaxf(m, a.mx[static_cast<int64_t>(row) * a.mx_stride + t]);
   a.m_start[i] = m;
 }
 
@@ -710,6 +847,114 @@ __global__ __launch_bounds__(128) void split_combine_kernel(SplitCombineArgs a) 
   const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + d;
   if (a.o_f32) static_cast<float*>(a.o)[off] = v;
   else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
+}
+
+// ---------------------------------------------------------------------------------------
+// Key ranges of a 2-D attention mask.  sfa:341-368 takes the last Lk mask columns as
+// key_valid and their last Lq (zero-extended in front when Lq > Lk) as query_valid;
+// sfa:406-427 then compares ranks among valid keys: key rank r(k) = #valid keys < k, query
+// anchor = query rank + #valid keys - #valid queries, which is r(j) for the query's own key
+// column j = p + Lk - Lq.  Row p (query_valid) sees the valid keys with rank in
+//   [max(0, anchor - window + 1) if window else 0,
+//    min(#valid - 1, anchor if causal, else anchor + window - 1 if window)]
+// and, ranks growing with k, those keys are exactly the valid keys between two positions:
+// row_lo = the key of rank lo, row_hi = the key of rank hi.  Without a mask (sfa:395-405)
+// the same rule runs on positions.  One workgroup per batch row.
+constexpr int kMaskThreads = 1024;
+constexpr int kMaskMaxWords = 16384;  // Lk <= 524288
+
+struct MaskBoundsArgs {
+  const uint8_t* mask;  // [B, Lk] (row stride mask_sb), nonzero = valid; nullptr: all valid
+  int64_t mask_sb;
+  int Lq, Lk, causal, window;
+  int* row_lo;          // [B, Lq]
+  int* row_hi;
+  uint32_t* key_bits;   // optional [B, key_words]
+  int64_t key_words;
+};
+
+__global__ __launch_bounds__(kMaskThreads) void mask_bounds_kernel(MaskBoundsArgs a) {
+  __shared__ uint32_t bits[kMaskMaxWords];
+  __shared__ int base[kMaskMaxWords];
+  __shared__ int part[kMaskThreads / 64];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nw = (a.Lk + 31) / 32;
+  for (int wd = tid; wd < nw; wd += kMaskThreads) {
+    const int n = min(32, a.Lk - 32 * wd);
+    uint32_t m = n == 32 ? ~0u : ((1u << n) - 1u);
+    if (a.mask) {
+      const uint8_t* src = a.mask + b * a.mask_sb + 32 * wd;
+      m = 0;
+      for (int i = 0; i < n; ++i) m |= (src[i] != 0 ? 1u : 0u) << i;
+    }
+    bits[wd] = m;
+  }
+  __syncthreads();
+  if (a.key_bits)
+    for (int64_t wd = tid; wd < a.key_words; wd += kMaskThreads)
+      a.key_bits[b * a.key_words + wd] = wd < nw ? bits[wd] : 0u;
+  // exclusive prefix counts of valid keys per word: contiguous word chunks per thread,
+  // wave scans of the chunk sums, then the 16 wave totals
+  const int chunk = (nw + kMaskThreads - 1) / kMaskThreads;
+  const int w0 = min(nw, tid * chunk), w1 = min(nw, w0 + chunk);
+  int own = 0;
+  for (int wd = w0; wd < w1; ++wd) own += __popc(bits[wd]);
+  const int lane = tid & 63, wv = tid >> 6;
+  int inc = own;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += y;
+  }
+  if (lane == 63) part[wv] = inc;
+  __syncthreads();
+  int before = inc - own;
+  for (int i = 0; i < wv; ++i) before += part[i];
+  int total = 0;
+  for (int i = 0; i < kMaskThreads / 64; ++i) total += part[i];
+  for (int wd = w0; wd < w1; ++wd) {
+    base[wd] = before;
+    before += __popc(bits[wd]);
+  }
+  __syncthreads();
+  // position of the valid key of rank r (0 <= r < total)
+  auto select = [&](int r) {
+    int lo = 0, hi = nw - 1;  // last word with base <= r
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (base[mid] <= r) lo = mid;
+      else hi = mid - 1;
+    }
+    uint32_t m = bits[lo];
+    for (int k = r - base[lo]; k > 0; --k) m &= m - 1u;
+    return 32 * lo + __ffs(static_cast<int>(m)) - 1;
+  };
+  for (int p = tid; p < a.Lq; p += kMaskThreads) {
+    int lo = a.Lk, hi = -1;
+    const int j = p + a.Lk - a.Lq;
+    // without a mask every query is valid and ranks are positions (sfa:395-405), so the
+    // anchor is j itself, negative for the first Lq - Lk queries when Lq > Lk
+    const bool valid = a.mask ? (j >= 0 && ((bits[j >> 5] >> (j & 31)) & 1u)) : true;
+    if (valid) {
+      // (signed: __popc is unsigned, and a negative j must stay negative)
+      const int64_t anchor =
+          a.mask ? static_cast<int64_t>(base[j >> 5]) + static_cast<int64_t>(__popc(bits[j >> 5] & ((1u << (j & 31)) - 1u)))
+                 : static_cast<int64_t>(j);
+      int64_t rlo = 0, rhi = total - 1;
+      if (a.causal) rhi = min(rhi, anchor);
+      if (a.window > 0) {
+        rlo = max(rlo, anchor - a.window + 1);
+        if (!a.causal) rhi = min(rhi, anchor + a.window - 1);
+      }
+      if (rlo <= rhi) {
+        lo = select(static_cast<int>(rlo));
+        hi = select(static_cast<int>(rhi));
+      }
+    }
+    a.row_lo[static_cast<int64_t>(b) * a.Lq + p] = lo;
+    a.row_hi[static_cast<int64_t>(b) * a.Lq + p] = hi;
+  }
 }
 
 }  // namespace faq

@@ -26,6 +26,22 @@ _c_int = ctypes.c_int
 _c_float = ctypes.c_float
 _vp = ctypes.c_void_p
 
+
+
+class AttnOpts(ctypes.Structure):
+    """``faq_attn_opts``: key-range masks and the logit softcap of the attention kernel."""
+
+    _fields_ = [
+        ("row_lo", _vp),
+        ("row_hi", _vp),
+        ("key_bits", _vp),
+        ("key_words", _c_i64),
+        ("softcap", _c_float),
+    ]
+
+
+_opts_p = ctypes.POINTER(AttnOpts)
+
 _SIGNATURES = {
     "faq_last_error": ([], ctypes.c_char_p),
     "faq_version": ([], ctypes.c_char_p),
@@ -55,8 +71,12 @@ _SIGNATURES = {
             _vp, _c_i64, _c_i64, _c_i64, _c_int,
             _vp, _c_int, _c_i64, _c_i64, _c_i64,
             _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp,
-            _c_int, _vp, _c_i64, _vp,
+            _c_int, _vp, _c_i64, _opts_p, _vp,
         ],
+        _c_int,
+    ),
+    "faq_attention_mask_bounds": (
+        [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_i64, _vp],
         _c_int,
     ),
     "faq_attention_fwd": (
@@ -65,7 +85,8 @@ _SIGNATURES = {
             _vp, _c_i64, _c_i64, _c_i64,
             _vp, _c_i64, _c_i64, _c_i64, _c_int,
             _vp, _c_int, _c_i64, _c_i64, _c_i64,
-            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp, _c_int, _vp,
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp, _c_int,
+            _opts_p, _vp,
         ],
         _c_int,
     ),

@@ -6,7 +6,9 @@ torch stream of that device.
 
 from __future__ import annotations
 
+import ctypes
 import math
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -219,6 +221,75 @@ def operand_prep_vt(v: torch.Tensor, *, levels: str | None) -> torch.Tensor:
     return vt
 
 
+@dataclass
+class KeyRanges:
+    """Per-row key ranges and valid-key bits of the attention kernel's key-range mode:
+    query position p of batch b sees the keys k in [row_lo[b, p], row_hi[b, p]] whose bit
+    k % 32 of key_bits[b, k // 32] is set."""
+
+    row_lo: torch.Tensor    # int32 [B, Lq]
+    row_hi: torch.Tensor    # int32 [B, Lq]
+    key_bits: torch.Tensor  # int32 [B, key_words], key_words = 4 * ceil(Lk / 128)
+
+
+def attention_key_ranges(
+    mask: torch.Tensor | None,
+    batch: int,
+    query_length: int,
+    key_length: int,
+    *,
+    causal: bool,
+    window: int | None = None,
+    device: torch.device | None = None,
+) -> KeyRanges:
+    """Key ranges of a 2-D attention mask (sfa:341-368 plus the rank form of sfa:371-427):
+    ``mask`` holds the last ``key_length`` columns of the caller's [B, L] mask (nonzero =
+    valid; a leading dimension of 1 broadcasts over the batch), or None for every key
+    valid.  ``window`` is the sliding window (None: none)."""
+    lib = _lib.load()
+    if mask is not None:
+        _lib.require_device(mask)
+        device = mask.device
+        if mask.ndim != 2 or mask.shape[-1] != key_length:
+            raise ValueError("the 2-D mask slice must be [B, key_length]")
+        if mask.shape[0] not in (1, batch):
+            raise ValueError("2-D attention mask batch does not match the query batch")
+        mask = mask.to(torch.bool)
+        if mask.shape[0] != batch:
+            mask = mask.expand(batch, key_length)
+        if mask.stride(-1) != 1 or (batch > 1 and mask.stride(0) < key_length):
+            mask = mask.contiguous()
+    if device is None:
+        raise ValueError("attention_key_ranges needs a device when mask is None")
+    if window is not None and window <= 0:
+        raise ValueError("sliding_window must be positive")
+    words = 4 * max(1, -(-key_length // KEY_TILE))
+    row_lo = torch.empty((batch, query_length), device=device, dtype=torch.int32)
+    row_hi = torch.empty_like(row_lo)
+    key_bits = torch.empty((batch, words), device=device, dtype=torch.int32)
+    _lib.check(
+        lib.faq_attention_mask_bounds(
+            _lib.ptr(mask), mask.stride(0) if mask is not None and batch > 1 else key_length,
+            batch, query_length, key_length, int(bool(causal)), int(window or 0),
+            row_lo.data_ptr(), row_hi.data_ptr(), key_bits.data_ptr(), words, _lib.stream_ptr(device),
+        )
+    )
+    return KeyRanges(row_lo, row_hi, key_bits)
+
+
+def _attn_opts(ranges: KeyRanges | None, softcap: float | None):
+    if ranges is None and not softcap:
+        return None
+    opts = _lib.AttnOpts()
+    if ranges is not None:
+        opts.row_lo = ranges.row_lo.data_ptr()
+        opts.row_hi = ranges.row_hi.data_ptr()
+        opts.key_bits = ranges.key_bits.data_ptr()
+        opts.key_words = ranges.key_bits.shape[-1]
+    opts.softcap = float(softcap or 0.0)
+    return ctypes.byref(opts), opts
+
+
 def attention_fwd(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -234,12 +305,29 @@ def attention_fwd(
     row_den: torch.Tensor | None = None,
     out_levels: str | None = None,
     split: int | None = None,
+    ranges: KeyRanges | None = None,
+    softcap: float | None = None,
 ) -> torch.Tensor:
     """Attention over bf16 operands q [B, Hq, Lq, 128], k [B, Hkv, Lk, 128] and
     vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16).
     ``out_levels`` adds a HiF4 QDQ of each 64-value half of every output row, after its
-    rounding to the output dtype (the o_proj-input quantizer, qwen3.py:167-171)."""
+    rounding to the output dtype (the o_proj-input quantizer, qwen3.py:167-171).
+    ``ranges`` (attention_key_ranges) replaces the causal flag by per-row key ranges;
+    ``softcap`` > 0 caps the scores (sfa:725-727)."""
     _lib.require_device(q, k, vt, out, row_den)
+    if softcap is not None and softcap < 0:
+        raise ValueError("softcap must be non-negative")
+    if ranges is None and softcap:
+        ranges = attention_key_ranges(None, q.shape[0], q.shape[2], int(key_length), causal=causal,
+                                      device=q.device)
+    if ranges is not None:
+        _lib.require_device(ranges.row_lo, ranges.row_hi, ranges.key_bits)
+        if tuple(ranges.row_lo.shape) != (q.shape[0], q.shape[2]) or tuple(ranges.row_hi.shape) != tuple(
+            ranges.row_lo.shape
+        ):
+            raise ValueError("key ranges must be [B, Lq]")
+    held = _attn_opts(ranges, softcap)
+    opts = held[0] if held else None
     lib = _lib.load()
     B, Hq, Lq, D = q.shape
     Hkv = k.shape[1]
@@ -264,7 +352,7 @@ def attention_fwd(
                 out.data_ptr(), _lib.dtype_code(out.dtype), *os_,
                 B, Hq, Hkv, Lq, int(key_length), int(bool(causal)), float(scale),
                 int(bool(quant_p)), int(p_levels), int(bool(norm_same)), _lib.ptr(row_den),
-                nsplit, ws.data_ptr(), ws.numel(), _lib.stream_ptr(q.device),
+                nsplit, ws.data_ptr(), ws.numel(), opts, _lib.stream_ptr(q.device),
             )
         )
         return out
@@ -274,7 +362,7 @@ def attention_fwd(
             out.data_ptr(), _lib.dtype_code(out.dtype), *os_,
             B, Hq, Hkv, Lq, int(key_length), int(bool(causal)), float(scale),
             int(bool(quant_p)), int(p_levels), int(bool(norm_same)), _lib.ptr(row_den),
-            int(out_levels) if out_levels else 0, _lib.stream_ptr(q.device),
+            int(out_levels) if out_levels else 0, opts, _lib.stream_ptr(q.device),
         )
     )
     return out

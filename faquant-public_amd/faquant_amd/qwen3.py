@@ -29,6 +29,7 @@ from .simulated_flash_attention import (
     _key_operand,
     _value_operand,
     count_tiles,
+    key_ranges,
     simulated_flash_attention_forward,
 )
 
@@ -102,12 +103,14 @@ def attention_core(
     value: torch.Tensor,
     *,
     scaling: Optional[float] = None,
+    attention_mask: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Post-RoPE Q/K/V -> attention output [B, L, Hq, 128], fused on the GPU.
 
     Equivalent to the reference's excursion followed by
-    ``simulated_flash_attention_forward(module, q, k, v, None, scaling=scaling)``
-    for mask-free causal prefill; other cases go through that drop-in.  When the module
+    ``simulated_flash_attention_forward(module, q, k, v, attention_mask, scaling=scaling)``
+    (qwen3.py:97-166); a 2-D padding mask runs as per-row key ranges in the same fused
+    launch, anything the fused path does not take goes through that drop-in.  When the module
     enables the attention-output quantizer (``faquant_attention_output_quant`` and o_proj
     does not quantize its own input, qwen3.py:167-171), the HiF4 QDQ of the output rows
     with ``faquant_core_quant_kwargs`` runs in the attention kernel's epilogue.
@@ -119,12 +122,14 @@ def attention_core(
     block = _block(rotation, getattr(module, "faquant_qk_rotation_block_size", None), query.shape[-1])
     qk_quant = bool(module.faquant_qk_matmul_quant)
     pv_quant = bool(module.faquant_pv_matmul_quant)
-    if query.dtype != torch.bfloat16 or int(module.faquant_attention_key_chunk_size) != _ops.KEY_TILE:
+    fused = (query.dtype == torch.bfloat16 and int(module.faquant_attention_key_chunk_size) == _ops.KEY_TILE
+             and (attention_mask is None or (attention_mask.ndim == 2 and attention_mask.shape[-1] == key.shape[2])))
+    if not fused:
         q, k = post_rope_qk_transform(
             query, key, smooth_scale=smooth_scale, key_offset=key_offset, rotation=rotation,
             rotation_block_size=getattr(module, "faquant_qk_rotation_block_size", None),
         )
-        out = simulated_flash_attention_forward(module, q, k, value, None, scaling=scaling)[0]
+        out = simulated_flash_attention_forward(module, q, k, value, attention_mask, scaling=scaling)[0]
         if _output_quant_levels(module) is not None:
             out = fake_quantize(out.reshape(*out.shape[:2], -1), **module.faquant_core_quant_kwargs).view(out.shape)
         return out
@@ -145,13 +150,15 @@ def attention_core(
     causal = bool(getattr(module, "is_causal", True))
     out = torch.empty((B, Lq, Hq, D), device=query.device, dtype=query.dtype)
     mode = getattr(module, "faquant_pv_normalizer_mode", "unquantized")
+    ranges, masked = key_ranges(module, attention_mask, batch=B, query_length=Lq, key_length=Lk, causal=causal,
+                                sliding_window=None, device=query.device)
     _ops.attention_fwd(q_op, k_op, vt, Lk, causal=causal, scale=scale, quant_p=pv_quant,
                        p_levels=levels["p"], norm_same=mode == "quantized_same", out=out.transpose(1, 2),
-                       out_levels=_output_quant_levels(module))
+                       out_levels=_output_quant_levels(module), ranges=ranges)
     count_tiles(
         module.faquant_simulated_attention_stats, batch=B, query_heads=Hq, query_length=Lq, key_length=Lk,
         head_dim=D, query_chunk=int(module.faquant_attention_query_chunk_size), key_chunk=_ops.KEY_TILE,
-        causal=causal, skip_fully_masked=bool(getattr(module, "faquant_skip_fully_masked_tiles", True)),
+        causal=causal, skip_fully_masked=bool(getattr(module, "faquant_skip_fully_masked_tiles", True)) and not masked,
         qk_quant=qk_quant, pv_quant=pv_quant, qk_group=qk_group, pv_group=pv_group,
     )
     return out

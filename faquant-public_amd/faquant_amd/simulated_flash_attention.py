@@ -8,10 +8,10 @@ V is written transposed for the PV MFMA operand) and the attention kernel.
 
 Supported on the GPU: head_dim 128, key tiles of 128 (the reference default),
 the HiF4 format with groups of 64 (or no quantization), causal (bottom-right)
-or full attention, attention_mask None or an all-valid 2-D mask, bf16 or fp32
-inputs.  Everything else the reference accepts (padding ranks, sliding window,
-softcap, 4-D masks, int/MXFP8 formats, the PV-normalizer probe) raises
-NotImplementedError: there is no fallback path.
+or full attention, 2-D attention masks (padding, in the reference's rank form),
+sliding windows, the logit softcap, bf16 or fp32 inputs.  Everything else the
+reference accepts (3-D/4-D masks, int/MXFP8 formats, the PV-normalizer probe)
+raises NotImplementedError: there is no fallback path.
 """
 
 from __future__ import annotations
@@ -59,6 +59,41 @@ def _record(stats: dict, operand: str, width: int, numel: int, group_size: int, 
     stats[f"{operand}_quantized_values"] += numel * repeats
     stats[f"{operand}_quant_blocks"] += vectors * groups * repeats
     stats[f"{operand}_quant_padding_values"] += vectors * (groups * g - width) * repeats
+
+
+def key_ranges(
+    module,
+    attention_mask: Optional[torch.Tensor],
+    *,
+    batch: int,
+    query_length: int,
+    key_length: int,
+    causal: bool,
+    sliding_window: Optional[int],
+    device: torch.device,
+):
+    """Per-row key ranges for a 2-D attention mask and / or a sliding window, and whether
+    a mask stays in force.  sfa:561-586: an all-valid mask of a single multi-token prompt
+    is the mask-free bottom-right case (tile skipping stays on); every other 2-D mask
+    keeps the rank form of sfa:406-427 (unpadded FlashAttention alignment), which the
+    kernel runs as key ranges plus valid-key bits."""
+    key_mask = None
+    if attention_mask is not None:
+        if attention_mask.ndim != 2:
+            raise NotImplementedError("3-D/4-D attention masks are not implemented on the MI355X")
+        skip = bool(getattr(module, "faquant_skip_fully_masked_tiles", True))
+        all_valid_prefill = (
+            skip and batch == 1 and query_length > 1 and bool(torch.all(attention_mask[:, -key_length:]).item())
+        )
+        if not all_valid_prefill:
+            if attention_mask.shape[-1] < key_length:
+                raise ValueError("2-D attention mask is shorter than the simulated key sequence")
+            key_mask = attention_mask[:, -key_length:]
+    if key_mask is None and sliding_window is None:
+        return None, False
+    ranges = _ops.attention_key_ranges(key_mask, batch, query_length, key_length, causal=causal,
+                                       window=sliding_window, device=device)
+    return ranges, key_mask is not None
 
 
 def count_tiles(
@@ -282,19 +317,10 @@ def simulated_flash_attention_forward(
     is_causal = bool(getattr(module, "is_causal", True) if requested_causal is None else requested_causal)
     skip = bool(getattr(module, "faquant_skip_fully_masked_tiles", True))
 
-    if attention_mask is not None:
-        if attention_mask.ndim == 2:
-            if not bool(torch.all(attention_mask[:, -key_length:]).item()):
-                raise NotImplementedError("padding masks (rank-based causal alignment) are not implemented on the MI355X")
-            attention_mask = None  # an all-valid mask is the mask-free bottom-right case
-        elif attention_mask.ndim in (3, 4):
-            raise NotImplementedError("3-D/4-D attention masks are not implemented on the MI355X")
-        else:
-            raise ValueError("attention mask must be rank 2, 3, or 4")
-    if sliding_window is not None:
-        raise NotImplementedError("sliding-window attention is not implemented on the MI355X")
-    if softcap:
-        raise NotImplementedError("logit softcap is not implemented on the MI355X")
+    if attention_mask is not None and attention_mask.ndim not in (2, 3, 4):
+        raise ValueError("attention mask must be rank 2, 3, or 4")
+    if attention_mask is not None and attention_mask.ndim != 2:
+        raise NotImplementedError("3-D/4-D attention masks are not implemented on the MI355X")
     if key_chunk != _ops.KEY_TILE:
         raise NotImplementedError(f"the HIP kernel uses key tiles of {_ops.KEY_TILE}, got {key_chunk}")
     if query_chunk <= 0:
@@ -314,16 +340,21 @@ def simulated_flash_attention_forward(
     k_op = _key_operand(module, key, enabled=qk_quant, query_length=query_length, levels=levels["k"])
     vt = _value_operand(module, value, enabled=pv_quant, query_length=query_length, levels=levels["v"])
 
+    ranges, masked = key_ranges(module, attention_mask, batch=batch, query_length=query_length,
+                                key_length=key_length, causal=is_causal, sliding_window=sliding_window,
+                                device=query.device)
     output = torch.empty((batch, query_length, query_heads, head_dim), device=query.device, dtype=query.dtype)
     _ops.attention_fwd(
         q_op, k_op, vt, key_length,
         causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
-        norm_same=mode == "quantized_same", out=output.transpose(1, 2),
+        norm_same=mode == "quantized_same", out=output.transpose(1, 2), ranges=ranges, softcap=softcap,
     )
     count_tiles(
         module.faquant_simulated_attention_stats,
         batch=batch, query_heads=query_heads, query_length=query_length, key_length=key_length,
         head_dim=head_dim, query_chunk=query_chunk, key_chunk=key_chunk, causal=is_causal,
-        skip_fully_masked=skip, qk_quant=qk_quant, pv_quant=pv_quant, qk_group=qk_group, pv_group=pv_group,
+        # the reference skips fully future tiles only without a mask or window (sfa:676-681)
+        skip_fully_masked=skip and not masked and sliding_window is None,
+        qk_quant=qk_quant, pv_quant=pv_quant, qk_group=qk_group, pv_group=pv_group,
     )
     return output, None

@@ -30,9 +30,11 @@
  *   faq_operand_prep_vt   the V QDQ of simulated_flash_attention.py:600-611
  *                         (written transposed for the PV operand)
  *   faq_attention_fwd     src/faquant/simulated_flash_attention.py:457-909
- *                         simulated_flash_attention_forward (key tiles of 128, masks: none /
- *                         bottom-right causal) and src/faquant/wan22_attention.py:165-183
- *                         hif4_attention
+ *                         simulated_flash_attention_forward (key tiles of 128; masks: none,
+ *                         bottom-right causal, or key ranges + valid keys; logit softcap)
+ *                         and src/faquant/wan22_attention.py:165-183 hif4_attention
+ *   faq_attention_mask_bounds  simulated_flash_attention.py:341-368 _two_dimensional_mask and
+ *                         the rank form of 371-427 _streaming_mask (padding, sliding window)
  *   faq_attention_fwd_split  the same recurrence divided over key ranges (decode, where
  *                         the reference appends one position to its QDQ cache,
  *                         simulated_flash_attention.py:243-289, and runs the tile loop)
@@ -139,6 +141,40 @@ int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int
                         int Lpad, uint16_t* vt, int levels, faq_stream_t stream);
 
 /*
+ * Score options of faq_attention_fwd / faq_attention_fwd_split (a NULL pointer: none).
+ *   row_lo, row_hi  int32 [B, Lq]: query position p of batch b sees only the keys in
+ *   key_bits        [row_lo, row_hi] (inclusive, within [0, Lk - 1]; row_lo > row_hi: no
+ *                   key, output row 0) whose bit k % 32 of key_bits word k / 32 is set;
+ *                   key_bits is uint32 [B, key_words], key_words >= 4 * ceil(Lk / 128), zero
+ *                   past Lk.  All three or none; none: the `causal` argument decides.
+ *   softcap         > 0: scores become softcap * tanh(scale * s / softcap) before masking
+ *                   (simulated_flash_attention.py:725-727; needs the key ranges); 0: off.
+ * faq_attention_mask_bounds computes row_lo / row_hi / key_bits from a 2-D mask (or, with
+ * mask = NULL, the plain causal / full ranges).
+ */
+typedef struct faq_attn_opts {
+  const int32_t* row_lo;
+  const int32_t* row_hi;
+  const uint32_t* key_bits;
+  int64_t key_words;
+  float softcap;
+} faq_attn_opts;
+
+/*
+ * Key ranges of a 2-D attention mask for faq_attn_opts.  `mask` is uint8/bool [B, Lk]
+ * with row stride mask_sb (the last Lk columns of the caller's mask; nonzero = valid), or
+ * NULL for all keys valid.  As the reference does (unpadded FlashAttention alignment):
+ * query position p is valid when mask column p + Lk - Lq is (invalid when that column is
+ * < 0), and it sees the valid keys whose rank among valid keys is <= its own column's rank
+ * (causal), > rank - window (window > 0) and < rank + window (window > 0, not causal).
+ * Writes row_lo / row_hi [B, Lq] and, if key_bits is non-NULL, key_bits [B, key_words]
+ * (key_words >= 4 * ceil(Lk / 128)).  Lk <= 524288.
+ */
+int faq_attention_mask_bounds(const uint8_t* mask, int64_t mask_sb, int B, int Lq, int Lk, int causal, int window,
+                              int32_t* row_lo, int32_t* row_hi, uint32_t* key_bits, int64_t key_words,
+                              faq_stream_t stream);
+
+/*
  * HiF4 QK/PV flash attention forward, head_dim 128, key tiles of 128 in ascending
  * order from key 0.
  *   q   bf16 [B, Hq, Lq, 128]  strides (q_sb, q_sh, q_sl)   (quantized or not by caller)
@@ -154,12 +190,14 @@ int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int
  *   out_levels  0, or HiF4 levels (123 / 12 / 13) of a QDQ of every 64-value half of each
  *               output row after its rounding to o_dtype: the o_proj-input activation
  *               quantizer of src/faquant/qwen3.py:167-171, fused into the epilogue
+ *   opts        NULL, or key-range masks and the logit softcap (faq_attn_opts)
  */
 int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
                       int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
                       int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                       int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels,
-                      int norm_same, float* row_den, int out_levels, faq_stream_t stream);
+                      int norm_same, float* row_den, int out_levels, const faq_attn_opts* opts,
+                      faq_stream_t stream);
 
 /*
  * Split-key form of faq_attention_fwd for grids that cannot fill the GPU (decode steps,
@@ -178,7 +216,7 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                             int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                             int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p,
                             int p_levels, int norm_same, float* row_den, int nsplit, void* workspace,
-                            int64_t workspace_bytes, faq_stream_t stream);
+                            int64_t workspace_bytes, const faq_attn_opts* opts, faq_stream_t stream);
 
 #ifdef __cplusplus
 }

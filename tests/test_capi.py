@@ -39,7 +39,7 @@ def test_header_lists_the_entry_points():
     assert names == sorted(
         ["faq_last_error", "faq_version", "faq_hif4_qdq_rows", "faq_hif4_unpack_rows", "faq_hadamard_rows",
          "faq_act_qdq_rows", "faq_operand_prep", "faq_operand_prep_vt", "faq_attention_fwd",
-         "faq_attention_fwd_split", "faq_attention_split_workspace"]
+         "faq_attention_fwd_split", "faq_attention_split_workspace", "faq_attention_mask_bounds"]
     )
 
 
@@ -72,14 +72,35 @@ def test_validation_statuses_without_device_work(lib):
     assert lib.faq_operand_prep(p16, 1, 128, 128, 128, 1, 1, 1, None, 0, None, 0, 0, 96, 1, None, p16, 128, 128, 128,
                                 123, None) == _lib.EUNSUP
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
-                               1, 3, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, None)
+                               1, 3, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, None, None)
     assert rc == _lib.EINVAL and "divisible" in lib.faq_last_error().decode()
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 100, p16, 1, 0, 0, 0,
-                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, None)
+                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, None, None)
     assert rc == _lib.EINVAL and "Lpad" in lib.faq_last_error().decode()
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
-                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 45, None)
+                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 45, None, None)
     assert rc == _lib.EINVAL and "123, 12 or 13" in lib.faq_last_error().decode()
+    # score options: ranges and key bits go together; the softcap needs the ranges
+    opts = _lib.AttnOpts()
+    opts.row_lo = p16
+    rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
+                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, ctypes.byref(opts), None)
+    assert rc == _lib.EINVAL and "go together" in lib.faq_last_error().decode()
+    opts = _lib.AttnOpts()
+    opts.softcap = 30.0
+    rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
+                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, ctypes.byref(opts), None)
+    assert rc == _lib.EINVAL and "softcap needs key ranges" in lib.faq_last_error().decode()
+    opts.softcap = -1.0
+    rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
+                               1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, ctypes.byref(opts), None)
+    assert rc == _lib.EINVAL and "non-negative" in lib.faq_last_error().decode()
+    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 4, 1, 0, None, None, None, 0, None) == _lib.EINVAL
+    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 4, 1, -2, p16, p16, None, 0, None) == _lib.EINVAL
+    assert "sliding_window" in lib.faq_last_error().decode()
+    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 1 << 20, 1, 0, p16, p16, None, 0, None) == _lib.EUNSUP
+    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 300, 1, 0, p16, p16, p16, 8, None) == _lib.EINVAL
+    assert "key_words" in lib.faq_last_error().decode()
 
 
 def test_status_maps_to_reference_exception_types(lib):

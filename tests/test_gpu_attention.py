@@ -332,14 +332,10 @@ def test_unsupported_features_raise(dev):
 
     q = torch.randn(1, 2, 8, 128, device=dev)
     k = torch.randn(1, 1, 8, 128, device=dev)
-    with pytest.raises(NotImplementedError, match="sliding"):
-        simulated_flash_attention_forward(module(), q, k, k, None, sliding_window=4)
     with pytest.raises(NotImplementedError, match="key tiles"):
         simulated_flash_attention_forward(module(key_chunk=64), q, k, k, None)
-    mask = torch.ones(1, 8, dtype=torch.bool, device=dev)
-    mask[0, 0] = False
-    with pytest.raises(NotImplementedError, match="padding"):
-        simulated_flash_attention_forward(module(), q, k, k, mask)
+    with pytest.raises(NotImplementedError, match="4-D"):
+        simulated_flash_attention_forward(module(), q, k, k, torch.zeros(1, 1, 8, 8, device=dev))
     with pytest.raises(NotImplementedError, match="head_dim"):
         simulated_flash_attention_forward(module(), q[..., :64], k[..., :64], k[..., :64], None)
     # an all-valid mask is the mask-free case
