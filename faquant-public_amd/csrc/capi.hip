@@ -89,6 +89,11 @@ void launch_prep_vt(const faq::OperandPrepVtArgs& a, int levels, dim3 grid, hipS
 
 template <int LV, int kMask>
 void launch_attn_lv(const faq::AttnArgs& a, int quant_p, int same, dim3 grid, hipStream_t st) {
+  if (a.diag) {  // the probe exists only with P quantization (validated by the caller)
+    if (same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true, kMask | 4>), grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false, kMask | 4>), grid, dim3(512), 0, st, a);
+    return;
+  }
   if (quant_p && same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true, kMask>), grid, dim3(512), 0, st, a);
   else if (quant_p) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false, kMask>), grid, dim3(512), 0, st, a);
   else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, false, false, kMask>), grid, dim3(512), 0, st, a);
@@ -124,6 +129,8 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
       return fail(FAQ_EINVAL, "softcap must be non-negative");
     if (opts->softcap > 0.0f && !any)
       return fail(FAQ_EINVAL, "%s: the softcap needs key ranges (faq_attention_mask_bounds)", who);
+    if (opts->pv_probe && !quant_p) return fail(FAQ_EINVAL, "%s: the PV-normalizer probe needs quant_p", who);
+    if (opts->pv_probe && !aligned16(opts->pv_probe)) return fail(FAQ_EINVAL, "%s: misaligned pv_probe", who);
   }
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "%s: bad sizes", who);
   if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
@@ -179,6 +186,7 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
     a.key_words = opts->key_words;
     a.softcap = opts->softcap;
     a.softcap_rec = opts->softcap > 0.0f ? static_cast<float>(1.0 / static_cast<double>(opts->softcap)) : 0.0f;
+    a.diag = opts->pv_probe;
   }
   // the softcap path scales inside the tanh, so its scores enter the exponent unscaled
   a.c1 = static_cast<float>(static_cast<double>(a.softcap > 0.0f ? 1.0f : scale) * 1.4426950408889634);
@@ -449,6 +457,7 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                                  v_sd, Lpad, o, o_dtype, o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p,
                                  p_levels, row_den, 0, opts, a, grid);
   if (rc != FAQ_OK) return rc == 1 ? FAQ_OK : rc;
+  if (a.diag) return fail(FAQ_EINVAL, "faq_attention_fwd_split: the PV-normalizer probe runs in faq_attention_fwd");
   const SplitLayout L = split_layout(B, Hq, Lq, Lk, nsplit);
   if (!workspace || !aligned16(workspace)) return fail(FAQ_EINVAL, "faq_attention_fwd_split: null or misaligned workspace");
   if (workspace_bytes < L.total)

@@ -97,6 +97,7 @@ struct AttnArgs {
   float scale;    // softmax scale (the softcap path applies it before the tanh)
   float softcap;  // > 0 (kMask 2): s -> softcap tanh(scale s / softcap)
   float softcap_rec;  // fp32(1 / softcap)
+  float* diag;        // PV-normalizer probe (kMode & 4): [rows_total, 5] per-row sums
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -364,13 +365,15 @@ __device__ __forceinline__ bf16x8 lds_read_at(const uint8_t* base, int byte_off)
   return *reinterpret_cast<const bf16x8*>(base + byte_off);
 }
 
-// kMask 0: masks from the shapes (none, bottom-right causal, ragged tail); 1: key ranges
-// and valid-key bits (a.row_lo, a.row_hi, a.key_bits); 2: key ranges and the logit
-// softcap.  One masking form per instantiation keeps each hot loop within its register
-// budget.
-template <int LV, bool kQuantP, bool kSame, int kMask>
+// kMode & 3 (kMask) 0: masks from the shapes (none, bottom-right causal, ragged tail);
+// 1: key ranges and valid-key bits (a.row_lo, a.row_hi, a.key_bits); 2: key ranges and the
+// logit softcap.  kMode & 4 (kDiag): the PV-normalizer probe (a.diag).  One form per
+// instantiation keeps each hot loop within its register budget.
+template <int LV, bool kQuantP, bool kSame, int kMode>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(AttnArgs a) {
+  constexpr int kMask = kMode & 3;
+  constexpr bool kDiag = kQuantP && (kMode & 4) != 0;
   // one LDS object: two K/V stages, then (key-range mode) the waves' key bounds
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes + (kMask ? 16 * 4 : 0)];
   int* const wg_keys = reinterpret_cast<int*>(lds + 2 * kStageBytes);
@@ -459,6 +462,10 @@ void attn_fwd_kernel(AttnArgs a) {
   // tiles before its split (sfa:788-806: P of tile t depends on the maximum after tile t)
   float m_run = (a.m_start && row_live) ? a.m_start[static_cast<int64_t>(split) * a.rows_total + row] : -INFINITY;
   float l_run = 0.0f;
+  // probe (kDiag): the other normalizer source (sum of P when l sums P^, and the reverse),
+  // rescaled like l, and per-element sums over this lane's keys: #(P^ = 0 < P),
+  // sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869)
+  float sh_run = 0.0f, dg_zero = 0.0f, dg_err = 0.0f, dg_ref = 0.0f;
   bf16x2_t ones2;
   {
     const uint32_t one2 = 0x3F803F80u;
@@ -629,6 +636,7 @@ void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
       l_run *= alpha;
+      if (kDiag) sh_run *= alpha;
     }
     // ---- P, its HiF4 QDQ and the row sum, one 8-key chunk at a time; chunk c of this lane
     // is keys 64 half + 8c .. 8c+7, the B operand of PV k-chunk c.
@@ -637,7 +645,7 @@ void attn_fwd_kernel(AttnArgs a) {
       // group maximum = P of the lane's largest score (same fma and exp2)
       pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
     }
-    float rowsum = 0.0f;
+    float rowsum = 0.0f, shadow = 0.0f;
     // Software pipeline over the eight 8-key chunks: iteration c computes chunk c's P^
     // (VALU) while the MFMAs of chunk c - 1 issue one at a time between those VALU
     // instructions.
@@ -660,16 +668,34 @@ void attn_fwd_kernel(AttnArgs a) {
           for (int j = 0; j < 8; ++j) rowsum += pc[j];
         }
         if (kQuantP) {
+          float pu[8];
+          if (kDiag) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              pu[j] = pc[j];
+              if (kSame) shadow += pc[j];
+            }
+          }
           pquant8<LV>(pc, pq);
           pcur = pack8<true>(pc);
-          if (kSame) {
+          if (kSame || kDiag) {
             uint32_t wv[4];
             __builtin_memcpy(wv, &pcur, 16);
+            float& qsum = kSame ? rowsum : shadow;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               bf16x2_t pr;
               __builtin_memcpy(&pr, &wv[i], 4);
-              rowsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, rowsum, false);
+              qsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, qsum, false);
+            }
+          }
+          if (kDiag) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const float d = pc[j] - pu[j];
+              dg_err = __builtin_fmaf(d, d, dg_err);
+              dg_ref = __builtin_fmaf(pu[j], pu[j], dg_ref);
+              dg_zero += (pc[j] == 0.0f && pu[j] > 0.0f) ? 1.0f : 0.0f;
             }
           }
         } else {
@@ -709,6 +735,7 @@ void attn_fwd_kernel(AttnArgs a) {
       plprev = plcur;
     }
     l_run += halves_sum(rowsum);
+    if (kDiag) sh_run += halves_sum(shadow);
   }
 
   if (!row_live || a.mx_out) return;
@@ -729,6 +756,18 @@ void attn_fwd_kernel(AttnArgs a) {
     return;
   }
   const float l = l_run;
+  if (kDiag) {
+    // per row: sum P^, sum P, #(P^ = 0 < P), sum (P^ - P)^2, sum P^2
+    const float zero = halves_sum(dg_zero), err = halves_sum(dg_err), ref = halves_sum(dg_ref);
+    if (half == 0) {
+      float* dg = a.diag + row * 5;
+      dg[0] = kSame ? l : sh_run;
+      dg[1] = kSame ? sh_run : l;
+      dg[2] = zero;
+      dg[3] = err;
+      dg[4] = ref;
+    }
+  }
   const float inv_guard = fmaxf(l, 1.17549435e-38f);
   if (a.row_den && half == 0) a.row_den[(static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos] = l;
   char* obase = static_cast<char*>(a.o);

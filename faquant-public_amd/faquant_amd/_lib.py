@@ -37,6 +37,7 @@ class AttnOpts(ctypes.Structure):
         ("key_bits", _vp),
         ("key_words", _c_i64),
         ("softcap", _c_float),
+        ("pv_probe", _vp),
     ]
 
 

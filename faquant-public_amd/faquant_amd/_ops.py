@@ -277,10 +277,11 @@ def attention_key_ranges(
     return KeyRanges(row_lo, row_hi, key_bits)
 
 
-def _attn_opts(ranges: KeyRanges | None, softcap: float | None):
-    if ranges is None and not softcap:
+def _attn_opts(ranges: KeyRanges | None, softcap: float | None, pv_probe: torch.Tensor | None = None):
+    if ranges is None and not softcap and pv_probe is None:
         return None
     opts = _lib.AttnOpts()
+    opts.pv_probe = _lib.ptr(pv_probe)
     if ranges is not None:
         opts.row_lo = ranges.row_lo.data_ptr()
         opts.row_hi = ranges.row_hi.data_ptr()
@@ -307,13 +308,16 @@ def attention_fwd(
     split: int | None = None,
     ranges: KeyRanges | None = None,
     softcap: float | None = None,
+    pv_probe: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention over bf16 operands q [B, Hq, Lq, 128], k [B, Hkv, Lk, 128] and
     vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16).
     ``out_levels`` adds a HiF4 QDQ of each 64-value half of every output row, after its
     rounding to the output dtype (the o_proj-input quantizer, qwen3.py:167-171).
     ``ranges`` (attention_key_ranges) replaces the causal flag by per-row key ranges;
-    ``softcap`` > 0 caps the scores (sfa:725-727)."""
+    ``softcap`` > 0 caps the scores (sfa:725-727).  ``pv_probe`` (fp32 [B, Hq, Lq, 5],
+    needs ``quant_p``) receives the PV-normalizer probe's per-row sums: sum P^, sum P,
+    #(P^ = 0 < P), sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869); it runs one pass."""
     _lib.require_device(q, k, vt, out, row_den)
     if softcap is not None and softcap < 0:
         raise ValueError("softcap must be non-negative")
@@ -326,7 +330,13 @@ def attention_fwd(
             ranges.row_lo.shape
         ):
             raise ValueError("key ranges must be [B, Lq]")
-    held = _attn_opts(ranges, softcap)
+    if pv_probe is not None:
+        _lib.require_device(pv_probe)
+        if pv_probe.dtype != torch.float32 or tuple(pv_probe.shape) != (q.shape[0], q.shape[1], q.shape[2], 5) \
+                or not pv_probe.is_contiguous():
+            raise ValueError("pv_probe must be a contiguous fp32 [B, Hq, Lq, 5] tensor")
+        split = 1
+    held = _attn_opts(ranges, softcap, pv_probe)
     opts = held[0] if held else None
     lib = _lib.load()
     B, Hq, Lq, D = q.shape

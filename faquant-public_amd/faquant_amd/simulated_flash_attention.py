@@ -9,8 +9,8 @@ V is written transposed for the PV MFMA operand) and the attention kernel.
 Supported on the GPU: head_dim 128, key tiles of 128 (the reference default),
 the HiF4 format with groups of 64 (or no quantization), causal (bottom-right)
 or full attention, 2-D attention masks (padding, in the reference's rank form),
-sliding windows, the logit softcap, bf16 or fp32 inputs.  Everything else the
-reference accepts (3-D/4-D masks, int/MXFP8 formats, the PV-normalizer probe)
+sliding windows, the logit softcap, the PV-normalizer probe, bf16 or fp32
+inputs.  Everything else the reference accepts (3-D/4-D masks, int/MXFP8 formats)
 raises NotImplementedError: there is no fallback path.
 """
 
@@ -39,6 +39,75 @@ def new_simulated_attention_stats() -> dict[str, int]:
         for field in ("quant_calls", "quantized_values", "quant_blocks", "quant_padding_values"):
             stats[f"{operand}_{field}"] = 0
     return stats
+
+
+_PV_DIAGNOSTIC_KEYS = ("rows", "mass_ratio_sum", "mass_ratio_sq_sum", "mass_ratio_min", "mass_ratio_max",
+                       "p_values", "p_zeroed_values", "p_error_sq_sum", "p_reference_sq_sum")
+
+
+def new_pv_normalizer_diagnostics() -> dict:
+    """Zeroed accumulators of the PV-normalizer probe (sfa:74-92): attach the dict to a
+    module as ``faquant_pv_normalizer_diagnostics``; the attention output is unchanged."""
+    d: dict = dict.fromkeys(_PV_DIAGNOSTIC_KEYS, 0.0)
+    d["mass_ratio_min"] = float("inf")
+    d["mass_ratio_max"] = float("-inf")
+    d["mass_ratio_histogram"] = [0.0] * (len(PV_MASS_RATIO_BIN_EDGES) + 1)
+    return d
+
+
+def summarize_pv_normalizer_diagnostics(diagnostics: dict) -> dict:
+    """Per-run scalars of the probe (sfa:95-130): mass-ratio moments, extremes and
+    histogram, the P zero-collapse rate and the relative L2 error of P-hat."""
+    rows = float(diagnostics["rows"])
+    values = float(diagnostics["p_values"])
+    energy = float(diagnostics["p_reference_sq_sum"])
+    summary: dict = {"rows": rows, "p_values": values}
+    if rows > 0:
+        hist = list(diagnostics["mass_ratio_histogram"])
+        mean = float(diagnostics["mass_ratio_sum"]) / rows
+        var = max(float(diagnostics["mass_ratio_sq_sum"]) / rows - mean * mean, 0.0)
+        summary.update(
+            mass_ratio_mean=mean,
+            mass_ratio_std=math.sqrt(var),
+            mass_ratio_min=float(diagnostics["mass_ratio_min"]),
+            mass_ratio_max=float(diagnostics["mass_ratio_max"]),
+            mass_ratio_bin_edges=list(PV_MASS_RATIO_BIN_EDGES),
+            mass_ratio_histogram=hist,
+            mass_ratio_fraction_below_one=sum(hist[: PV_MASS_RATIO_BIN_EDGES.index(1.0) + 1]) / rows,
+            mean_relative_scale_error=mean - 1.0,
+        )
+    if values > 0:
+        summary["p_zero_collapse_rate"] = float(diagnostics["p_zeroed_values"]) / values
+    if energy > 0:
+        summary["p_relative_l2"] = math.sqrt(float(diagnostics["p_error_sq_sum"]) / energy)
+    return summary
+
+
+def _record_probe(diagnostics: dict, probe: torch.Tensor, p_values: int) -> None:
+    """Fold the kernel's per-row probe sums into the accumulators (sfa:130-185, 835-869):
+    the elementwise P-hat error terms, and sum(P-hat) / sum(P) of every row whose
+    unquantized denominator is positive."""
+    t = probe.double()
+    diagnostics["p_values"] += float(p_values)
+    sums = t[..., 2:].sum(dim=tuple(range(t.dim() - 1))).tolist()
+    diagnostics["p_zeroed_values"] += sums[0]
+    diagnostics["p_error_sq_sum"] += sums[1]
+    diagnostics["p_reference_sq_sum"] += sums[2]
+    quantized, unquantized = t[..., 0], t[..., 1]
+    valid = unquantized > 0
+    if not bool(valid.any()):
+        return
+    ratio = (quantized[valid] / unquantized[valid]).flatten()
+    diagnostics["rows"] += float(ratio.numel())
+    diagnostics["mass_ratio_sum"] += float(ratio.sum())
+    diagnostics["mass_ratio_sq_sum"] += float(ratio.square().sum())
+    diagnostics["mass_ratio_min"] = min(diagnostics["mass_ratio_min"], float(ratio.min()))
+    diagnostics["mass_ratio_max"] = max(diagnostics["mass_ratio_max"], float(ratio.max()))
+    edges = torch.tensor(PV_MASS_RATIO_BIN_EDGES, device=ratio.device, dtype=ratio.dtype)
+    counts = torch.bincount(torch.bucketize(ratio, edges), minlength=len(PV_MASS_RATIO_BIN_EDGES) + 1)
+    hist = diagnostics["mass_ratio_histogram"]
+    for i, c in enumerate(counts.tolist()):
+        hist[i] += float(c)
 
 
 def register_simulated_attention_backend() -> None:
@@ -332,8 +401,8 @@ def simulated_flash_attention_forward(
             raise NotImplementedError(f"the HIP attention path takes bf16 or fp32 operands, got {t.dtype}")
     qk_group = _hif4_group(qk_quant_kwargs, "QK") if qk_quant else 64
     pv_group = _hif4_group(pv_quant_kwargs, "PV") if pv_quant else 64
-    if pv_quant and isinstance(getattr(module, "faquant_pv_normalizer_diagnostics", None), dict):
-        raise NotImplementedError("the PV normalizer probe is not implemented on the MI355X")
+    diagnostics = getattr(module, "faquant_pv_normalizer_diagnostics", None)
+    collect = pv_quant and isinstance(diagnostics, dict)
 
     levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
     q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None)
@@ -344,11 +413,15 @@ def simulated_flash_attention_forward(
                                 key_length=key_length, causal=is_causal, sliding_window=sliding_window,
                                 device=query.device)
     output = torch.empty((batch, query_length, query_heads, head_dim), device=query.device, dtype=query.dtype)
+    probe = (torch.empty((batch, query_heads, query_length, 5), device=query.device, dtype=torch.float32)
+             if collect else None)
     _ops.attention_fwd(
         q_op, k_op, vt, key_length,
         causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
         norm_same=mode == "quantized_same", out=output.transpose(1, 2), ranges=ranges, softcap=softcap,
+        pv_probe=probe,
     )
+    p_values_before = module.faquant_simulated_attention_stats["p_quantized_values"]
     count_tiles(
         module.faquant_simulated_attention_stats,
         batch=batch, query_heads=query_heads, query_length=query_length, key_length=key_length,
@@ -357,4 +430,8 @@ def simulated_flash_attention_forward(
         skip_fully_masked=skip and not masked and sliding_window is None,
         qk_quant=qk_quant, pv_quant=pv_quant, qk_group=qk_group, pv_group=pv_group,
     )
+    if collect:
+        # every processed P tile counts all its values (sfa:139), as the P QDQ stats do
+        _record_probe(diagnostics, probe,
+                      module.faquant_simulated_attention_stats["p_quantized_values"] - p_values_before)
     return output, None

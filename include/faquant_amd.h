@@ -149,6 +149,11 @@ int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int
  *                   past Lk.  All three or none; none: the `causal` argument decides.
  *   softcap         > 0: scores become softcap * tanh(scale * s / softcap) before masking
  *                   (simulated_flash_attention.py:725-727; needs the key ranges); 0: off.
+ *   pv_probe        fp32 [B, Hq, Lq, 5] (faq_attention_fwd with quant_p only), or NULL:
+ *                   the PV-normalizer probe of simulated_flash_attention.py:36-185, 835-869.
+ *                   Per row: sum of P-hat and sum of P (each rescaled like the running
+ *                   denominator), #(P-hat = 0 < P), sum (P-hat - P)^2 and sum P^2 over
+ *                   every processed key.
  * faq_attention_mask_bounds computes row_lo / row_hi / key_bits from a 2-D mask (or, with
  * mask = NULL, the plain causal / full ranges).
  */
@@ -158,6 +163,7 @@ typedef struct faq_attn_opts {
   const uint32_t* key_bits;
   int64_t key_words;
   float softcap;
+  float* pv_probe;
 } faq_attn_opts;
 
 /*
