@@ -9,21 +9,23 @@ disabled for the whole device build.
 
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SRC = os.path.join(HERE, "csrc", "capi.hip")
+CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "faquant_amd", "libfaquant_amd.so")
+ATTN_MASK_FORMS = 5  # attn_instances.hip is compiled once per masking form
 
-FLAGS = [
+COMPILE = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
@@ -36,16 +38,33 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> str:
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *FLAGS, SRC, "-o", tmp]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
         raise RuntimeError(f"hipcc failed with status {proc.returncode}")
-    os.replace(tmp, OUT)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the C ABI and the attention instantiations (one object per masking form,
+    in parallel) and link libfaquant_amd.so."""
+    with tempfile.TemporaryDirectory(prefix="faq_build_") as tmp:
+        units = [(os.path.join(CSRC, "capi.hip"), [], os.path.join(tmp, "capi.o"))]
+        for m in range(ATTN_MASK_FORMS):
+            units.append((os.path.join(CSRC, "attn_instances.hip"), [f"-DFAQ_ATTN_MASK={m}"],
+                          os.path.join(tmp, f"attn_m{m}.o")))
+        jobs = min(len(units), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+        with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
+            futures = [pool.submit(_run, [hipcc(), *COMPILE, *defs, "-c", src, "-o", obj], verbose)
+                       for src, defs, obj in units]
+            for f in futures:
+                f.result()
+        tmp_out = OUT + ".tmp"
+        _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *(obj for _, _, obj in units), "-o", tmp_out],
+             verbose)
+        os.replace(tmp_out, OUT)
     return OUT
 
 

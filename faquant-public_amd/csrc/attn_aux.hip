@@ -1,0 +1,195 @@
+// Split-key passes (tile maxima scan, combine) and the key ranges of 2-D masks: the small
+// kernels around the attention kernel (hif4_attention.hip), compiled with the C ABI.
+#pragma once
+#include "hif4_attention.hip"
+
+namespace faq {
+
+// ---------------------------------------------------------------------------------------
+// Split-key attention (decode and other short grids): after the maxima pass, the running
+// maximum before split j of row r is the maximum of the c1-scaled tile maxima of its first
+// t_lo(j) tiles (-inf if none), restricted to the tiles the row sees.
+struct SplitScanArgs {
+  const float* mx;     // [rows_total, mx_stride]
+  int mx_stride;
+  float* m_start;      // [nsplit, rows_total]
+  int rows_total;
+  int nsplit;
+  int tiles_per_split;
+  int Hq, Lq, Lk, causal;
+  const int* row_lo;  // key-range mode: the row's key range (the attention kernel's bounds)
+  const int* row_hi;
+};
+
+__global__ __launch_bounds__(256) void split_scan_kernel(SplitScanArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<int64_t>(a.rows_total) * a.nsplit) return;
+  const int row = static_cast<int>(i % a.rows_total);
+  const int split = static_cast<int>(i / a.rows_total);
+  const int pos = row % a.Lq;
+  // key tiles [t0, t1) of this row; the maxima pass wrote every one of them
+  int t0 = 0, t1;
+  if (a.row_lo) {
+    const int64_t br = static_cast<int64_t>(row / (a.Hq * a.Lq)) * a.Lq + pos;
+    const int lo = a.row_lo[br], hi = a.row_hi[br];
+    t0 = lo <= hi ? lo / kKeyTile : 0;
+    t1 = lo <= hi ? hi / kKeyTile + 1 : 0;
+  } else {
+    const int kend = a.causal ? min(a.Lk, max(0, pos + a.Lk - a.Lq + 1)) : a.Lk;
+    t1 = (kend + kKeyTile - 1) / kKeyTile;
+  }
+  const int upto = min(t1, split * a.tiles_per_split);
+  float m = -INFINITY;
+  for (int t = t0; t < upto; ++t) m = fmaxf(m, a.mx[static_cast<int64_t>(row) * a.mx_stride + t]);
+  a.m_start[i] = m;
+}
+
+// O = sum_j 2^(m_j - M) O_j / sum_j 2^(m_j - M) l_j with M the row's final running maximum;
+// the per-split recurrences already used the reference's maxima, so only the fp32 order of
+// the O and l sums differs from one pass.
+struct SplitCombineArgs {
+  const float* part_o;   // [nsplit, rows_total, 128]
+  const float* part_lm;  // [nsplit, rows_total, 2]
+  int rows_total, nsplit;
+  int Hq, Lq;
+  void* o;               // [B, Hq, Lq, 128] via strides
+  int64_t o_sb, o_sh, o_sl;
+  int o_f32;
+  float* row_den;        // optional [rows_total]
+};
+
+__global__ __launch_bounds__(128) void split_combine_kernel(SplitCombineArgs a) {
+  const int row = blockIdx.x;
+  const int d = threadIdx.x;
+  float mmax = -INFINITY;
+  for (int j = 0; j < a.nsplit; ++j) mmax = fmaxf(mmax, a.part_lm[(static_cast<int64_t>(j) * a.rows_total + row) * 2 + 1]);
+  float l = 0.0f, acc = 0.0f;
+  if (mmax != -INFINITY) {
+    for (int j = 0; j < a.nsplit; ++j) {
+      const int64_t r = static_cast<int64_t>(j) * a.rows_total + row;
+      const float lj = a.part_lm[r * 2];
+      if (lj == 0.0f) continue;
+      const float w = __builtin_amdgcn_exp2f(a.part_lm[r * 2 + 1] - mmax);
+      l = __builtin_fmaf(w, lj, l);
+      acc = __builtin_fmaf(w, a.part_o[r * kDim + d], acc);
+    }
+  }
+  const int pos = row % a.Lq;
+  const int hq = (row / a.Lq) % a.Hq;
+  const int b = row / (a.Lq * a.Hq);
+  if (a.row_den && d == 0) a.row_den[row] = l;
+  const float v = l > 0.0f ? acc / fmaxf(l, 1.17549435e-38f) : 0.0f;
+  const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + d;
+  if (a.o_f32) static_cast<float*>(a.o)[off] = v;
+  else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
+}
+
+// ---------------------------------------------------------------------------------------
+// Key ranges of a 2-D attention mask.  sfa:341-368 takes the last Lk mask columns as
+// key_valid and their last Lq (zero-extended in front when Lq > Lk) as query_valid;
+// sfa:406-427 then compares ranks among valid keys: key rank r(k) = #valid keys < k, query
+// anchor = query rank + #valid keys - #valid queries, which is r(j) for the query's own key
+// column j = p + Lk - Lq.  Row p (query_valid) sees the valid keys with rank in
+//   [max(0, anchor - window + 1) if window else 0,
+//    min(#valid - 1, anchor if causal, else anchor + window - 1 if window)]
+// and, ranks growing with k, those keys are exactly the valid keys between two positions:
+// row_lo = the key of rank lo, row_hi = the key of rank hi.  Without a mask (sfa:395-405)
+// the same rule runs on positions.  One workgroup per batch row.
+constexpr int kMaskThreads = 1024;
+constexpr int kMaskMaxWords = 16384;  // Lk <= 524288
+
+struct MaskBoundsArgs {
+  const uint8_t* mask;  // [B, Lk] (row stride mask_sb), nonzero = valid; nullptr: all valid
+  int64_t mask_sb;
+  int Lq, Lk, causal, window;
+  int* row_lo;          // [B, Lq]
+  int* row_hi;
+  uint32_t* key_bits;   // optional [B, key_words]
+  int64_t key_words;
+};
+
+__global__ __launch_bounds__(kMaskThreads) void mask_bounds_kernel(MaskBoundsArgs a) {
+  __shared__ uint32_t bits[kMaskMaxWords];
+  __shared__ int base[kMaskMaxWords];
+  __shared__ int part[kMaskThreads / 64];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nw = (a.Lk + 31) / 32;
+  for (int wd = tid; wd < nw; wd += kMaskThreads) {
+    const int n = min(32, a.Lk - 32 * wd);
+    uint32_t m = n == 32 ? ~0u : ((1u << n) - 1u);
+    if (a.mask) {
+      const uint8_t* src = a.mask + b * a.mask_sb + 32 * wd;
+      m = 0;
+      for (int i = 0; i < n; ++i) m |= (src[i] != 0 ? 1u : 0u) << i;
+    }
+    bits[wd] = m;
+  }
+  __syncthreads();
+  if (a.key_bits)
+    for (int64_t wd = tid; wd < a.key_words; wd += kMaskThreads)
+      a.key_bits[b * a.key_words + wd] = wd < nw ? bits[wd] : 0u;
+  // exclusive prefix counts of valid keys per word: contiguous word chunks per thread,
+  // wave scans of the chunk sums, then the 16 wave totals
+  const int chunk = (nw + kMaskThreads - 1) / kMaskThreads;
+  const int w0 = min(nw, tid * chunk), w1 = min(nw, w0 + chunk);
+  int own = 0;
+  for (int wd = w0; wd < w1; ++wd) own += __popc(bits[wd]);
+  const int lane = tid & 63, wv = tid >> 6;
+  int inc = own;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += y;
+  }
+  if (lane == 63) part[wv] = inc;
+  __syncthreads();
+  int before = inc - own;
+  for (int i = 0; i < wv; ++i) before += part[i];
+  int total = 0;
+  for (int i = 0; i < kMaskThreads / 64; ++i) total += part[i];
+  for (int wd = w0; wd < w1; ++wd) {
+    base[wd] = before;
+    before += __popc(bits[wd]);
+  }
+  __syncthreads();
+  // position of the valid key of rank r (0 <= r < total)
+  auto select = [&](int r) {
+    int lo = 0, hi = nw - 1;  // last word with base <= r
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (base[mid] <= r) lo = mid;
+      else hi = mid - 1;
+    }
+    uint32_t m = bits[lo];
+    for (int k = r - base[lo]; k > 0; --k) m &= m - 1u;
+    return 32 * lo + __ffs(static_cast<int>(m)) - 1;
+  };
+  for (int p = tid; p < a.Lq; p += kMaskThreads) {
+    int lo = a.Lk, hi = -1;
+    const int j = p + a.Lk - a.Lq;
+    // without a mask every query is valid and ranks are positions (sfa:395-405), so the
+    // anchor is j itself, negative for the first Lq - Lk queries when Lq > Lk
+    const bool valid = a.mask ? (j >= 0 && ((bits[j >> 5] >> (j & 31)) & 1u)) : true;
+    if (valid) {
+      // (signed: __popc is unsigned, and a negative j must stay negative)
+      const int64_t anchor =
+          a.mask ? static_cast<int64_t>(base[j >> 5]) + static_cast<int64_t>(__popc(bits[j >> 5] & ((1u << (j & 31)) - 1u)))
+                 : static_cast<int64_t>(j);
+      int64_t rlo = 0, rhi = total - 1;
+      if (a.causal) rhi = min(rhi, anchor);
+      if (a.window > 0) {
+        rlo = max(rlo, anchor - a.window + 1);
+        if (!a.causal) rhi = min(rhi, anchor + a.window - 1);
+      }
+      if (rlo <= rhi) {
+        lo = select(static_cast<int>(rlo));
+        hi = select(static_cast<int>(rhi));
+      }
+    }
+    a.row_lo[static_cast<int64_t>(b) * a.Lq + p] = lo;
+    a.row_hi[static_cast<int64_t>(b) * a.Lq + p] = hi;
+  }
+}
+
+}  // namespace faq

@@ -7,6 +7,7 @@
 #include <string>
 
 #include "../../include/faquant_amd.h"
+#include "attn_aux.hip"
 #include "hif4_attention.hip"
 #include "hif4_quant.hip"
 
@@ -87,18 +88,6 @@ void launch_prep_vt(const faq::OperandPrepVtArgs& a, int levels, dim3 grid, hipS
   else hipLaunchKernelGGL((faq::operand_prep_vt_kernel<Tin, 123>), grid, dim3(256), 0, st, a);
 }
 
-template <int LV, int kMask>
-void launch_attn_lv(const faq::AttnArgs& a, int quant_p, int same, dim3 grid, hipStream_t st) {
-  if (a.diag) {  // the probe exists only with P quantization (validated by the caller)
-    if (same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true, kMask | 4>), grid, dim3(512), 0, st, a);
-    else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false, kMask | 4>), grid, dim3(512), 0, st, a);
-    return;
-  }
-  if (quant_p && same) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, true, kMask>), grid, dim3(512), 0, st, a);
-  else if (quant_p) hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, true, false, kMask>), grid, dim3(512), 0, st, a);
-  else hipLaunchKernelGGL((faq::attn_fwd_kernel<LV, false, false, kMask>), grid, dim3(512), 0, st, a);
-}
-
 // fp32(sqrt(n)), its fp32 reciprocal and whether it is a power of two (n = 4^k)
 faq::SqrtDiv sqrt_div(int n) {
   faq::SqrtDiv d{};
@@ -127,9 +116,13 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
       return fail(FAQ_EINVAL, "%s: key_words must be >= 4 * ceil(Lk / 128)", who);
     if (!(opts->softcap >= 0.0f) || opts->softcap == INFINITY)
       return fail(FAQ_EINVAL, "softcap must be non-negative");
-    if (opts->softcap > 0.0f && !any)
+    if (opts->softcap > 0.0f && !any && !opts->dense_mask)
       return fail(FAQ_EINVAL, "%s: the softcap needs key ranges (faq_attention_mask_bounds)", who);
     if (opts->pv_probe && !quant_p) return fail(FAQ_EINVAL, "%s: the PV-normalizer probe needs quant_p", who);
+    if (opts->dense_mask && any)
+      return fail(FAQ_EINVAL, "%s: a dense mask and key ranges are exclusive", who);
+    if (opts->dense_mask && (!aligned16(opts->dense_mask) || (opts->dm_sb | opts->dm_sh | opts->dm_sq) & 3))
+      return fail(FAQ_EINVAL, "%s: the dense mask needs 16-byte aligned rows", who);
     if (opts->pv_probe && !aligned16(opts->pv_probe)) return fail(FAQ_EINVAL, "%s: misaligned pv_probe", who);
   }
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "%s: bad sizes", who);
@@ -187,9 +180,15 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
     a.softcap = opts->softcap;
     a.softcap_rec = opts->softcap > 0.0f ? static_cast<float>(1.0 / static_cast<double>(opts->softcap)) : 0.0f;
     a.diag = opts->pv_probe;
+    a.amask = opts->dense_mask;
+    a.am_sb = opts->dm_sb;
+    a.am_sh = opts->dm_sh;
+    a.am_sq = opts->dm_sq;
+    if (a.amask) a.causal = 0;  // the dense mask replaces the causal rule (sfa:731-757)
   }
-  // the softcap path scales inside the tanh, so its scores enter the exponent unscaled
-  a.c1 = static_cast<float>(static_cast<double>(a.softcap > 0.0f ? 1.0f : scale) * 1.4426950408889634);
+  // the softcap and dense-mask paths scale the scores themselves, which then enter the
+  // exponent unscaled
+  a.c1 = static_cast<float>(static_cast<double>(a.softcap > 0.0f || a.amask ? 1.0f : scale) * 1.4426950408889634);
   a.hpw = hpw;
   a.n_pblocks = (Lq + pos_per_wg - 1) / pos_per_wg;
   a.row_den = row_den;
@@ -199,19 +198,12 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
   return FAQ_OK;
 }
 
-template <int kMask>
-void launch_attention_m(const faq::AttnArgs& a, int quant_p, int p_levels, int norm_same, dim3 grid,
-                         hipStream_t st) {
-  const int lv = quant_p ? p_levels : 123;
-  if (lv == 12) launch_attn_lv<12, kMask>(a, quant_p, norm_same, grid, st);
-  else if (lv == 13) launch_attn_lv<13, kMask>(a, quant_p, norm_same, grid, st);
-  else launch_attn_lv<123, kMask>(a, quant_p, norm_same, grid, st);
-}
-
 void launch_attention(const faq::AttnArgs& a, int quant_p, int p_levels, int norm_same, dim3 grid, hipStream_t st) {
-  if (a.softcap > 0.0f) launch_attention_m<2>(a, quant_p, p_levels, norm_same, grid, st);
-  else if (a.row_lo) launch_attention_m<1>(a, quant_p, p_levels, norm_same, grid, st);
-  else launch_attention_m<0>(a, quant_p, p_levels, norm_same, grid, st);
+  if (a.amask && a.softcap > 0.0f) faq::launch_attention_mask<4>(a, quant_p, p_levels, norm_same, grid, st);
+  else if (a.amask) faq::launch_attention_mask<3>(a, quant_p, p_levels, norm_same, grid, st);
+  else if (a.softcap > 0.0f) faq::launch_attention_mask<2>(a, quant_p, p_levels, norm_same, grid, st);
+  else if (a.row_lo) faq::launch_attention_mask<1>(a, quant_p, p_levels, norm_same, grid, st);
+  else faq::launch_attention_mask<0>(a, quant_p, p_levels, norm_same, grid, st);
 }
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -474,7 +466,7 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   launch_attention(am, quant_p, p_levels, norm_same, grid, st);
   // 2. running maximum before each split
   faq::SplitScanArgs sa{am.mx_out, am.mx_stride, reinterpret_cast<float*>(ws + L.m_start), a.rows_total, nsplit,
-                        L.tiles_per_split, Hq, Lq, Lk, causal != 0, a.row_lo, a.row_hi};
+                        L.tiles_per_split, Hq, Lq, Lk, a.causal, a.row_lo, a.row_hi};
   const int64_t scan_threads = static_cast<int64_t>(a.rows_total) * nsplit;
   hipLaunchKernelGGL(faq::split_scan_kernel, dim3(grid_for(scan_threads)), dim3(256), 0, st, sa);
   // 3. per-split recurrences from those maxima

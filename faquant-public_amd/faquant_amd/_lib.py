@@ -38,6 +38,10 @@ class AttnOpts(ctypes.Structure):
         ("key_words", _c_i64),
         ("softcap", _c_float),
         ("pv_probe", _vp),
+        ("dense_mask", _vp),
+        ("dm_sb", _c_i64),
+        ("dm_sh", _c_i64),
+        ("dm_sq", _c_i64),
     ]
 
 

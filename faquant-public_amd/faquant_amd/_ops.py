@@ -277,11 +277,47 @@ def attention_key_ranges(
     return KeyRanges(row_lo, row_hi, key_bits)
 
 
-def _attn_opts(ranges: KeyRanges | None, softcap: float | None, pv_probe: torch.Tensor | None = None):
-    if ranges is None and not softcap and pv_probe is None:
+def dense_attention_mask(mask: torch.Tensor, batch: int, heads: int, query_length: int,
+                         key_length: int) -> torch.Tensor:
+    """The kernel's form of a 3-D/4-D attention mask (sfa:430-454): fp32
+    [B or 1, Hq or 1, Lq or 1, Lpad], 0 / the additive value where allowed, -inf where the
+    reference masks (boolean False, -inf, or <= finfo.min / 2), -inf past key_length.
+    Query rows are the mask's last query_length rows (one row broadcasts); keys are its
+    first key_length columns."""
+    if mask.ndim == 3:
+        mask = mask[:, None]
+    if mask.ndim != 4:
+        raise ValueError("attention mask must be rank 2, 3, or 4")
+    mq = mask.shape[-2]
+    if mq == 1:
+        rows = slice(0, 1)
+    elif mq >= query_length:
+        rows = slice(mq - query_length, mq)
+    else:
+        raise ValueError("4-D attention mask is shorter than the query sequence")
+    if mask.shape[0] not in (1, batch) or mask.shape[1] not in (1, heads) or mask.shape[-1] < key_length:
+        raise ValueError("4-D attention mask does not broadcast to the attention scores")
+    m = mask[..., rows, :key_length]
+    if m.dtype == torch.bool or not m.is_floating_point():
+        add = torch.zeros(m.shape, device=m.device, dtype=torch.float32).masked_fill(~m.to(torch.bool), -math.inf)
+    else:
+        invalid = torch.isneginf(m) | (m <= torch.finfo(m.dtype).min / 2)
+        add = m.to(torch.float32).masked_fill(invalid, -math.inf)
+    out = torch.full((*m.shape[:-1], _pad_keys(key_length)), -math.inf, device=m.device, dtype=torch.float32)
+    out[..., :key_length] = add
+    return out
+
+
+def _attn_opts(ranges: KeyRanges | None, softcap: float | None, pv_probe: torch.Tensor | None = None,
+               dense_mask: torch.Tensor | None = None):
+    if ranges is None and not softcap and pv_probe is None and dense_mask is None:
         return None
     opts = _lib.AttnOpts()
     opts.pv_probe = _lib.ptr(pv_probe)
+    if dense_mask is not None:
+        opts.dense_mask = dense_mask.data_ptr()
+        sb, sh, sq = (dense_mask.stride(i) if dense_mask.shape[i] > 1 else 0 for i in range(3))
+        opts.dm_sb, opts.dm_sh, opts.dm_sq = sb, sh, sq
     if ranges is not None:
         opts.row_lo = ranges.row_lo.data_ptr()
         opts.row_hi = ranges.row_hi.data_ptr()
@@ -309,6 +345,7 @@ def attention_fwd(
     ranges: KeyRanges | None = None,
     softcap: float | None = None,
     pv_probe: torch.Tensor | None = None,
+    dense_mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention over bf16 operands q [B, Hq, Lq, 128], k [B, Hkv, Lk, 128] and
     vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16).
@@ -317,11 +354,20 @@ def attention_fwd(
     ``ranges`` (attention_key_ranges) replaces the causal flag by per-row key ranges;
     ``softcap`` > 0 caps the scores (sfa:725-727).  ``pv_probe`` (fp32 [B, Hq, Lq, 5],
     needs ``quant_p``) receives the PV-normalizer probe's per-row sums: sum P^, sum P,
-    #(P^ = 0 < P), sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869); it runs one pass."""
+    #(P^ = 0 < P), sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869); it runs one pass.
+    ``dense_mask`` (dense_attention_mask) is a 3-D/4-D mask: added to the scaled scores in
+    place of the causal rule (sfa:730-757)."""
     _lib.require_device(q, k, vt, out, row_den)
     if softcap is not None and softcap < 0:
         raise ValueError("softcap must be non-negative")
-    if ranges is None and softcap:
+    if dense_mask is not None:
+        _lib.require_device(dense_mask)
+        if ranges is not None:
+            raise ValueError("a dense mask and key ranges are exclusive")
+        if (dense_mask.dtype != torch.float32 or dense_mask.ndim != 4 or dense_mask.stride(-1) != 1
+                or dense_mask.shape[-1] < _pad_keys(int(key_length))):
+            raise ValueError("dense_mask must be fp32 [B|1, Hq|1, Lq|1, Lpad] with unit key stride")
+    if ranges is None and softcap and dense_mask is None:
         ranges = attention_key_ranges(None, q.shape[0], q.shape[2], int(key_length), causal=causal,
                                       device=q.device)
     if ranges is not None:
@@ -336,7 +382,7 @@ def attention_fwd(
                 or not pv_probe.is_contiguous():
             raise ValueError("pv_probe must be a contiguous fp32 [B, Hq, Lq, 5] tensor")
         split = 1
-    held = _attn_opts(ranges, softcap, pv_probe)
+    held = _attn_opts(ranges, softcap, pv_probe, dense_mask)
     opts = held[0] if held else None
     lib = _lib.load()
     B, Hq, Lq, D = q.shape

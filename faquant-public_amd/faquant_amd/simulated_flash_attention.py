@@ -9,9 +9,9 @@ V is written transposed for the PV MFMA operand) and the attention kernel.
 Supported on the GPU: head_dim 128, key tiles of 128 (the reference default),
 the HiF4 format with groups of 64 (or no quantization), causal (bottom-right)
 or full attention, 2-D attention masks (padding, in the reference's rank form),
-sliding windows, the logit softcap, the PV-normalizer probe, bf16 or fp32
-inputs.  Everything else the reference accepts (3-D/4-D masks, int/MXFP8 formats)
-raises NotImplementedError: there is no fallback path.
+3-D/4-D masks (boolean or additive), sliding windows, the logit softcap, the
+PV-normalizer probe, bf16 or fp32 inputs.  Everything else the reference accepts
+(int/MXFP8 formats) raises NotImplementedError: there is no fallback path.
 """
 
 from __future__ import annotations
@@ -149,7 +149,7 @@ def key_ranges(
     key_mask = None
     if attention_mask is not None:
         if attention_mask.ndim != 2:
-            raise NotImplementedError("3-D/4-D attention masks are not implemented on the MI355X")
+            raise ValueError("key ranges come from a 2-D attention mask")
         skip = bool(getattr(module, "faquant_skip_fully_masked_tiles", True))
         all_valid_prefill = (
             skip and batch == 1 and query_length > 1 and bool(torch.all(attention_mask[:, -key_length:]).item())
@@ -388,8 +388,6 @@ def simulated_flash_attention_forward(
 
     if attention_mask is not None and attention_mask.ndim not in (2, 3, 4):
         raise ValueError("attention mask must be rank 2, 3, or 4")
-    if attention_mask is not None and attention_mask.ndim != 2:
-        raise NotImplementedError("3-D/4-D attention masks are not implemented on the MI355X")
     if key_chunk != _ops.KEY_TILE:
         raise NotImplementedError(f"the HIP kernel uses key tiles of {_ops.KEY_TILE}, got {key_chunk}")
     if query_chunk <= 0:
@@ -409,9 +407,15 @@ def simulated_flash_attention_forward(
     k_op = _key_operand(module, key, enabled=qk_quant, query_length=query_length, levels=levels["k"])
     vt = _value_operand(module, value, enabled=pv_quant, query_length=query_length, levels=levels["v"])
 
-    ranges, masked = key_ranges(module, attention_mask, batch=batch, query_length=query_length,
-                                key_length=key_length, causal=is_causal, sliding_window=sliding_window,
-                                device=query.device)
+    dense = None
+    if attention_mask is not None and attention_mask.ndim in (3, 4):
+        # sfa:730-757: a 3-D/4-D mask is added to the scores instead of the causal / window rule
+        dense = _ops.dense_attention_mask(attention_mask, batch, query_heads, query_length, key_length)
+        ranges, masked = None, True
+    else:
+        ranges, masked = key_ranges(module, attention_mask, batch=batch, query_length=query_length,
+                                    key_length=key_length, causal=is_causal, sliding_window=sliding_window,
+                                    device=query.device)
     output = torch.empty((batch, query_length, query_heads, head_dim), device=query.device, dtype=query.dtype)
     probe = (torch.empty((batch, query_heads, query_length, 5), device=query.device, dtype=torch.float32)
              if collect else None)
@@ -419,7 +423,7 @@ def simulated_flash_attention_forward(
         q_op, k_op, vt, key_length,
         causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
         norm_same=mode == "quantized_same", out=output.transpose(1, 2), ranges=ranges, softcap=softcap,
-        pv_probe=probe,
+        pv_probe=probe, dense_mask=dense,
     )
     p_values_before = module.faquant_simulated_attention_stats["p_quantized_values"]
     count_tiles(

@@ -149,6 +149,12 @@ int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int
  *                   past Lk.  All three or none; none: the `causal` argument decides.
  *   softcap         > 0: scores become softcap * tanh(scale * s / softcap) before masking
  *                   (simulated_flash_attention.py:725-727; needs the key ranges); 0: off.
+ *   dense_mask      fp32 additive mask (3-D/4-D masks, simulated_flash_attention.py:430-454):
+ *   dm_sb, dm_sh,   element [b, h, p, k] at dense_mask + b dm_sb + h dm_sh + p dm_sq + k
+ *   dm_sq           (0 broadcasts; multiples of 4), k < Lpad; -inf masks, columns >= Lk
+ *                   must be -inf.  Scores become scale * s (softcapped if softcap > 0)
+ *                   + mask and the `causal` argument is not applied.  Exclusive with
+ *                   the key ranges.
  *   pv_probe        fp32 [B, Hq, Lq, 5] (faq_attention_fwd with quant_p only), or NULL:
  *                   the PV-normalizer probe of simulated_flash_attention.py:36-185, 835-869.
  *                   Per row: sum of P-hat and sum of P (each rescaled like the running
@@ -164,6 +170,8 @@ typedef struct faq_attn_opts {
   int64_t key_words;
   float softcap;
   float* pv_probe;
+  const float* dense_mask;
+  int64_t dm_sb, dm_sh, dm_sq;
 } faq_attn_opts;
 
 /*

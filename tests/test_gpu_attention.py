@@ -334,8 +334,10 @@ def test_unsupported_features_raise(dev):
     k = torch.randn(1, 1, 8, 128, device=dev)
     with pytest.raises(NotImplementedError, match="key tiles"):
         simulated_flash_attention_forward(module(key_chunk=64), q, k, k, None)
-    with pytest.raises(NotImplementedError, match="4-D"):
-        simulated_flash_attention_forward(module(), q, k, k, torch.zeros(1, 1, 8, 8, device=dev))
+    mod = module()
+    mod.faquant_matmul_quant_kwargs = dict(mod.faquant_matmul_quant_kwargs, quant_format="int")
+    with pytest.raises(NotImplementedError, match="quant_format"):
+        simulated_flash_attention_forward(mod, q, k, k, None)
     with pytest.raises(NotImplementedError, match="head_dim"):
         simulated_flash_attention_forward(module(), q[..., :64], k[..., :64], k[..., :64], None)
     # an all-valid mask is the mask-free case

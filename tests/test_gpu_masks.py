@@ -196,3 +196,59 @@ def test_split_key_path_with_ranges_equals_one_pass(dev):
         cfg = OA.SimConfig(pv_normalizer_mode="quantized_same")
         ref = OA.simulated_flash_attention(q, k, v, cfg, attention_mask=mask, sliding_window=window)
         assert_close_attention(outs[1], ref, f"split ranges window={window}")
+
+
+def _dense_case(kind, batch, hq, lq, lk, seed):
+    """(torch mask, numpy mask for the oracle) of the 3-D/4-D forms of sfa:430-454."""
+    g = OI.rng(seed)
+    causal = np.tril(np.ones((lq, lk), bool), k=lk - lq)
+    if kind == "bool_causal":
+        m = np.broadcast_to(causal, (batch, 1, lq, lk)).copy()
+        return torch.from_numpy(m), m
+    if kind == "additive_heads":
+        m = (g.uniform(-3, 0, size=(batch, hq, lq, lk))).astype(np.float32)
+        m[g.random(m.shape) < 0.1] = -np.inf
+        m[g.random(m.shape) < 0.05] = np.finfo(np.float32).min
+        m[:, :, 3] = -np.inf  # a fully masked row
+        return torch.from_numpy(m), m
+    if kind == "fp16_min":
+        m = np.where(causal, 0.0, np.finfo(np.float16).min).astype(np.float16)[None, None]
+        m = np.broadcast_to(m, (batch, 1, lq, lk)).copy()
+        return torch.from_numpy(m), m
+    if kind == "bf16_longer_rows":  # more mask rows than queries: the last lq rows are used
+        full = np.tril(np.ones((lq + 7, lk), bool), k=lk - lq - 7)
+        m = np.where(full, 0.0, -1e30).astype(np.float32)[None, None]
+        m = np.broadcast_to(m, (batch, 1, lq + 7, lk)).copy()
+        t = torch.from_numpy(m).to(torch.bfloat16)
+        return t, t.float().numpy()
+    if kind == "one_row":
+        m = g.random((batch, 1, 1, lk)) > 0.2
+        return torch.from_numpy(m), m
+    if kind == "three_d":
+        m = (g.random((batch, lq, lk)) > 0.1) & causal
+        m[:, :, 0] = True
+        return torch.from_numpy(m), m
+    raise KeyError(kind)
+
+
+@pytest.mark.parametrize("kind,batch,lq,lk", [("bool_causal", 2, 300, 300), ("additive_heads", 1, 200, 260),
+                                              ("fp16_min", 1, 256, 300), ("bf16_longer_rows", 1, 130, 300),
+                                              ("one_row", 2, 1, 500), ("three_d", 2, 150, 150)])
+@pytest.mark.parametrize("softcap", [None, 2.5])
+def test_dense_masks_through_drop_in(dev, kind, batch, lq, lk, softcap):
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward
+
+    hq = 4
+    q, k, v = _qkv(lq + lk, batch, hq, 2, lq, lk)
+    tmask, nmask = _dense_case(kind, batch, hq, lq, lk, seed=lk)
+    mod = module()
+    qt, kt, vt = (to_dev(a, dev, torch.bfloat16) for a in (q, k, v))
+    out, _ = simulated_flash_attention_forward(mod, qt, kt, vt, tmask.to(dev), softcap=softcap)
+    stats = OA.new_stats()
+    ref = OA.simulated_flash_attention(q, k, v, OA.SimConfig(pv_normalizer_mode="quantized_same"),
+                                       attention_mask=nmask, softcap=softcap, dtype="bfloat16", stats=stats)
+    got = out.float().cpu().numpy()
+    assert_close_attention(got, ref, f"dense {kind} softcap={softcap}")
+    assert mod.faquant_simulated_attention_stats == stats
+    if kind == "additive_heads":
+        assert np.count_nonzero(got[:, 3]) == 0  # fully masked rows give zeros
