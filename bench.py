@@ -135,10 +135,11 @@ def cpu_baseline(cfg, rows):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    # the GPU clock settles after a few tens of ms of load: the default warmup covers that
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="qwen8b_32k", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-rows", type=int, default=512)
+    ap.add_argument("--cpu-rows", type=int, default=4096)  # about 10-15 s of CPU work at 32k
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE scaling)")
