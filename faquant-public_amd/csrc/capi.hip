@@ -67,8 +67,8 @@ void launch_act(const faq::ActQdqArgs& a, int levels, int64_t threads, hipStream
 }
 
 template <typename Tin, typename Tround>
-void launch_prep(const faq::OperandPrepArgs& a, int levels, int64_t threads, hipStream_t st) {
-  const dim3 grid(grid_for(threads));
+void launch_prep(const faq::OperandPrepArgs& a, int levels, int64_t, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((a.L + 15) / 16), static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
   if (levels == 12) hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 12>), grid, dim3(256), 0, st, a);
   else if (levels == 13) hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 13>), grid, dim3(256), 0, st, a);
   else hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 123>), grid, dim3(256), 0, st, a);
@@ -348,6 +348,7 @@ int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_
     return fail(FAQ_EINVAL, "faq_operand_prep: strides must keep 16-byte alignment");
   const int64_t rows = static_cast<int64_t>(B) * H * L;
   if (rows == 0) return FAQ_OK;
+  if (B > 65535 || H > 65535) return fail(FAQ_EUNSUP, "faq_operand_prep: at most 65535 batches and heads");
   faq::OperandPrepArgs a{};
   a.x = x;
   a.sb = sb;

@@ -477,17 +477,17 @@ struct OperandPrepArgs {
   int quant;                     // 1: HiF4 QDQ after the cast
 };
 
-// One lane owns 8 of a row's 128 values; a row spans 16 lanes.
+// One lane owns 8 of a row's 128 values; a row spans 16 lanes.  Grid: x = blocks of 16
+// positions, y = head, z = batch (no integer division in the index math).
 template <typename Tin, typename Tround, int LV>
 __global__ __launch_bounds__(256) void operand_prep_kernel(OperandPrepArgs a) {
-  const int64_t rows = static_cast<int64_t>(a.B) * a.H * a.L;
-  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const bool live = (tid >> 4) < rows;
-  const int64_t r = live ? (tid >> 4) : 0;
+  const int h = static_cast<int>(blockIdx.y);
+  const int b = static_cast<int>(blockIdx.z);
+  const int lp = static_cast<int>(blockIdx.x) * 16 + static_cast<int>(threadIdx.x >> 4);
+  const bool live = lp < a.L;
+  const int l = live ? lp : 0;
+  const int64_t r = (static_cast<int64_t>(b) * a.H + h) * a.L + l;
   const int part = threadIdx.x & 15;
-  const int l = static_cast<int>(r % a.L);
-  const int h = static_cast<int>((r / a.L) % a.H);
-  const int b = static_cast<int>(r / (static_cast<int64_t>(a.L) * a.H));
   const int d0 = part * 8;
   float v[8];
   if (live) {

@@ -252,3 +252,26 @@ def test_dense_masks_through_drop_in(dev, kind, batch, lq, lk, softcap):
     assert mod.faquant_simulated_attention_stats == stats
     if kind == "additive_heads":
         assert np.count_nonzero(got[:, 3]) == 0  # fully masked rows give zeros
+
+
+def test_attention_core_with_padding_mask_equals_drop_in(dev):
+    """qwen3.attention_core runs a 2-D mask in its fused launch; the result equals the
+    reference composition: excursion, then the drop-in with the same mask."""
+    from faquant_amd.qwen3 import attention_core, post_rope_qk_transform
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward
+
+    q, k, v = (to_dev(a, dev, torch.bfloat16) for a in _qkv(61, 3, 8, 2, 330, 330))
+    mask = torch.from_numpy(make_mask("left", 3, 330, seed=61)).to(dev)
+
+    def mk():
+        m = module()
+        m.faquant_qk_rotation = True
+        m.faquant_qk_rotation_block_size = 64
+        return m
+
+    fused_mod, ref_mod = mk(), mk()
+    got = attention_core(fused_mod, q, k, v, attention_mask=mask)
+    qr, kr = post_rope_qk_transform(q, k, rotation=True, rotation_block_size=64)
+    ref, _ = simulated_flash_attention_forward(ref_mod, qr, kr, v, mask)
+    assert torch.equal(got, ref)
+    assert fused_mod.faquant_simulated_attention_stats == ref_mod.faquant_simulated_attention_stats
