@@ -104,6 +104,7 @@ struct MaskBoundsArgs {
   int Lq, Lk, causal, window;
   int* row_lo;          // [B, Lq]
   int* row_hi;
+  int* row_blocks;      // [B, ceil(Lq / 32), 4] (see AttnArgs::row_blocks)
   uint32_t* key_bits;   // optional [B, key_words]
   int64_t key_words;
 };
@@ -165,12 +166,14 @@ __global__ __launch_bounds__(kMaskThreads) void mask_bounds_kernel(MaskBoundsArg
     for (int k = r - base[lo]; k > 0; --k) m &= m - 1u;
     return 32 * lo + __ffs(static_cast<int>(m)) - 1;
   };
-  for (int p = tid; p < a.Lq; p += kMaskThreads) {
+  const int nblk = (a.Lq + 31) / 32;
+  for (int p0 = 0; p0 < a.Lq; p0 += kMaskThreads) {
+    const int p = p0 + tid;  // every thread takes part in the 32-position summaries
     int lo = a.Lk, hi = -1;
     const int j = p + a.Lk - a.Lq;
     // without a mask every query is valid and ranks are positions (sfa:395-405), so the
     // anchor is j itself, negative for the first Lq - Lk queries when Lq > Lk
-    const bool valid = a.mask ? (j >= 0 && ((bits[j >> 5] >> (j & 31)) & 1u)) : true;
+    const bool valid = p < a.Lq && (a.mask ? (j >= 0 && ((bits[j >> 5] >> (j & 31)) & 1u)) : true);
     if (valid) {
       // (signed: __popc is unsigned, and a negative j must stay negative)
       const int64_t anchor =
@@ -187,8 +190,28 @@ __global__ __launch_bounds__(kMaskThreads) void mask_bounds_kernel(MaskBoundsArg
         hi = select(static_cast<int>(rhi));
       }
     }
-    a.row_lo[static_cast<int64_t>(b) * a.Lq + p] = lo;
-    a.row_hi[static_cast<int64_t>(b) * a.Lq + p] = hi;
+    if (p < a.Lq) {
+      a.row_lo[static_cast<int64_t>(b) * a.Lq + p] = lo;
+      a.row_hi[static_cast<int64_t>(b) * a.Lq + p] = hi;
+    }
+    // summaries of the 32 positions [32 q, 32 q + 32) held by 32 consecutive lanes
+    const bool any = lo <= hi;
+    int kb = any ? lo : a.Lk, ke = any ? hi + 1 : 0;
+    int lmax = p < a.Lq ? (any ? lo : a.Lk) : 0, hmin = p < a.Lq ? (any ? hi : -1) : a.Lk;
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) {
+      kb = min(kb, __shfl_xor(kb, m, 64));
+      ke = max(ke, __shfl_xor(ke, m, 64));
+      lmax = max(lmax, __shfl_xor(lmax, m, 64));
+      hmin = min(hmin, __shfl_xor(hmin, m, 64));
+    }
+    if ((p & 31) == 0 && p < a.Lq) {
+      int* rb = a.row_blocks + (static_cast<int64_t>(b) * nblk + (p >> 5)) * 4;
+      rb[0] = kb;
+      rb[1] = ke;
+      rb[2] = lmax;
+      rb[3] = hmin;
+    }
   }
 }
 

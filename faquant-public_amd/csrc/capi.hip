@@ -88,6 +88,31 @@ void launch_prep_vt(const faq::OperandPrepVtArgs& a, int levels, dim3 grid, hipS
   else hipLaunchKernelGGL((faq::operand_prep_vt_kernel<Tin, 123>), grid, dim3(256), 0, st, a);
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Workgroups of the attention kernel for n_items work items per split: one per CU in total
+// (a multiple of 8 when that many), never more than the items.
+int workers_for(int n_items, int nsplit) {
+  int p = std::max(1, device_cus() / std::max(1, nsplit));
+  if (p >= 8) p -= p % 8;
+  return std::max(1, std::min(n_items, p));
+}
+
+int n_items_of(const faq::AttnArgs& a) {
+  return a.B * a.Hkv * (a.Hq / a.Hkv / a.hpw) * a.n_pblocks;
+}
+
 // fp32(sqrt(n)), its fp32 reciprocal and whether it is a power of two (n = 4^k)
 faq::SqrtDiv sqrt_div(int n) {
   faq::SqrtDiv d{};
@@ -109,9 +134,11 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
                     float* row_den, int out_levels, const faq_attn_opts* opts, faq::AttnArgs& a, dim3& grid) {
   if (!q || !k || !vt || !o) return fail(FAQ_EINVAL, "%s: null operand", who);
   if (opts) {
-    const bool any = opts->row_lo || opts->row_hi || opts->key_bits;
-    if (any && !(opts->row_lo && opts->row_hi && opts->key_bits))
-      return fail(FAQ_EINVAL, "%s: row_lo, row_hi and key_bits go together", who);
+    const bool any = opts->row_lo || opts->row_hi || opts->row_blocks || opts->key_bits;
+    if (any && !(opts->row_lo && opts->row_hi && opts->row_blocks && opts->key_bits))
+      return fail(FAQ_EINVAL, "%s: row_lo, row_hi, row_blocks and key_bits go together", who);
+    if (opts->row_blocks && (reinterpret_cast<uintptr_t>(opts->row_blocks) & 15u))
+      return fail(FAQ_EINVAL, "%s: row_blocks must be 16-byte aligned", who);
     if (any && opts->key_words < 4 * ((static_cast<int64_t>(Lk) + 127) / 128))
       return fail(FAQ_EINVAL, "%s: key_words must be >= 4 * ceil(Lk / 128)", who);
     if (!(opts->softcap >= 0.0f) || opts->softcap == INFINITY)
@@ -175,6 +202,7 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
   if (opts) {
     a.row_lo = opts->row_lo;
     a.row_hi = opts->row_hi;
+    a.row_blocks = opts->row_blocks;
     a.key_bits = opts->key_bits;
     a.key_words = opts->key_words;
     a.softcap = opts->softcap;
@@ -194,7 +222,11 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
   a.row_den = row_den;
   a.out_levels = out_levels;
   a.rows_total = B * Hq * Lq;
-  grid = dim3(static_cast<unsigned>(B * Hkv * (G / hpw)), static_cast<unsigned>(a.n_pblocks));
+  // one workgroup per CU (the K/V stages fill most of its LDS) running work items back to
+  // back; P a multiple of 8 keeps item i on XCD i % 8, as a one-item-per-workgroup grid does
+  const int64_t n_items = static_cast<int64_t>(B) * Hkv * (G / hpw) * a.n_pblocks;
+  if (n_items > INT32_MAX) return fail(FAQ_EUNSUP, "%s: too many work items", who);
+  grid = dim3(static_cast<unsigned>(workers_for(static_cast<int>(n_items), 1)), 1, 1);
   return FAQ_OK;
 }
 
@@ -415,9 +447,9 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
 }
 
 int faq_attention_mask_bounds(const uint8_t* mask, int64_t mask_sb, int B, int Lq, int Lk, int causal, int window,
-                              int32_t* row_lo, int32_t* row_hi, uint32_t* key_bits, int64_t key_words,
-                              faq_stream_t stream) {
-  if (!row_lo || !row_hi) return fail(FAQ_EINVAL, "faq_attention_mask_bounds: null output");
+                              int32_t* row_lo, int32_t* row_hi, int32_t* row_blocks, uint32_t* key_bits,
+                              int64_t key_words, faq_stream_t stream) {
+  if (!row_lo || !row_hi || !row_blocks) return fail(FAQ_EINVAL, "faq_attention_mask_bounds: null output");
   if (B < 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "faq_attention_mask_bounds: bad sizes");
   if (window < 0) return fail(FAQ_EINVAL, "sliding_window must be positive");
   if (Lk > 32 * faq::kMaskMaxWords)
@@ -426,7 +458,7 @@ int faq_attention_mask_bounds(const uint8_t* mask, int64_t mask_sb, int B, int L
     return fail(FAQ_EINVAL, "faq_attention_mask_bounds: key_words must be >= 4 * ceil(Lk / 128)");
   if (mask && mask_sb < Lk) return fail(FAQ_EINVAL, "faq_attention_mask_bounds: mask row stride < Lk");
   if (B == 0 || (Lq == 0 && !key_bits)) return FAQ_OK;
-  faq::MaskBoundsArgs a{mask, mask_sb, Lq, Lk, causal != 0, window, row_lo, row_hi, key_bits, key_words};
+  faq::MaskBoundsArgs a{mask, mask_sb, Lq, Lk, causal != 0, window, row_lo, row_hi, row_blocks, key_bits, key_words};
   hipLaunchKernelGGL(faq::mask_bounds_kernel, dim3(static_cast<unsigned>(B)), dim3(faq::kMaskThreads), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("faq_attention_mask_bounds");
@@ -458,6 +490,7 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                 static_cast<long long>(workspace_bytes), static_cast<long long>(L.total));
   char* ws = static_cast<char*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  grid.x = static_cast<unsigned>(workers_for(n_items_of(a), nsplit));
   grid.z = static_cast<unsigned>(nsplit);
   a.tiles_per_split = L.tiles_per_split;
   // 1. c1-scaled tile maxima of every row

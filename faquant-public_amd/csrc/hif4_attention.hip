@@ -93,6 +93,9 @@ struct AttnArgs {
   // range (lo > hi), and key_words covers every key tile, 4 words per tile, zero past Lk.
   const int* row_lo;
   const int* row_hi;
+  const int* row_blocks;  // [B, ceil(Lq / 32), 4] per 32 positions: min lo, max hi + 1 over
+                          // non-empty rows (Lk, 0 if none), max lo, min hi over rows (an
+                          // empty row counts as lo = Lk, hi = -1)
   const uint32_t* key_bits;
   int64_t key_words;
   float scale;    // softmax scale (the softcap path applies it before the tanh)
@@ -376,6 +379,19 @@ __device__ __forceinline__ bf16x8 lds_read_at(const uint8_t* base, int byte_off)
 // logit softcap; 3: a dense additive mask (a.amask); 4: the dense mask and the softcap.
 // kMode & 8 (kDiag): the PV-normalizer probe (a.diag).  One form per
 // instantiation keeps each hot loop within its register budget.
+// kMode & 7 (kMask) 0: masks from the shapes (none, bottom-right causal, ragged tail);
+// 1: key ranges and valid-key bits (a.row_lo, a.row_hi, a.row_blocks, a.key_bits); 2: key
+// ranges and the logit softcap; 3: a dense additive mask (a.amask); 4: the dense mask and
+// the softcap.  kMode & 8 (kDiag): the PV-normalizer probe (a.diag).  One form per
+// instantiation keeps each hot loop within its register budget.
+//
+// Work items: item i = y X + x with x = (b, kvh, hg) and y the position block (causal:
+// the longest blocks first); X = B Hkv (Hq / Hkv / hpw), n_items = X n_pblocks.  Workgroup
+// wid of P = gridDim.x takes items wid, wid + P, wid + 2P, ... (every second round in
+// reverse inside each XCD's share, so large and small items pair up), and runs them as
+// one stream of key tiles: the DMA of the next item's first tile is issued during the
+// current item's last tile, and no workgroup is relaunched between items.  P = n_items
+// gives one item per workgroup.
 template <int LV, bool kQuantP, bool kSame, int kMode>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(AttnArgs a) {
@@ -383,10 +399,8 @@ void attn_fwd_kernel(AttnArgs a) {
   constexpr bool kDiag = kQuantP && (kMode & 8) != 0;
   constexpr bool kDense = kMask == 3 || kMask == 4;
   constexpr bool kSoftcap = kMask == 2 || kMask == 4;
-  // one LDS object: two K/V stages, then (key-range mode) the waves' key bounds
   constexpr bool kRanges = kMask == 1 || kMask == 2;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes + (kRanges ? 16 * 4 : 0)];
-  int* const wg_keys = reinterpret_cast<int*>(lds + 2 * kStageBytes);
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -396,94 +410,62 @@ void attn_fwd_kernel(AttnArgs a) {
 
   const int G = a.Hq / a.Hkv;
   const int hgroups = G / a.hpw;
-  const int bx = blockIdx.x;
-  const int hg = bx % hgroups;
-  const int kvh = (bx / hgroups) % a.Hkv;
-  const int b = bx / (hgroups * a.Hkv);
-  const int pb = a.causal ? (a.n_pblocks - 1 - static_cast<int>(blockIdx.y)) : static_cast<int>(blockIdx.y);
+  const int X = a.B * a.Hkv * hgroups;
+  const int n_items = X * a.n_pblocks;
   const int pos_per_wg = 32 * (8 / a.hpw);
-  const int hq = kvh * G + hg * a.hpw + (w % a.hpw);
-  const int p0w = pb * pos_per_wg + (w / a.hpw) * 32;
   const int off = a.Lk - a.Lq;  // bottom-right alignment: row p sees keys <= p + off
-
-  const int pos = p0w + n;
-  const bool row_live = pos < a.Lq;
-  const int64_t row = (static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos;
-
-  // Keys [kbeg, kend) seen by some row of this wave / workgroup.
-  int kbeg_w = 0, kbeg_wg = 0;
-  int kend_wg = a.Lk;
-  int kend_w = p0w < a.Lq ? a.Lk : 0;
-  // Key-range mode: a tile needs no per-key mask when every row of the wave sees all of
-  // it (lo_max <= key0 and key0 + 127 <= hi_min).
-  int lo_max = 0, hi_min = a.Lk - 1;
-  int rlo = a.Lk, rhi = -1;  // this row's key range
-  if (kRanges) {
-    if (row_live) {
-      rlo = a.row_lo[static_cast<int64_t>(b) * a.Lq + pos];
-      rhi = a.row_hi[static_cast<int64_t>(b) * a.Lq + pos];
-    }
-    const bool any = rlo <= rhi;
-    kbeg_w = wave_min_i32(any ? rlo : a.Lk);
-    kend_w = wave_max_i32(any ? rhi + 1 : 0);
-    lo_max = wave_max_i32(any ? rlo : a.Lk);
-    hi_min = wave_min_i32(any ? rhi : -1);
-    if (lane == 0) {
-      wg_keys[w] = kbeg_w;
-      wg_keys[8 + w] = kend_w;
-    }
-    __syncthreads();
-    kbeg_wg = wg_keys[0];
-    kend_wg = wg_keys[8];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) {
-      kbeg_wg = min(kbeg_wg, wg_keys[i]);
-      kend_wg = max(kend_wg, wg_keys[8 + i]);
-    }
-    kbeg_wg = __builtin_amdgcn_readfirstlane(kbeg_wg);
-    kend_wg = __builtin_amdgcn_readfirstlane(kend_wg);
-  } else if (a.causal) {
-    kend_wg = min(a.Lk, min(pb * pos_per_wg + pos_per_wg, a.Lq) - 1 + off + 1);
-    if (p0w < a.Lq) kend_w = max(0, min(a.Lk, min(p0w + 31, a.Lq - 1) + off + 1));
-  }
-  const int ntiles = kend_wg > 0 ? (kend_wg + kKeyTile - 1) / kKeyTile : 0;
-  const int t_first = kbeg_wg < kend_wg ? kbeg_wg / kKeyTile : ntiles;
-
   const int split = static_cast<int>(blockIdx.z);
-  const int t_lo = a.tiles_per_split ? max(t_first, min(ntiles, split * a.tiles_per_split)) : t_first;
-  const int t_hi = a.tiles_per_split ? min(ntiles, split * a.tiles_per_split + a.tiles_per_split) : ntiles;
-  bf16x8 qf[8];
-  {
-    const uint16_t* qp = a.q + b * a.q_sb + hq * a.q_sh + static_cast<int64_t>(row_live ? pos : 0) * a.q_sl + 8 * half;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      if (row_live) {
-        qf[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
-      } else {
-        qf[c] = bf16x8{};
-      }
-    }
-  }
+  const int P = static_cast<int>(gridDim.x);
+  const int wid = static_cast<int>(blockIdx.x);
+  const int nblk = (a.Lq + 31) / 32;
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  typedef const __attribute__((address_space(4))) i32x4 const_i4;
 
-  floatx16 acc[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) acc[mb] = floatx16{};
-  // a partial pass continues the reference's recurrence from the running maximum of the
-  // tiles before its split (sfa:788-806: P of tile t depends on the maximum after tile t)
-  float m_run = (a.m_start && row_live) ? a.m_start[static_cast<int64_t>(split) * a.rows_total + row] : -INFINITY;
-  float l_run = 0.0f;
-  // probe (kDiag): the other normalizer source (sum of P when l sums P^, and the reverse),
-  // rescaled like l, and per-element sums over this lane's keys: #(P^ = 0 < P),
-  // sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869)
-  float sh_run = 0.0f, dg_zero = 0.0f, dg_err = 0.0f, dg_ref = 0.0f;
+  // item of round k for this workgroup (n_items or more: none)
+  auto item_of = [&](int k) -> int {
+    const int r = (k & 1) ? ((P % 8 == 0) ? (wid % 8) + 8 * (P / 8 - 1 - wid / 8) : P - 1 - wid) : wid;
+    return k * P + r;
+  };
+  // workgroup-uniform geometry of an item: coordinates and its key-tile range
+  struct Geo {
+    int b, kvh, hg, pb, t_lo, t_hi;
+  };
+  auto geo_of = [&](int i) -> Geo {
+    Geo g;
+    const int x = i % X, y = i / X;
+    g.hg = x % hgroups;
+    g.kvh = (x / hgroups) % a.Hkv;
+    g.b = x / (hgroups * a.Hkv);
+    g.pb = a.causal ? (a.n_pblocks - 1 - y) : y;
+    int kbeg_wg = 0, kend_wg = a.Lk;
+    if (kRanges) {
+      // the rows' key ranges, summarized per 32 positions (scalar loads of a.row_blocks)
+      const_i4* blk = (const_i4*)(a.row_blocks) + static_cast<int64_t>(g.b) * nblk;
+      const int b0 = g.pb * (pos_per_wg / 32);
+      kbeg_wg = a.Lk;
+      kend_wg = 0;
+      for (int j = 0; j < pos_per_wg / 32; ++j) {
+        if (b0 + j < nblk) {
+          const i32x4 v = blk[b0 + j];
+          kbeg_wg = min(kbeg_wg, v.x);
+          kend_wg = max(kend_wg, v.y);
+        }
+      }
+    } else if (a.causal) {
+      kend_wg = min(a.Lk, min(g.pb * pos_per_wg + pos_per_wg, a.Lq) - 1 + off + 1);
+    }
+    const int ntiles = kend_wg > 0 ? (kend_wg + kKeyTile - 1) / kKeyTile : 0;
+    const int t_first = kbeg_wg < kend_wg ? kbeg_wg / kKeyTile : ntiles;
+    g.t_lo = a.tiles_per_split ? max(t_first, min(ntiles, split * a.tiles_per_split)) : t_first;
+    g.t_hi = a.tiles_per_split ? min(ntiles, split * a.tiles_per_split + a.tiles_per_split) : ntiles;
+    return g;
+  };
+
   bf16x2_t ones2;
   {
     const uint32_t one2 = 0x3F803F80u;
     __builtin_memcpy(&ones2, &one2, 4);
   }
-
-  const uint16_t* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
-  const uint16_t* vbase = a.vt + b * a.v_sb + kvh * a.v_sh;
 
   // DMA assignment: instruction j (0..3) of wave w fills tile units 512 j + 64 w + lane;
   // waves 0 and 1 also fill units 2048 + 64 w + lane (j = 4).  Unit u is piece u % 17 of
@@ -501,11 +483,14 @@ void attn_fwd_kernel(AttnArgs a) {
     kvo[j] = static_cast<uint32_t>(r * static_cast<int>(a.k_sl) + 8 * p) * 2u;
     vvo[j] = static_cast<uint32_t>(r * static_cast<int>(a.v_sd) + 8 * p) * 2u;
   }
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, a.Lk > 0 ? static_cast<uint32_t>(((a.Lk - 1) * a.k_sl + kDim) * 2) : 0u);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, static_cast<uint32_t>((127 * a.v_sd + a.v_sd) * 2));
+  const uint32_t k_bytes = a.Lk > 0 ? static_cast<uint32_t>(((a.Lk - 1) * a.k_sl + kDim) * 2) : 0u;
+  const uint32_t v_bytes = static_cast<uint32_t>((127 * a.v_sd + a.v_sd) * 2);
 
-  auto load_tile = [&](int t) {
-    uint8_t* const st = lds + (t & 1) * kStageBytes;
+  // DMA of key tile t of the item at (b, kvh) into LDS stage `stage`
+  auto load_tile = [&](int gb, int gkvh, int t, int stage) {
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.k + gb * a.k_sb + gkvh * a.k_sh, k_bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.vt + gb * a.v_sb + gkvh * a.v_sh, v_bytes);
+    uint8_t* const st = lds + stage * kStageBytes;
     const int key0 = t * kKeyTile;
     const uint32_t ksoff = static_cast<uint32_t>(key0 * a.k_sl) * 2u;
     const uint32_t vsoff = static_cast<uint32_t>(key0) * 2u;
@@ -536,298 +521,393 @@ void attn_fwd_kernel(AttnArgs a) {
   // PV: V^T row 32 mb + n, piece 8 half + c.
   const int vbyte = kTileBytes + n * (kRowUnits * 16) + half * 128;
 
-  if (t_lo < t_hi) load_tile(t_lo);
+  int k_round = 0;
+  int item = item_of(0);
+  if (item >= n_items) return;
+  Geo g = geo_of(item);
+  int step = 0;  // key tiles processed by this workgroup: LDS stage parity
+  bool issued = false;  // the DMA of the current item's first tile is in flight
 
-  for (int t = t_lo; t < t_hi; ++t) {
-    // tile t has landed for every wave; every wave is done with tile t - 1, whose stage
-    // the DMA of tile t + 1 overwrites
-    wait_all_memory();
-    __syncthreads();
-    if (t + 1 < t_hi) load_tile(t + 1);
-    const uint8_t* const st = lds + (t & 1) * kStageBytes;
-    const uint8_t* const kp = st + kbyte;
-    const uint8_t* const vp = st + vbyte;
+  for (;;) {
+    // first tile of the item, unless the previous item's last tile already fetched it (its
+    // stage was last read two steps ago, before the last barrier)
+    if (!issued && g.t_lo < g.t_hi) load_tile(g.b, g.kvh, g.t_lo, step & 1);
+    issued = false;
+    // ---- per-item state: rows, bounds, Q fragment, recurrence state
+    const int b = g.b;
+    const int hq = g.kvh * G + g.hg * a.hpw + (w % a.hpw);
+    const int p0w = g.pb * pos_per_wg + (w / a.hpw) * 32;
+    const int pos = p0w + n;
+    const bool row_live = pos < a.Lq;
+    const int64_t row = (static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos;
 
-    const int key0 = t * kKeyTile;
-    if (key0 >= kend_w || key0 + kKeyTile <= kbeg_w) continue;
-    floatx16 s[4];
+    // keys [kbeg_w, kend_w) seen by some row of this wave; a tile needs no per-key mask when
+    // every row of the wave sees all of it (lo_max <= key0 and key0 + 127 <= hi_min)
+    int kbeg_w = 0;
+    int kend_w = p0w < a.Lq ? a.Lk : 0;
+    int lo_max = 0, hi_min = a.Lk - 1;
+    int rlo = a.Lk, rhi = -1;  // this row's key range
+    if (kRanges) {
+      kend_w = 0;
+      kbeg_w = a.Lk;
+      if (p0w < a.Lq) {
+        const i32x4 v = ((const_i4*)(a.row_blocks))[static_cast<int64_t>(b) * nblk + p0w / 32];
+        kbeg_w = v.x;
+        kend_w = v.y;
+        lo_max = v.z;
+        hi_min = v.w;
+      }
+      if (row_live) {
+        rlo = a.row_lo[static_cast<int64_t>(b) * a.Lq + pos];
+        rhi = a.row_hi[static_cast<int64_t>(b) * a.Lq + pos];
+      }
+    } else if (a.causal && p0w < a.Lq) {
+      kend_w = max(0, min(a.Lk, min(p0w + 31, a.Lq - 1) + off + 1));
+    }
+
+    // Q fragment of this wave's rows: lane (n, half) holds Q[row n][16 c + 8 half .. + 7].
+    // (Fetching the next item's fragment during the last tile was tried: the conditional
+    // overwrite of a loop-carried register array costs register copies in every tile.)
+    bf16x8 qf[8];
     {
-      // ---- S^T = K Q^T, c-major (four independent accumulation chains); the K fragments
-      // of step c + 1 are read while the MFMAs of step c run
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) s[kb] = floatx16{};
-      bf16x8 kf[2][4];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) kf[0][kb] = lds_read_at(kp, kb * 16 * kRowUnits * 16);
+      const uint16_t* qp = a.q + b * a.q_sb + hq * a.q_sh + static_cast<int64_t>(row_live ? pos : 0) * a.q_sl + 8 * half;
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        if (c + 1 < 8) {
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) kf[(c + 1) & 1][kb] = lds_read_at(kp, kb * 16 * kRowUnits * 16 + (c + 1) * 32);
+        if (row_live) {
+          qf[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
+        } else {
+          qf[c] = bf16x8{};
         }
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) s[kb] = mfma32(kf[c & 1][kb], qf[c], s[kb]);
       }
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
-#pragma unroll
-      for (int c = 0; c < 7; ++c) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
     }
-    __builtin_amdgcn_sched_barrier(0);
 
-    if (kSoftcap) {
-      // sfa:725-727: scores * scale, then softcap * tanh(scores / softcap)
+    floatx16 acc[4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          // scale, then the quotient by softcap: q = t rc corrected by one fma step
-          const float t = s[kb][i] * a.scale;
-          const float q0 = t * a.softcap_rec;
-          const float q = __builtin_fmaf(__builtin_fmaf(-q0, a.softcap, t), a.softcap_rec, q0);
-          s[kb][i] = softcap_tanh(q) * a.softcap;
-        }
-    }
-    if (kDense) {
-      // sfa:430-454: scores (scaled, and softcapped above for kMask 4) plus the mask row
-      // (its columns past Lk hold -inf, which also masks the ragged tail)
-      const float* mr = a.amask + b * a.am_sb + hq * a.am_sh + (row_live ? pos : 0) * a.am_sq + key0 + 64 * half;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        float mv[16];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) *reinterpret_cast<float4*>(&mv[4 * u]) = *reinterpret_cast<const float4*>(mr + 16 * kb + 4 * u);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[kb][i] = (kSoftcap ? s[kb][i] : s[kb][i] * a.scale) + mv[i];
+    for (int mb = 0; mb < 4; ++mb) acc[mb] = floatx16{};
+    // a partial pass continues the reference's recurrence from the running maximum of the
+    // tiles before its split (sfa:788-806: P of tile t depends on the maximum after tile t)
+    float m_run = (a.m_start && row_live) ? a.m_start[static_cast<int64_t>(split) * a.rows_total + row] : -INFINITY;
+    float l_run = 0.0f;
+    // probe (kDiag): the other normalizer source (sum of P when l sums P^, and the reverse),
+    // rescaled like l, and per-element sums over this lane's keys: #(P^ = 0 < P),
+    // sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869)
+    float sh_run = 0.0f, dg_zero = 0.0f, dg_err = 0.0f, dg_ref = 0.0f;
+
+    // next item of this workgroup (its first tile is fetched during this item's last one)
+    const int next_item = item_of(k_round + 1);
+    Geo ng{};
+    if (next_item < n_items) ng = geo_of(next_item);
+
+    for (int t = g.t_lo; t < g.t_hi; ++t, ++step) {
+      // tile t has landed for every wave; every wave is done with the previous step, whose
+      // stage the DMA of the next step overwrites
+      wait_all_memory();
+      __syncthreads();
+      if (t + 1 < g.t_hi) {
+        load_tile(b, g.kvh, t + 1, (step + 1) & 1);
+      } else if (next_item < n_items && ng.t_lo < ng.t_hi) {
+        load_tile(ng.b, ng.kvh, ng.t_lo, (step + 1) & 1);
+        issued = true;
       }
-    }
-    // ---- masks (ragged key tail, causal diagonal, key ranges and invalid keys)
-    if (kRanges) {
-      // the tile's four valid-key words, loaded as scalars (wave-uniform address): no wait
-      // on the vector-memory counter, which the in-flight DMA of the next tile also holds
-      // (the constant address space: this kernel never writes key_bits)
-      typedef const __attribute__((address_space(4))) uint32_t const_u32;
-      const_u32* kw = (const_u32*)(a.key_bits + b * a.key_words + (key0 >> 5));
-      const uint32_t kw0 = kw[0], kw1 = kw[1], kw2 = kw[2], kw3 = kw[3];
-      if (!(lo_max <= key0 && key0 + kKeyTile - 1 <= hi_min) || (kw0 & kw1 & kw2 & kw3) != ~0u) {
-        const bool hi_half = half != 0;
-        const int base = key0 + (hi_half ? 64 : 0);
-        const uint32_t m0 = bit_range32(rlo - base, rhi - base) & (hi_half ? kw2 : kw0);
-        const uint32_t m1 = bit_range32(rlo - base - 32, rhi - base - 32) & (hi_half ? kw3 : kw1);
-        // keep = all ones for an allowed key (sign-extended bit), else -inf: bfe + bfi
+      do {
+        const uint8_t* const st = lds + (step & 1) * kStageBytes;
+        const uint8_t* const kp = st + kbyte;
+        const uint8_t* const vp = st + vbyte;
+
+        const int key0 = t * kKeyTile;
+        if (key0 >= kend_w || key0 + kKeyTile <= kbeg_w) continue;
+        floatx16 s[4];
+        {
+          // ---- S^T = K Q^T, c-major (four independent accumulation chains); the K fragments
+          // of step c + 1 are read while the MFMAs of step c run
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) s[kb] = floatx16{};
+          bf16x8 kf[2][4];
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) kf[0][kb] = lds_read_at(kp, kb * 16 * kRowUnits * 16);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            if (c + 1 < 8) {
+#pragma unroll
+              for (int kb = 0; kb < 4; ++kb) kf[(c + 1) & 1][kb] = lds_read_at(kp, kb * 16 * kRowUnits * 16 + (c + 1) * 32);
+            }
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) s[kb] = mfma32(kf[c & 1][kb], qf[c], s[kb]);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+          for (int c = 0; c < 7; ++c) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        if (kSoftcap) {
+          // sfa:725-727: scores * scale, then softcap * tanh(scores / softcap)
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              // scale, then the quotient by softcap: q = t rc corrected by one fma step
+              const float t = s[kb][i] * a.scale;
+              const float q0 = t * a.softcap_rec;
+              const float q = __builtin_fmaf(__builtin_fmaf(-q0, a.softcap, t), a.softcap_rec, q0);
+              s[kb][i] = softcap_tanh(q) * a.softcap;
+            }
+        }
+        if (kDense) {
+          // sfa:430-454: scores (scaled, and softcapped above for kMask 4) plus the mask row
+          // (its columns past Lk hold -inf, which also masks the ragged tail)
+          const float* mr = a.amask + b * a.am_sb + hq * a.am_sh + (row_live ? pos : 0) * a.am_sq + key0 + 64 * half;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) {
+            float mv[16];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) *reinterpret_cast<float4*>(&mv[4 * u]) = *reinterpret_cast<const float4*>(mr + 16 * kb + 4 * u);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[kb][i] = (kSoftcap ? s[kb][i] : s[kb][i] * a.scale) + mv[i];
+          }
+        }
+        // ---- masks (ragged key tail, causal diagonal, key ranges and invalid keys)
+        if (kRanges) {
+          // the tile's four valid-key words, loaded as scalars (wave-uniform address): no wait
+          // on the vector-memory counter, which the in-flight DMA of the next tile also holds
+          // (the constant address space: this kernel never writes key_bits)
+          typedef const __attribute__((address_space(4))) uint32_t const_u32;
+          const_u32* kw = (const_u32*)(a.key_bits + b * a.key_words + (key0 >> 5));
+          const uint32_t kw0 = kw[0], kw1 = kw[1], kw2 = kw[2], kw3 = kw[3];
+          if (!(lo_max <= key0 && key0 + kKeyTile - 1 <= hi_min) || (kw0 & kw1 & kw2 & kw3) != ~0u) {
+            const bool hi_half = half != 0;
+            const int base = key0 + (hi_half ? 64 : 0);
+            const uint32_t m0 = bit_range32(rlo - base, rhi - base) & (hi_half ? kw2 : kw0);
+            const uint32_t m1 = bit_range32(rlo - base - 32, rhi - base - 32) & (hi_half ? kw3 : kw1);
+            // keep = all ones for an allowed key (sign-extended bit), else -inf: bfe + bfi
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                const int j = 16 * kb + i;
+                const uint32_t keep = static_cast<uint32_t>(
+                    __builtin_amdgcn_sbfe(static_cast<int>(j < 32 ? m0 : m1), static_cast<uint32_t>(j & 31), 1u));
+                s[kb][i] = __uint_as_float((__float_as_uint(s[kb][i]) & keep) | (0xFF800000u & ~keep));
+              }
+          }
+        } else if (kMask == 0 && ((key0 + kKeyTile > a.Lk) || (a.causal && key0 + kKeyTile - 1 > p0w + off))) {
+          const int lim = a.causal ? min(a.Lk - 1, pos + off) : a.Lk - 1;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              if (key0 + 64 * half + 16 * kb + i > lim) s[kb][i] = -INFINITY;
+        }
+        // ---- online softmax in the log2 domain
+        float mx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int j = 16 * kb + i;
-            const uint32_t keep = static_cast<uint32_t>(
-                __builtin_amdgcn_sbfe(static_cast<int>(j < 32 ? m0 : m1), static_cast<uint32_t>(j & 31), 1u));
-            s[kb][i] = __uint_as_float((__float_as_uint(s[kb][i]) & keep) | (0xFF800000u & ~keep));
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+        const float mx_row = halves_max(mx);
+        if (a.mx_out) {
+          // maxima pass: the tile's c1-scaled row maximum only
+          if (row_live && half == 0) a.mx_out[row * a.mx_stride + t] = mx_row * a.c1;
+          continue;
+        }
+        const float m_new = fmaxf(m_run, mx_row * a.c1);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float nm = -m_use;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        m_run = m_new;
+        if (__ballot(alpha != 1.0f) != 0) {
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
+          l_run *= alpha;
+          if (kDiag) sh_run *= alpha;
+        }
+        // ---- P, its HiF4 QDQ and the row sum, one 8-key chunk at a time; chunk c of this lane
+        // is keys 64 half + 8c .. 8c+7, the B operand of PV k-chunk c.
+        PQuant pq;
+        if (kQuantP) {
+          // group maximum = P of the lane's largest score (same fma and exp2)
+          pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
+        }
+        float rowsum = 0.0f, shadow = 0.0f;
+        // Software pipeline over the eight 8-key chunks: iteration c computes chunk c's P^
+        // (VALU) while the MFMAs of chunk c - 1 issue one at a time between those VALU
+        // instructions.
+        bf16x8 pprev, plprev;
+#pragma unroll
+        for (int c = 0; c <= 8; ++c) {
+          bf16x8 va[4];
+          if (c >= 1) {
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) va[mb] = lds_read_at(vp, mb * 32 * kRowUnits * 16 + (c - 1) * 16);
           }
+          bf16x8 pcur, plcur;
+          if (c < 8) {
+            float pc[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
+            if (!(kQuantP && kSame)) {
+              // the normalizer sums P (unquantized mode, or no P quantization)
+#pragma unroll
+              for (int j = 0; j < 8; ++j) rowsum += pc[j];
+            }
+            if (kQuantP) {
+              float pu[8];
+              if (kDiag) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                  pu[j] = pc[j];
+                  if (kSame) shadow += pc[j];
+                }
+              }
+              pquant8<LV>(pc, pq);
+              pcur = pack8<true>(pc);
+              if (kSame || kDiag) {
+                uint32_t wv[4];
+                __builtin_memcpy(wv, &pcur, 16);
+                float& qsum = kSame ? rowsum : shadow;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                  bf16x2_t pr;
+                  __builtin_memcpy(&pr, &wv[i], 4);
+                  qsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, qsum, false);
+                }
+              }
+              if (kDiag) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                  const float d = pc[j] - pu[j];
+                  dg_err = __builtin_fmaf(d, d, dg_err);
+                  dg_ref = __builtin_fmaf(pu[j], pu[j], dg_ref);
+                  dg_zero += (pc[j] == 0.0f && pu[j] > 0.0f) ? 1.0f : 0.0f;
+                }
+              }
+            } else {
+              // Unquantized P is not exact in bf16: it goes in as hi + lo bf16 parts
+              // (16 significant bits) so PV keeps the fp32-operand accuracy of the reference.
+              float r[8];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) r[j] = pc[j] - bf16_rne(pc[j]);
+              pcur = pack8<false>(pc);
+              plcur = pack8<false>(r);
+            }
+          }
+          if (c >= 1) {
+            // ---- O^T += V^T P^T for chunk c - 1
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+              acc[mb] = mfma32(va[mb], pprev, acc[mb]);
+              if (!kQuantP) acc[mb] = mfma32(va[mb], plprev, acc[mb]);
+            }
+            // issue order: the four LDS reads, ~20 VALU (read latency), then one MFMA per
+            // ~12 VALU instructions
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            if (c < 8) {
+              __builtin_amdgcn_sched_group_barrier(0x002, 20, 0);
+#pragma unroll
+              for (int i = 0; i < (kQuantP ? 4 : 8); ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kQuantP ? 12 : 6, 0);
+              }
+              __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
+            } else {
+              __builtin_amdgcn_sched_group_barrier(0x008, kQuantP ? 4 : 8, 0);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          pprev = pcur;
+          plprev = plcur;
+        }
+        l_run += halves_sum(rowsum);
+        if (kDiag) sh_run += halves_sum(shadow);
+      } while (false);
+    }
+
+    // ---- epilogue of the item
+    if (row_live && !a.mx_out) {
+      if (a.part_o) {
+        // partial pass: unnormalized O^T column of this row, its l and running maximum
+        float* po = a.part_o + (static_cast<int64_t>(split) * a.rows_total + row) * kDim;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<float4*>(po + 32 * mb + 8 * j + 4 * half) =
+                make_float4(acc[mb][4 * j], acc[mb][4 * j + 1], acc[mb][4 * j + 2], acc[mb][4 * j + 3]);
+        if (half == 0) {
+          float* lm = a.part_lm + (static_cast<int64_t>(split) * a.rows_total + row) * 2;
+          lm[0] = l_run;
+          lm[1] = m_run;
+        }
+      } else {
+      const float l = l_run;
+      if (kDiag) {
+        // per row: sum P^, sum P, #(P^ = 0 < P), sum (P^ - P)^2, sum P^2
+        const float zero = halves_sum(dg_zero), err = halves_sum(dg_err), ref = halves_sum(dg_ref);
+        if (half == 0) {
+          float* dg = a.diag + row * 5;
+          dg[0] = kSame ? l : sh_run;
+          dg[1] = kSame ? sh_run : l;
+          dg[2] = zero;
+          dg[3] = err;
+          dg[4] = ref;
+        }
       }
-    } else if (kMask == 0 && ((key0 + kKeyTile > a.Lk) || (a.causal && key0 + kKeyTile - 1 > p0w + off))) {
-      const int lim = a.causal ? min(a.Lk - 1, pos + off) : a.Lk - 1;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (key0 + 64 * half + 16 * kb + i > lim) s[kb][i] = -INFINITY;
-    }
-    // ---- online softmax in the log2 domain
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-    const float mx_row = halves_max(mx);
-    if (a.mx_out) {
-      // maxima pass: the tile's c1-scaled row maximum only
-      if (row_live && half == 0) a.mx_out[row * a.mx_stride + t] = mx_row * a.c1;
-      continue;
-    }
-    const float m_new = fmaxf(m_run, mx_row * a.c1);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float nm = -m_use;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
-    if (__ballot(alpha != 1.0f) != 0) {
+      const float inv_guard = fmaxf(l, 1.17549435e-38f);
+      // acc / l as the reference divides: rl = RN(1 / l), then one correction step from
+      // q0 = RN(acc rl) gives the correctly rounded quotient (Markstein's theorem)
+      const float rl = 1.0f / inv_guard;
+      if (a.row_den && half == 0) a.row_den[(static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos] = l;
+      // this lane's part of the output row: element 4 half, then constant offsets 32 mb + 8 j
+      const int64_t orow = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + 4 * half;
+      char* const orow_p = static_cast<char*>(a.o) + orow * (a.o_f32 ? 4 : 2);
+      // o = acc / l (0 for rows that saw no key), in the output dtype
+      float val[4][4][4];
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
-      l_run *= alpha;
-      if (kDiag) sh_run *= alpha;
-    }
-    // ---- P, its HiF4 QDQ and the row sum, one 8-key chunk at a time; chunk c of this lane
-    // is keys 64 half + 8c .. 8c+7, the B operand of PV k-chunk c.
-    PQuant pq;
-    if (kQuantP) {
-      // group maximum = P of the lane's largest score (same fma and exp2)
-      pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
-    }
-    float rowsum = 0.0f, shadow = 0.0f;
-    // Software pipeline over the eight 8-key chunks: iteration c computes chunk c's P^
-    // (VALU) while the MFMAs of chunk c - 1 issue one at a time between those VALU
-    // instructions.
-    bf16x8 pprev, plprev;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int c = 0; c <= 8; ++c) {
-      bf16x8 va[4];
-      if (c >= 1) {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) va[mb] = lds_read_at(vp, mb * 32 * kRowUnits * 16 + (c - 1) * 16);
-      }
-      bf16x8 pcur, plcur;
-      if (c < 8) {
-        float pc[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
-        if (!(kQuantP && kSame)) {
-          // the normalizer sums P (unquantized mode, or no P quantization)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) rowsum += pc[j];
-        }
-        if (kQuantP) {
-          float pu[8];
-          if (kDiag) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              pu[j] = pc[j];
-              if (kSame) shadow += pc[j];
-            }
+          for (int r = 0; r < 4; ++r) {
+            const float xa = acc[mb][4 * j + r];
+            const float q0 = xa * rl;
+            const float x = l > 0.0f ? __builtin_fmaf(__builtin_fmaf(-q0, inv_guard, xa), rl, q0) : 0.0f;
+            val[mb][j][r] = a.o_f32 ? x : bf16_round_hw(x);
           }
-          pquant8<LV>(pc, pq);
-          pcur = pack8<true>(pc);
-          if (kSame || kDiag) {
-            uint32_t wv[4];
-            __builtin_memcpy(wv, &pcur, 16);
-            float& qsum = kSame ? rowsum : shadow;
+      // the o_proj-input QDQ of the output row (qwen3.py:167-171), on the output-dtype values
+      if (a.out_levels == 123) qdq_out_row<123>(val, half);
+      else if (a.out_levels == 12) qdq_out_row<12>(val, half);
+      else if (a.out_levels == 13) qdq_out_row<13>(val, half);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              bf16x2_t pr;
-              __builtin_memcpy(&pr, &wv[i], 4);
-              qsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, qsum, false);
-            }
+      for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = 32 * mb + 8 * j;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = val[mb][j][r];
+          if (a.o_f32) {
+            *reinterpret_cast<float4*>(orow_p + d * 4) = make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            // the values are bf16 already (rounded above, or HiF4 values): pack the upper halves
+            const uint32_t w0 = __builtin_amdgcn_perm(__float_as_uint(v[1]), __float_as_uint(v[0]), 0x07060302u);
+            const uint32_t w1 = __builtin_amdgcn_perm(__float_as_uint(v[3]), __float_as_uint(v[2]), 0x07060302u);
+            *reinterpret_cast<uint2*>(orow_p + d * 2) = make_uint2(w0, w1);
           }
-          if (kDiag) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const float d = pc[j] - pu[j];
-              dg_err = __builtin_fmaf(d, d, dg_err);
-              dg_ref = __builtin_fmaf(pu[j], pu[j], dg_ref);
-              dg_zero += (pc[j] == 0.0f && pu[j] > 0.0f) ? 1.0f : 0.0f;
-            }
-          }
-        } else {
-          // Unquantized P is not exact in bf16: it goes in as hi + lo bf16 parts
-          // (16 significant bits) so PV keeps the fp32-operand accuracy of the reference.
-          float r[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) r[j] = pc[j] - bf16_rne(pc[j]);
-          pcur = pack8<false>(pc);
-          plcur = pack8<false>(r);
         }
       }
-      if (c >= 1) {
-        // ---- O^T += V^T P^T for chunk c - 1
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          acc[mb] = mfma32(va[mb], pprev, acc[mb]);
-          if (!kQuantP) acc[mb] = mfma32(va[mb], plprev, acc[mb]);
-        }
-        // issue order: the four LDS reads, ~20 VALU (read latency), then one MFMA per
-        // ~12 VALU instructions
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-        if (c < 8) {
-          __builtin_amdgcn_sched_group_barrier(0x002, 20, 0);
-#pragma unroll
-          for (int i = 0; i < (kQuantP ? 4 : 8); ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, kQuantP ? 12 : 6, 0);
-          }
-          __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
-        } else {
-          __builtin_amdgcn_sched_group_barrier(0x008, kQuantP ? 4 : 8, 0);
-        }
       }
-      __builtin_amdgcn_sched_barrier(0);
-      pprev = pcur;
-      plprev = plcur;
-    }
-    l_run += halves_sum(rowsum);
-    if (kDiag) sh_run += halves_sum(shadow);
-  }
 
-  if (!row_live || a.mx_out) return;
-  if (a.part_o) {
-    // partial pass: unnormalized O^T column of this row, its l and running maximum
-    float* po = a.part_o + (static_cast<int64_t>(split) * a.rows_total + row) * kDim;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<float4*>(po + 32 * mb + 8 * j + 4 * half) =
-            make_float4(acc[mb][4 * j], acc[mb][4 * j + 1], acc[mb][4 * j + 2], acc[mb][4 * j + 3]);
-    if (half == 0) {
-      float* lm = a.part_lm + (static_cast<int64_t>(split) * a.rows_total + row) * 2;
-      lm[0] = l_run;
-      lm[1] = m_run;
     }
-    return;
-  }
-  const float l = l_run;
-  if (kDiag) {
-    // per row: sum P^, sum P, #(P^ = 0 < P), sum (P^ - P)^2, sum P^2
-    const float zero = halves_sum(dg_zero), err = halves_sum(dg_err), ref = halves_sum(dg_ref);
-    if (half == 0) {
-      float* dg = a.diag + row * 5;
-      dg[0] = kSame ? l : sh_run;
-      dg[1] = kSame ? sh_run : l;
-      dg[2] = zero;
-      dg[3] = err;
-      dg[4] = ref;
-    }
-  }
-  const float inv_guard = fmaxf(l, 1.17549435e-38f);
-  if (a.row_den && half == 0) a.row_den[(static_cast<int64_t>(b) * a.Hq + hq) * a.Lq + pos] = l;
-  char* obase = static_cast<char*>(a.o);
-  const int64_t orow = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl;
-  // o = acc / l (0 for rows that saw no key), in the output dtype
-  float val[4][4][4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float x = l > 0.0f ? acc[mb][4 * j + r] / inv_guard : 0.0f;
-        val[mb][j][r] = a.o_f32 ? x : bf16_rne(x);
-      }
-  // the o_proj-input QDQ of the output row (qwen3.py:167-171), on the output-dtype values
-  if (a.out_levels == 123) qdq_out_row<123>(val, half);
-  else if (a.out_levels == 12) qdq_out_row<12>(val, half);
-  else if (a.out_levels == 13) qdq_out_row<13>(val, half);
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = 32 * mb + 8 * j + 4 * half;
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = val[mb][j][r];
-      if (a.o_f32) {
-        *reinterpret_cast<float4*>(obase + (orow + d) * 4) = make_float4(v[0], v[1], v[2], v[3]);
-      } else {
-        const uint32_t w0 = static_cast<uint32_t>(f32_to_bf16_bits_rne(v[0])) |
-                            (static_cast<uint32_t>(f32_to_bf16_bits_rne(v[1])) << 16);
-        const uint32_t w1 = static_cast<uint32_t>(f32_to_bf16_bits_rne(v[2])) |
-                            (static_cast<uint32_t>(f32_to_bf16_bits_rne(v[3])) << 16);
-        *reinterpret_cast<uint2*>(obase + (orow + d) * 2) = make_uint2(w0, w1);
-      }
-    }
+    ++k_round;
+    item = next_item;
+    if (item >= n_items) break;
+    g = ng;
   }
 }
 

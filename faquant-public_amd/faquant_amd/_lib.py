@@ -34,6 +34,7 @@ class AttnOpts(ctypes.Structure):
     _fields_ = [
         ("row_lo", _vp),
         ("row_hi", _vp),
+        ("row_blocks", _vp),
         ("key_bits", _vp),
         ("key_words", _c_i64),
         ("softcap", _c_float),
@@ -81,7 +82,7 @@ _SIGNATURES = {
         _c_int,
     ),
     "faq_attention_mask_bounds": (
-        [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_i64, _vp],
+        [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _vp],
         _c_int,
     ),
     "faq_attention_fwd": (

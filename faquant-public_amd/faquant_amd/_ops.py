@@ -227,9 +227,10 @@ class KeyRanges:
     query position p of batch b sees the keys k in [row_lo[b, p], row_hi[b, p]] whose bit
     k % 32 of key_bits[b, k // 32] is set."""
 
-    row_lo: torch.Tensor    # int32 [B, Lq]
-    row_hi: torch.Tensor    # int32 [B, Lq]
-    key_bits: torch.Tensor  # int32 [B, key_words], key_words = 4 * ceil(Lk / 128)
+    row_lo: torch.Tensor      # int32 [B, Lq]
+    row_hi: torch.Tensor      # int32 [B, Lq]
+    row_blocks: torch.Tensor  # int32 [B, ceil(Lq / 32), 4]: per-32-position summaries
+    key_bits: torch.Tensor    # int32 [B, key_words], key_words = 4 * ceil(Lk / 128)
 
 
 def attention_key_ranges(
@@ -266,15 +267,17 @@ def attention_key_ranges(
     words = 4 * max(1, -(-key_length // KEY_TILE))
     row_lo = torch.empty((batch, query_length), device=device, dtype=torch.int32)
     row_hi = torch.empty_like(row_lo)
+    row_blocks = torch.empty((batch, -(-query_length // 32), 4), device=device, dtype=torch.int32)
     key_bits = torch.empty((batch, words), device=device, dtype=torch.int32)
     _lib.check(
         lib.faq_attention_mask_bounds(
             _lib.ptr(mask), mask.stride(0) if mask is not None and batch > 1 else key_length,
             batch, query_length, key_length, int(bool(causal)), int(window or 0),
-            row_lo.data_ptr(), row_hi.data_ptr(), key_bits.data_ptr(), words, _lib.stream_ptr(device),
+            row_lo.data_ptr(), row_hi.data_ptr(), row_blocks.data_ptr(), key_bits.data_ptr(), words,
+            _lib.stream_ptr(device),
         )
     )
-    return KeyRanges(row_lo, row_hi, key_bits)
+    return KeyRanges(row_lo, row_hi, row_blocks, key_bits)
 
 
 def dense_attention_mask(mask: torch.Tensor, batch: int, heads: int, query_length: int,
@@ -321,6 +324,7 @@ def _attn_opts(ranges: KeyRanges | None, softcap: float | None, pv_probe: torch.
     if ranges is not None:
         opts.row_lo = ranges.row_lo.data_ptr()
         opts.row_hi = ranges.row_hi.data_ptr()
+        opts.row_blocks = ranges.row_blocks.data_ptr()
         opts.key_bits = ranges.key_bits.data_ptr()
         opts.key_words = ranges.key_bits.shape[-1]
     opts.softcap = float(softcap or 0.0)

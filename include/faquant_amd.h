@@ -146,7 +146,12 @@ int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int
  *   key_bits        [row_lo, row_hi] (inclusive, within [0, Lk - 1]; row_lo > row_hi: no
  *                   key, output row 0) whose bit k % 32 of key_bits word k / 32 is set;
  *                   key_bits is uint32 [B, key_words], key_words >= 4 * ceil(Lk / 128), zero
- *                   past Lk.  All three or none; none: the `causal` argument decides.
+ *                   past Lk.
+ *   row_blocks      int32 [B, ceil(Lq / 32), 4], 16-byte aligned: per 32 positions, the
+ *                   minimum row_lo and maximum row_hi + 1 of the non-empty rows (Lk and 0
+ *                   if none), the maximum row_lo and minimum row_hi of all rows (an empty
+ *                   row counting as Lk and -1).  row_lo, row_hi, row_blocks and key_bits:
+ *                   all or none; none: the `causal` argument decides.
  *   softcap         > 0: scores become softcap * tanh(scale * s / softcap) before masking
  *                   (simulated_flash_attention.py:725-727; needs the key ranges); 0: off.
  *   dense_mask      fp32 additive mask (3-D/4-D masks, simulated_flash_attention.py:430-454):
@@ -166,6 +171,7 @@ int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int
 typedef struct faq_attn_opts {
   const int32_t* row_lo;
   const int32_t* row_hi;
+  const int32_t* row_blocks;
   const uint32_t* key_bits;
   int64_t key_words;
   float softcap;
@@ -181,12 +187,12 @@ typedef struct faq_attn_opts {
  * query position p is valid when mask column p + Lk - Lq is (invalid when that column is
  * < 0), and it sees the valid keys whose rank among valid keys is <= its own column's rank
  * (causal), > rank - window (window > 0) and < rank + window (window > 0, not causal).
- * Writes row_lo / row_hi [B, Lq] and, if key_bits is non-NULL, key_bits [B, key_words]
- * (key_words >= 4 * ceil(Lk / 128)).  Lk <= 524288.
+ * Writes row_lo / row_hi [B, Lq], row_blocks [B, ceil(Lq / 32), 4] and, if key_bits is
+ * non-NULL, key_bits [B, key_words] (key_words >= 4 * ceil(Lk / 128)).  Lk <= 524288.
  */
 int faq_attention_mask_bounds(const uint8_t* mask, int64_t mask_sb, int B, int Lq, int Lk, int causal, int window,
-                              int32_t* row_lo, int32_t* row_hi, uint32_t* key_bits, int64_t key_words,
-                              faq_stream_t stream);
+                              int32_t* row_lo, int32_t* row_hi, int32_t* row_blocks, uint32_t* key_bits,
+                              int64_t key_words, faq_stream_t stream);
 
 /*
  * HiF4 QK/PV flash attention forward, head_dim 128, key tiles of 128 in ascending

@@ -95,11 +95,11 @@ def test_validation_statuses_without_device_work(lib):
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,
                                1, 2, 2, 1, 1, 1, 0.1, 1, 123, 1, None, 0, ctypes.byref(opts), None)
     assert rc == _lib.EINVAL and "non-negative" in lib.faq_last_error().decode()
-    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 4, 1, 0, None, None, None, 0, None) == _lib.EINVAL
-    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 4, 1, -2, p16, p16, None, 0, None) == _lib.EINVAL
+    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 4, 1, 0, None, None, None, None, 0, None) == _lib.EINVAL
+    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 4, 1, -2, p16, p16, p16, None, 0, None) == _lib.EINVAL
     assert "sliding_window" in lib.faq_last_error().decode()
-    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 1 << 20, 1, 0, p16, p16, None, 0, None) == _lib.EUNSUP
-    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 300, 1, 0, p16, p16, p16, 8, None) == _lib.EINVAL
+    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 1 << 20, 1, 0, p16, p16, p16, None, 0, None) == _lib.EUNSUP
+    assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 300, 1, 0, p16, p16, p16, p16, 8, None) == _lib.EINVAL
     assert "key_words" in lib.faq_last_error().decode()
 
 
