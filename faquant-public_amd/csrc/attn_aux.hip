@@ -9,9 +9,13 @@ namespace faq {
 // Split-key attention (decode and other short grids): after the maxima pass, the running
 // maximum before split j of row r is the maximum of the c1-scaled tile maxima of its first
 // t_lo(j) tiles (-inf if none), restricted to the tiles the row sees.
+constexpr int kScanThreads = 256;
+constexpr int kScanMaxTiles = 16384;  // the row's tile maxima in LDS (64 KiB)
+
 struct SplitScanArgs {
   const float* mx;     // [rows_total, mx_stride]
   int mx_stride;
+  int ntiles;          // key tiles of Lk (<= kScanMaxTiles)
   float* m_start;      // [nsplit, rows_total]
   int rows_total;
   int nsplit;
@@ -21,11 +25,15 @@ struct SplitScanArgs {
   const int* row_hi;
 };
 
-__global__ __launch_bounds__(256) void split_scan_kernel(SplitScanArgs a) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= static_cast<int64_t>(a.rows_total) * a.nsplit) return;
-  const int row = static_cast<int>(i % a.rows_total);
-  const int split = static_cast<int>(i / a.rows_total);
+// One workgroup per row: the row's tile maxima (-inf outside the tiles it sees) go to LDS in
+// one coalesced pass, thread j takes the maximum of split j's tiles, and a Hillis-Steele scan
+// over the splits (in chunks of 256 with a carry) gives each split the exclusive prefix
+// maximum.  The maxima are exact, so the result equals a serial scan.
+__global__ __launch_bounds__(kScanThreads) void split_scan_kernel(SplitScanArgs a) {
+  extern __shared__ float tm[];  // [ntiles]
+  __shared__ float sm[kScanThreads];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
   const int pos = row % a.Lq;
   // key tiles [t0, t1) of this row; the maxima pass wrote every one of them
   int t0 = 0, t1;
@@ -38,15 +46,37 @@ __global__ __launch_bounds__(256) void split_scan_kernel(SplitScanArgs a) {
     const int kend = a.causal ? min(a.Lk, max(0, pos + a.Lk - a.Lq + 1)) : a.Lk;
     t1 = (kend + kKeyTile - 1) / kKeyTile;
   }
-  const int upto = min(t1, split * a.tiles_per_split);
-  float m = -INFINITY;
-  for (int t = t0; t < upto; ++t) m = fmaxf(m, a.mx[static_cast<int64_t>(row) * a.mx_stride + t]);
-  a.m_start[i] = m;
+  const float* mr = a.mx + static_cast<int64_t>(row) * a.mx_stride;
+  for (int t = tid; t < a.ntiles; t += kScanThreads) tm[t] = (t >= t0 && t < t1) ? mr[t] : -INFINITY;
+  __syncthreads();
+  float carry = -INFINITY;
+  for (int j0 = 0; j0 < a.nsplit; j0 += kScanThreads) {
+    const int j = j0 + tid;
+    float m = -INFINITY;
+    if (j < a.nsplit) {
+      const int e = min(a.ntiles, (j + 1) * a.tiles_per_split);
+      for (int t = j * a.tiles_per_split; t < e; ++t) m = fmaxf(m, tm[t]);
+    }
+    sm[tid] = m;
+    __syncthreads();
+    for (int d = 1; d < kScanThreads; d <<= 1) {
+      const float o = tid >= d ? sm[tid - d] : -INFINITY;
+      __syncthreads();
+      sm[tid] = fmaxf(sm[tid], o);
+      __syncthreads();
+    }
+    if (j < a.nsplit) a.m_start[static_cast<int64_t>(j) * a.rows_total + row] = fmaxf(carry, tid > 0 ? sm[tid - 1] : -INFINITY);
+    carry = fmaxf(carry, sm[kScanThreads - 1]);
+    __syncthreads();
+  }
 }
 
 // O = sum_j 2^(m_j - M) O_j / sum_j 2^(m_j - M) l_j with M the row's final running maximum;
 // the per-split recurrences already used the reference's maxima, so only the fp32 order of
 // the O and l sums differs from one pass.
+constexpr int kCombineThreads = 256;
+constexpr int kCombineMaxSplits = 4096;
+
 struct SplitCombineArgs {
   const float* part_o;   // [nsplit, rows_total, 128]
   const float* part_lm;  // [nsplit, rows_total, 2]
@@ -58,30 +88,71 @@ struct SplitCombineArgs {
   float* row_den;        // optional [rows_total]
 };
 
-__global__ __launch_bounds__(128) void split_combine_kernel(SplitCombineArgs a) {
+// One workgroup per row.  The split weights w_j = 2^(m_j - M) (0 for an empty split) go to
+// LDS; threads (g, d), g = tid / 128, sum w_j O_j[d] over the splits j = g mod 2 with eight
+// loads in flight, and the two halves and the weighted l sums are added in a fixed order
+// (deterministic results).
+__global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCombineArgs a) {
+  __shared__ float wsh[kCombineMaxSplits];
+  __shared__ float red[kCombineThreads];
+  __shared__ float half_acc[kDim];
   const int row = blockIdx.x;
-  const int d = threadIdx.x;
-  float mmax = -INFINITY;
-  for (int j = 0; j < a.nsplit; ++j) mmax = fmaxf(mmax, a.part_lm[(static_cast<int64_t>(j) * a.rows_total + row) * 2 + 1]);
-  float l = 0.0f, acc = 0.0f;
-  if (mmax != -INFINITY) {
-    for (int j = 0; j < a.nsplit; ++j) {
-      const int64_t r = static_cast<int64_t>(j) * a.rows_total + row;
-      const float lj = a.part_lm[r * 2];
-      if (lj == 0.0f) continue;
-      const float w = __builtin_amdgcn_exp2f(a.part_lm[r * 2 + 1] - mmax);
-      l = __builtin_fmaf(w, lj, l);
-      acc = __builtin_fmaf(w, a.part_o[r * kDim + d], acc);
-    }
+  const int tid = threadIdx.x;
+  // M: the maximum over the splits
+  float mloc = -INFINITY;
+  for (int j = tid; j < a.nsplit; j += kCombineThreads)
+    mloc = fmaxf(mloc, a.part_lm[(static_cast<int64_t>(j) * a.rows_total + row) * 2 + 1]);
+  red[tid] = mloc;
+  __syncthreads();
+  for (int d = kCombineThreads / 2; d > 0; d >>= 1) {
+    if (tid < d) red[tid] = fmaxf(red[tid], red[tid + d]);
+    __syncthreads();
   }
-  const int pos = row % a.Lq;
-  const int hq = (row / a.Lq) % a.Hq;
-  const int b = row / (a.Lq * a.Hq);
-  if (a.row_den && d == 0) a.row_den[row] = l;
-  const float v = l > 0.0f ? acc / fmaxf(l, 1.17549435e-38f) : 0.0f;
-  const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + d;
-  if (a.o_f32) static_cast<float*>(a.o)[off] = v;
-  else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
+  const float mmax = red[0];
+  __syncthreads();
+  // weights and the weighted l terms
+  float lloc = 0.0f;
+  for (int j = tid; j < a.nsplit; j += kCombineThreads) {
+    const int64_t r = static_cast<int64_t>(j) * a.rows_total + row;
+    const float lj = a.part_lm[r * 2];
+    const float w = (mmax == -INFINITY || lj == 0.0f) ? 0.0f : __builtin_amdgcn_exp2f(a.part_lm[r * 2 + 1] - mmax);
+    wsh[j] = w;
+    lloc = __builtin_fmaf(w, lj, lloc);
+  }
+  red[tid] = lloc;
+  __syncthreads();
+  for (int d = kCombineThreads / 2; d > 0; d >>= 1) {
+    if (tid < d) red[tid] += red[tid + d];
+    __syncthreads();
+  }
+  const float l = red[0];
+  // O: split j of parity g, eight loads in flight per thread
+  const int g = tid / kDim, d = tid % kDim;
+  const float* po = a.part_o + static_cast<int64_t>(row) * kDim + d;
+  const int64_t js = static_cast<int64_t>(a.rows_total) * kDim;
+  float acc = 0.0f;
+  int j = g;
+  for (; j + 14 < a.nsplit; j += 16) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = po[static_cast<int64_t>(j + 2 * u) * js];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(wsh[j + 2 * u], v[u], acc);
+  }
+  for (; j < a.nsplit; j += 2) acc = __builtin_fmaf(wsh[j], po[static_cast<int64_t>(j) * js], acc);
+  if (g == 1) half_acc[d] = acc;
+  __syncthreads();
+  if (g == 0) {
+    acc += half_acc[d];
+    const int pos = row % a.Lq;
+    const int hq = (row / a.Lq) % a.Hq;
+    const int b = row / (a.Lq * a.Hq);
+    if (a.row_den && d == 0) a.row_den[row] = l;
+    const float v = l > 0.0f ? acc / fmaxf(l, 1.17549435e-38f) : 0.0f;
+    const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + d;
+    if (a.o_f32) static_cast<float*>(a.o)[off] = v;
+    else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
+  }
 }
 
 // ---------------------------------------------------------------------------------------

@@ -475,7 +475,8 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                             int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p,
                             int p_levels, int norm_same, float* row_den, int nsplit, void* workspace,
                             int64_t workspace_bytes, const faq_attn_opts* opts, faq_stream_t stream) {
-  if (nsplit < 1 || nsplit > 4096) return fail(FAQ_EINVAL, "faq_attention_fwd_split: nsplit must be in [1, 4096]");
+  if (nsplit < 1 || nsplit > faq::kCombineMaxSplits)
+    return fail(FAQ_EINVAL, "faq_attention_fwd_split: nsplit must be in [1, %d]", faq::kCombineMaxSplits);
   faq::AttnArgs a;
   dim3 grid;
   const int rc = attention_setup("faq_attention_fwd_split", q, q_sb, q_sh, q_sl, k, k_sb, k_sh, k_sl, vt, v_sb, v_sh,
@@ -484,6 +485,9 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   if (rc != FAQ_OK) return rc == 1 ? FAQ_OK : rc;
   if (a.diag) return fail(FAQ_EINVAL, "faq_attention_fwd_split: the PV-normalizer probe runs in faq_attention_fwd");
   const SplitLayout L = split_layout(B, Hq, Lq, Lk, nsplit);
+  if (L.ntiles > faq::kScanMaxTiles)
+    return fail(FAQ_EUNSUP, "faq_attention_fwd_split: %d key tiles, the split path handles at most %d", L.ntiles,
+                faq::kScanMaxTiles);
   if (!workspace || !aligned16(workspace)) return fail(FAQ_EINVAL, "faq_attention_fwd_split: null or misaligned workspace");
   if (workspace_bytes < L.total)
     return fail(FAQ_EINVAL, "faq_attention_fwd_split: workspace of %lld bytes, need %lld",
@@ -499,10 +503,10 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   am.mx_stride = std::max(L.ntiles, 1);
   launch_attention(am, quant_p, p_levels, norm_same, grid, st);
   // 2. running maximum before each split
-  faq::SplitScanArgs sa{am.mx_out, am.mx_stride, reinterpret_cast<float*>(ws + L.m_start), a.rows_total, nsplit,
-                        L.tiles_per_split, Hq, Lq, Lk, a.causal, a.row_lo, a.row_hi};
-  const int64_t scan_threads = static_cast<int64_t>(a.rows_total) * nsplit;
-  hipLaunchKernelGGL(faq::split_scan_kernel, dim3(grid_for(scan_threads)), dim3(256), 0, st, sa);
+  faq::SplitScanArgs sa{am.mx_out, am.mx_stride, L.ntiles, reinterpret_cast<float*>(ws + L.m_start), a.rows_total,
+                        nsplit, L.tiles_per_split, Hq, Lq, Lk, a.causal, a.row_lo, a.row_hi};
+  hipLaunchKernelGGL(faq::split_scan_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(faq::kScanThreads),
+                     static_cast<size_t>(std::max(L.ntiles, 1)) * sizeof(float), st, sa);
   // 3. per-split recurrences from those maxima
   faq::AttnArgs ap = a;
   ap.m_start = sa.m_start;
@@ -511,7 +515,8 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   launch_attention(ap, quant_p, p_levels, norm_same, grid, st);
   // 4. combine
   faq::SplitCombineArgs ca{ap.part_o, ap.part_lm, a.rows_total, nsplit, Hq, Lq, o, o_sb, o_sh, o_sl, a.o_f32, row_den};
-  hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(128), 0, st, ca);
+  hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(faq::kCombineThreads), 0,
+                     st, ca);
   return check_launch("faq_attention_fwd_split");
 }
 

@@ -510,9 +510,12 @@ void attn_fwd_kernel(AttnArgs a) {
         }
       }
     }
+    // the maxima pass reads K only
+    if (!a.mx_out) {
 #pragma unroll
-    for (int j = 0; j < 5; ++j)
-      if (j < nj) dma16(vrs, vvo[j], vsoff, reinterpret_cast<uint16_t*>(st + kTileBytes + ((j < 4 ? 512 * j : 2048) + 64 * ws) * 16));
+      for (int j = 0; j < 5; ++j)
+        if (j < nj) dma16(vrs, vvo[j], vsoff, reinterpret_cast<uint16_t*>(st + kTileBytes + ((j < 4 ? 512 * j : 2048) + 64 * ws) * 16));
+    }
   };
 
   // LDS operand offsets (bytes).  QK: key row pi(0, n) + 16 kb, piece 2c + half.

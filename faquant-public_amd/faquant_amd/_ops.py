@@ -402,7 +402,7 @@ def attention_fwd(
     os_ = (out.stride(0), out.stride(1), out.stride(2))
     if out.stride(3) != 1:
         raise ValueError("attention output needs a unit stride along head_dim")
-    nsplit = _split_count(B, Hq, Hkv, Lq, int(key_length)) if split is None else int(split)
+    nsplit = _split_count(B, Hq, Hkv, Lq, int(key_length), _device_cus(q.device)) if split is None else int(split)
     if nsplit > 1 and not out_levels:
         ws_bytes = lib.faq_attention_split_workspace(B, Hq, Lq, int(key_length), nsplit)
         ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
@@ -428,18 +428,31 @@ def attention_fwd(
     return out
 
 
-def _split_count(B: int, Hq: int, Hkv: int, Lq: int, Lk: int) -> int:
-    """Key ranges for decode-sized queries (Lq <= 64) whose grid cannot fill 256 CUs: the
-    one-pass kernel runs one 256-row workgroup per (KV head group, 256/hpw positions).
-    Longer query blocks keep the one-pass kernel, so a prefill fed in chunks stays
+_CUS: dict = {}
+SPLIT_MAX_TILES = 16384  # the split path's scan holds one row's tile maxima in LDS
+
+
+def _device_cus(device) -> int:
+    """Compute units of a device (cached): the attention kernel runs one workgroup per CU."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    if key not in _CUS:
+        _CUS[key] = int(torch.cuda.get_device_properties(key).multi_processor_count)
+    return _CUS[key]
+
+
+def _split_count(B: int, Hq: int, Hkv: int, Lq: int, Lk: int, cus: int = 256) -> int:
+    """Key ranges for decode-sized queries (Lq <= 64) whose work items cannot fill the CUs:
+    the one-pass kernel runs one 256-row work item per (KV head group, 256/hpw positions).
+    The split count gives each CU one item (cus / items ranges), each range at least one key
+    tile.  Longer query blocks keep the one-pass kernel, so a prefill fed in chunks stays
     bitwise equal to one pass."""
     G = Hq // Hkv
     hpw = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
     wgs = B * Hkv * (G // hpw) * -(-Lq // (256 // hpw))
     ntiles = -(-Lk // KEY_TILE)
-    if Lq > 64 or wgs >= 128 or ntiles < 4:
+    if Lq > 64 or 2 * wgs > cus or ntiles < 4 or ntiles > SPLIT_MAX_TILES:
         return 1
-    return min(ntiles // 2, max(2, -(-512 // wgs)))
+    return max(2, min(cus // wgs, ntiles))
 
 
 def attention_pairs(query_length: int, key_length: int, causal: bool) -> int:

@@ -228,7 +228,8 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
  * the reference's sequential recurrence holds there, sfa:788-806), each range then runs
  * the recurrence from it, and a combine rescales and sums the ranges.  `workspace` is
  * device memory of at least faq_attention_split_workspace(B, Hq, Lq, Lk, nsplit) bytes,
- * 16-byte aligned.
+ * 16-byte aligned.  nsplit is 1..4096 and Lk at most 16384 key tiles (2097152 keys);
+ * beyond that the call returns FAQ_EUNSUP (use faq_attention_fwd).
  */
 int64_t faq_attention_split_workspace(int B, int Hq, int Lq, int Lk, int nsplit);
 int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,

@@ -195,3 +195,18 @@ def test_stats_closed_form_matches_oracle_counters():
                     key_chunk=128, causal=causal, skip_fully_masked=True, qk_quant=True, pv_quant=True,
                     qk_group=64, pv_group=64)
         assert sg == so
+
+
+def test_split_count_rule():
+    """Decode-sized grids split the key tiles so each CU holds one work item; prefill-sized
+    query blocks, full grids and key lengths past the split path's tile limit do not split."""
+    from faquant_amd import _ops
+
+    # Qwen3-8B decode: 8 work items on 256 CUs -> 32 ranges, at most one per key tile
+    assert [_ops._split_count(1, 32, 8, 1, lk) for lk in (1024, 4096, 32768, 131072)] == [8, 32, 32, 32]
+    assert _ops._split_count(1, 32, 8, 1, 300) == 1                       # under four key tiles
+    assert _ops._split_count(1, 32, 8, 65, 32768) == 1                    # a prefill chunk
+    assert _ops._split_count(32, 32, 8, 1, 32768) == 1                    # 256 items fill the GPU
+    assert _ops._split_count(16, 32, 8, 1, 32768) == 2                    # 128 items: two ranges
+    assert _ops._split_count(1, 32, 8, 1, 32768, cus=80) == 10            # fewer CUs, fewer ranges
+    assert _ops._split_count(1, 32, 8, 1, (_ops.SPLIT_MAX_TILES + 1) * 128) == 1
