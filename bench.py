@@ -34,7 +34,10 @@ HBM_PEAK_GBPS = 8000.0
 # scaled by the same counters on a 256 MiB device copy (bench.py --calibrate-copy):
 # profiles/attn_fwd_<config>_counters.md.  None where no counter run was made.
 MEASURED_TRAFFIC_BYTES = {
-    "qwen8b_32k": 1.674e9,
+    "qwen8b_32k": 1.684e9,
+    "qwen32b_16k": 1.101e9,
+    "wan480p": 1.990e10,
+    "wan720p": 1.118e11,
 }
 
 CONFIGS = {
