@@ -68,7 +68,9 @@ void launch_act(const faq::ActQdqArgs& a, int levels, int64_t threads, hipStream
 
 template <typename Tin, typename Tround>
 void launch_prep(const faq::OperandPrepArgs& a, int levels, int64_t, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((a.L + 15) / 16), static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
+  const int per_block = 16 * faq::kPrepRows;
+  const dim3 grid(static_cast<unsigned>((a.L + per_block - 1) / per_block), static_cast<unsigned>(a.H),
+                  static_cast<unsigned>(a.B));
   if (levels == 12) hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 12>), grid, dim3(256), 0, st, a);
   else if (levels == 13) hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 13>), grid, dim3(256), 0, st, a);
   else hipLaunchKernelGGL((faq::operand_prep_kernel<Tin, Tround, 123>), grid, dim3(256), 0, st, a);

@@ -224,14 +224,6 @@ struct PQuant {
   float ns4;    // -s / 4
 };
 
-// fp32 -> bf16 (round to nearest even, the hardware conversion) -> fp32.
-__device__ __forceinline__ float bf16_round_hw(float x) {
-  const __bf16 h = static_cast<__bf16>(x);
-  uint16_t u;
-  __builtin_memcpy(&u, &h, 2);
-  return __uint_as_float(static_cast<uint32_t>(u) << 16);
-}
-
 // Same values as hif4_scale (hif4.py:91-115) for m1 >= 0: s0 = bf16(m1 bf16(1/div)),
 // clamped to [2^-48, 49152] (integer clamp of the non-negative bit pattern), E6M2
 // round-half-even on the bits, and rec = bf16(1/s): 1/s = 2^-e / (1 + m/4) lies far from

@@ -30,6 +30,27 @@ __device__ __forceinline__ float bf16_rne(float x) {
   return __uint_as_float(u);
 }
 
+// fp32 -> bf16 -> fp32 with the hardware conversion (v_cvt_pk_bf16_f32): round to nearest
+// even like bf16_rne for every non-NaN input (checked exhaustively on gfx950), and a NaN
+// stays a NaN (bf16_rne can carry a NaN's payload into infinity).
+__device__ __forceinline__ float bf16_round_hw(float x) {
+  const __bf16 h = static_cast<__bf16>(x);
+  uint16_t u;
+  __builtin_memcpy(&u, &h, 2);
+  return __uint_as_float(static_cast<uint32_t>(u) << 16);
+}
+
+// Two fp32 values rounded to bf16 (hardware conversion, as bf16_round_hw) and packed, the
+// first in the low half: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack2_bf16_hw(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  const bf16x2v r = __builtin_convertvector((f32x2){lo, hi}, bf16x2v);
+  uint32_t u;
+  __builtin_memcpy(&u, &r, 4);
+  return u;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }

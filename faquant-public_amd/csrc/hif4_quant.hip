@@ -47,7 +47,7 @@ struct Io<__hip_bfloat16> {
   static __device__ __forceinline__ void store(T* p, float v) {
     *reinterpret_cast<uint16_t*>(p) = f32_to_bf16_bits_rne(v);
   }
-  static __device__ __forceinline__ float round(float v) { return bf16_rne(v); }
+  static __device__ __forceinline__ float round(float v) { return bf16_round_hw(v); }
   static __device__ __forceinline__ void load8(const T* p, float* v) {
     const uint4 a = *reinterpret_cast<const uint4*>(p);
     const uint32_t w[4] = {a.x, a.y, a.z, a.w};
@@ -60,9 +60,7 @@ struct Io<__hip_bfloat16> {
   static __device__ __forceinline__ void store8(T* p, const float* v) {
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = static_cast<uint32_t>(f32_to_bf16_bits_rne(v[2 * i])) |
-             (static_cast<uint32_t>(f32_to_bf16_bits_rne(v[2 * i + 1])) << 16);
+    for (int i = 0; i < 4; ++i) w[i] = pack2_bf16_hw(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 };
@@ -308,36 +306,66 @@ __global__ __launch_bounds__(256) void unpack_rows_kernel(UnpackArgs a) {
 // cross-lane stages of stride 8 m for m = 1, 2, ... < n / 8, pairing lane l with l ^ m.
 // Each stage writes (left + right, left - right) with the left half at the lower
 // index, the order of rotation.py:21-28.
-__device__ __forceinline__ void fwht8_lanes(float* v, int n) {
+template <int S>
+__device__ __forceinline__ void fwht_inlane_stage(float* v) {
 #pragma unroll
-  for (int s = 1; s < 8; s <<= 1) {
-    if (s >= n) break;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if ((i & s) == 0) {
-        const float l = v[i];
-        const float r = v[i + s];
-        v[i] = l + r;
-        v[i + s] = l - r;
-      }
+  for (int i = 0; i < 8; ++i) {
+    if ((i & S) == 0) {
+      const float l = v[i];
+      const float r = v[i + S];
+      v[i] = l + r;
+      v[i + S] = l - r;
     }
   }
-  auto stage = [&](auto m_tag) {
-    constexpr int m = decltype(m_tag)::value;
-    if (m * 8 >= n) return;
-    const bool upper = (threadIdx.x & m) != 0;
+}
+
+// Cross-lane stage of stride 8 M: (left + right, left - right) with the left half at the
+// lower lane; the upper lane of a pair computes other - v as fma(-1, v, other), the lower
+// one v + other as fma(1, v, other), both exactly the rounded sum or difference.
+template <int M>
+__device__ __forceinline__ void fwht_lane_stage(float* v) {
+  const float sgn = (threadIdx.x & M) != 0 ? -1.0f : 1.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float other = lane_xor<m>(v[i]);
-      v[i] = upper ? other - v[i] : v[i] + other;
-    }
-  };
-  stage(LaneMask<1>{});
-  stage(LaneMask<2>{});
-  stage(LaneMask<4>{});
-  stage(LaneMask<8>{});
-  stage(LaneMask<16>{});
-  stage(LaneMask<32>{});
+  for (int i = 0; i < 8; ++i) {
+    const float other = lane_xor<M>(v[i]);
+    v[i] = __builtin_fmaf(sgn, v[i], other);
+  }
+}
+
+// All stages of a block of N values (N a power of two in [2, 512]).
+template <int N>
+__device__ __forceinline__ void fwht8_fixed(float* v) {
+  if constexpr (N >= 2) fwht_inlane_stage<1>(v);
+  if constexpr (N >= 4) fwht_inlane_stage<2>(v);
+  if constexpr (N >= 8) fwht_inlane_stage<4>(v);
+  if constexpr (N > 8) fwht_lane_stage<1>(v);
+  if constexpr (N > 16) fwht_lane_stage<2>(v);
+  if constexpr (N > 32) fwht_lane_stage<4>(v);
+  if constexpr (N > 64) fwht_lane_stage<8>(v);
+  if constexpr (N > 128) fwht_lane_stage<16>(v);
+  if constexpr (N > 256) fwht_lane_stage<32>(v);
+}
+
+// The block sizes of the attention prologues (64, 128) run as straight-line code; other
+// sizes take one uniform branch per stage (each branch joins with register copies).
+__device__ __forceinline__ void fwht8_lanes(float* v, int n) {
+  if (n == 64) {
+    fwht8_fixed<64>(v);
+    return;
+  }
+  if (n == 128) {
+    fwht8_fixed<128>(v);
+    return;
+  }
+  if (n >= 2) fwht_inlane_stage<1>(v);
+  if (n >= 4) fwht_inlane_stage<2>(v);
+  if (n >= 8) fwht_inlane_stage<4>(v);
+  if (n > 8) fwht_lane_stage<1>(v);
+  if (n > 16) fwht_lane_stage<2>(v);
+  if (n > 32) fwht_lane_stage<4>(v);
+  if (n > 64) fwht_lane_stage<8>(v);
+  if (n > 128) fwht_lane_stage<16>(v);
+  if (n > 256) fwht_lane_stage<32>(v);
 }
 
 // Division by d = fp32(sqrt(n)) with the result of the IEEE division x / d (the reference
@@ -477,48 +505,68 @@ struct OperandPrepArgs {
   int quant;                     // 1: HiF4 QDQ after the cast
 };
 
-// One lane owns 8 of a row's 128 values; a row spans 16 lanes.  Grid: x = blocks of 16
-// positions, y = head, z = batch (no integer division in the index math).
+// One lane owns 8 of a row's 128 values; a row spans 16 lanes, and each lane takes
+// kPrepRows rows 16 positions apart (a block covers 16 kPrepRows consecutive positions): the
+// loads of all its rows are issued before any arithmetic, so each wave keeps kPrepRows KiB
+// in flight (one row per lane is latency-bound at under half the HBM rate).  Grid: x =
+// blocks of positions, y = head, z = batch (no integer division in the index math).
+constexpr int kPrepRows = 2;
+
 template <typename Tin, typename Tround, int LV>
 __global__ __launch_bounds__(256) void operand_prep_kernel(OperandPrepArgs a) {
   const int h = static_cast<int>(blockIdx.y);
   const int b = static_cast<int>(blockIdx.z);
-  const int lp = static_cast<int>(blockIdx.x) * 16 + static_cast<int>(threadIdx.x >> 4);
-  const bool live = lp < a.L;
-  const int l = live ? lp : 0;
-  const int64_t r = (static_cast<int64_t>(b) * a.H + h) * a.L + l;
+  const int lp0 = static_cast<int>(blockIdx.x) * (16 * kPrepRows) + static_cast<int>(threadIdx.x >> 4);
   const int part = threadIdx.x & 15;
   const int d0 = part * 8;
-  float v[8];
-  if (live) {
-    Io<Tin>::load8(static_cast<const Tin*>(a.x) + b * a.sb + h * a.sh + l * a.sl + d0, v);
-  } else {
+  float v[kPrepRows][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  for (int j = 0; j < kPrepRows; ++j) {
+    const int lp = lp0 + 16 * j;
+    if (lp < a.L) {
+      Io<Tin>::load8(static_cast<const Tin*>(a.x) + b * a.sb + h * a.sh + static_cast<int64_t>(lp) * a.sl + d0, v[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[j][i] = 0.0f;
+    }
   }
+  float off[8], sc[8];
   if (a.key_offset) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = v[i] - a.key_offset[h * a.off_sh + d0 + i];
+    for (int i = 0; i < 8; ++i) off[i] = a.key_offset[h * a.off_sh + d0 + i];
   }
   if (a.smooth) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float sc = a.smooth[h * a.smooth_sh + d0 + i];
-      v[i] = a.smooth_divide ? v[i] / sc : v[i] * sc;
-    }
+    for (int i = 0; i < 8; ++i) sc[i] = a.smooth[h * a.smooth_sh + d0 + i];
   }
-  if (a.hadamard) {
-    fwht8_lanes(v, a.hadamard);
-    div_sqrt_n(v, a.div);
-  }
-  // the single cast back to the operand dtype (qwen3.py:129-130)
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = Io<Tround>::round(v[i]);
-  if (a.rotated && live) Io<Tround>::store8(static_cast<Tround*>(a.rotated) + r * 128 + d0, v);
-  if (a.quant) qdq8<LV>(v);
-  if (live) {
-    Io<__hip_bfloat16>::store8(
-        reinterpret_cast<__hip_bfloat16*>(static_cast<uint16_t*>(a.y) + b * a.yb + h * a.yh + l * a.yl + d0), v);
+  for (int j = 0; j < kPrepRows; ++j) {
+    const int lp = lp0 + 16 * j;
+    const bool live = lp < a.L;
+    const int l = live ? lp : 0;
+    const int64_t r = (static_cast<int64_t>(b) * a.H + h) * a.L + l;
+    float* w = v[j];
+    if (a.key_offset) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w[i] = w[i] - off[i];
+    }
+    if (a.smooth) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w[i] = a.smooth_divide ? w[i] / sc[i] : w[i] * sc[i];
+    }
+    if (a.hadamard) {
+      fwht8_lanes(w, a.hadamard);
+      div_sqrt_n(w, a.div);
+    }
+    // the single cast back to the operand dtype (qwen3.py:129-130)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = Io<Tround>::round(w[i]);
+    if (a.rotated && live) Io<Tround>::store8(static_cast<Tround*>(a.rotated) + r * 128 + d0, w);
+    if (a.quant) qdq8<LV>(w);
+    if (live) {
+      Io<__hip_bfloat16>::store8(
+          reinterpret_cast<__hip_bfloat16*>(static_cast<uint16_t*>(a.y) + b * a.yb + h * a.yh + static_cast<int64_t>(l) * a.yl + d0), w);
+    }
   }
 }
 
