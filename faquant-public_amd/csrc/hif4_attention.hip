@@ -47,7 +47,8 @@
 // m3 rec >= 2, >= 4 of the reference are exactly floor2 comparisons).  The code is then
 // one fused multiply-add against the magic constant M_K = 2^(23+k):
 //   z = fma(p, 4 rec, M_K)  ->  z = M_K + K * rint(p * 4 rec / K)
-// (M_K has unit-in-last-place K), clamped at M_K + 7K (the bit pattern of M_K plus 7),
+// (M_K has unit-in-last-place K), clamped at M_K + 7K (a 16-bit min of the pattern's low
+// half, which holds the code),
 // and dequantized exactly by y = fma(z, s/4, -M_K s/4) = K * code * s/4 = code * ds / 4.
 // This equals the reference's floor(fp32(p * qm) * 4 + 0.5) except on the measure-zero
 // sets where p * qm * 4 rounds onto, or is exactly, a half-integer (ties round to even
@@ -243,6 +244,17 @@ __device__ __forceinline__ PQuant pquant_setup(float m1) {
   return q;
 }
 
+// Code clamp at 7 of z = M_K + code ulp: M_K = 2^(23 + k) has a zero low half, and the
+// code is at most 8 (p rec / K < 2 within a 4-key group, and m1 rec < 8 for the group
+// maximum), so the low 16 bits of z's pattern are the code.  One 16-bit min against 7 in
+// place (SDWA; the upper half is preserved) replaces a 32-bit min against a per-group
+// bound.
+__device__ __forceinline__ float clamp_code7(float z) {
+  uint32_t u = __float_as_uint(z);
+  asm("v_min_u16_sdwa %0, %0, 7 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_0" : "+v"(u));
+  return __uint_as_float(u);
+}
+
 // HiF4 QDQ in place of one 8-key group g[0..7] (two 4-key groups) of a lane's P group.
 template <int LV>
 __device__ __forceinline__ void pquant8(float* g, const PQuant& q) {
@@ -268,17 +280,12 @@ __device__ __forceinline__ void pquant8(float* g, const PQuant& q) {
     mka = __builtin_amdgcn_fmed3f(xa, 8388608.0f, 16777216.0f);
     mkb = __builtin_amdgcn_fmed3f(xb, 8388608.0f, 16777216.0f);
   }
-  // code clamp at 7: z = M_K + code ulp, compared as integers (z > 0)
-  const uint32_t cka = __float_as_uint(mka) + 7u;
-  const uint32_t ckb = __float_as_uint(mkb) + 7u;
   const float nka = mka * q.ns4;
   const float nkb = mkb * q.ns4;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float za = __uint_as_float(min(__float_as_uint(__builtin_fmaf(g[j], q.rec4, mka)), cka));
-    g[j] = __builtin_fmaf(za, q.s4, nka);
-    const float zb = __uint_as_float(min(__float_as_uint(__builtin_fmaf(g[4 + j], q.rec4, mkb)), ckb));
-    g[4 + j] = __builtin_fmaf(zb, q.s4, nkb);
+    g[j] = __builtin_fmaf(clamp_code7(__builtin_fmaf(g[j], q.rec4, mka)), q.s4, nka);
+    g[4 + j] = __builtin_fmaf(clamp_code7(__builtin_fmaf(g[4 + j], q.rec4, mkb)), q.s4, nkb);
   }
 }
 
