@@ -12,18 +12,20 @@
 // and O = acc / l (0 where l == 0).  HiF4-quantized Q/K/V/P values carry at most six
 // significant bits, so they are exact bf16 MFMA operands.
 //
-// Work decomposition: a 512-thread workgroup (eight waves of 32 query rows, one
-// workgroup per CU, two waves per SIMD) owns 256 query rows that share one KV head (GQA:
-// hpw query heads x 256 / hpw positions), so each K/V tile staged in LDS serves 256 rows.
-// K and V^T tiles are double-buffered in LDS and move HBM -> LDS by buffer loads that
-// write LDS directly (no VGPR staging); the DMA of tile t + 1 is issued at the top of
-// tile t, behind the tile's single barrier.
+// Work decomposition: a work item is 256 query rows that share one KV head (GQA: hpw
+// query heads x 256 / hpw positions), so each K/V tile staged in LDS serves 256 rows.  A
+// 512-thread workgroup (eight waves of 32 query rows, two waves per SIMD) runs on each
+// CU and streams its items one after another.  K and V^T tiles are double-buffered in
+// LDS and move HBM -> LDS by buffer loads that write LDS directly (no VGPR staging); the
+// DMA of tile t + 1 (or of the next item's first tile) is issued at the top of tile t,
+// behind the tile's single barrier.
 //
 // Masks: bottom-right causal from the shapes, or per-row key ranges [row_lo, row_hi]
 // plus a key-validity bitmap (2-D padding masks in the unpadded-rank form of sfa:371-427,
-// sliding windows); keys outside become -inf before the row maximum, and key tiles no
-// row of a wave sees are skipped (bitwise the same as processing an all -inf tile).
-// An optional logit softcap replaces s by softcap tanh(scale s / softcap) (sfa:725-727).
+// sliding windows), or a dense additive fp32 mask (3-D/4-D masks, sfa:430-454); keys
+// outside become -inf before the row maximum, and key tiles no row of a wave sees are
+// skipped (bitwise the same as processing an all -inf tile).  An optional logit softcap
+// replaces s by softcap tanh(scale s / softcap) (sfa:725-727).
 //
 // MFMA layout (v_mfma_f32_32x32x16_bf16; lane l, m = l % 32, half = l / 32):
 //   QK computes S^T = K Q^T.  The B operand is the wave's Q fragment (lane holds
@@ -48,8 +50,8 @@
 // one fused multiply-add against the magic constant M_K = 2^(23+k):
 //   z = fma(p, 4 rec, M_K)  ->  z = M_K + K * rint(p * 4 rec / K)
 // (M_K has unit-in-last-place K), clamped at M_K + 7K (a 16-bit min of the pattern's low
-// half, which holds the code),
-// and dequantized exactly by y = fma(z, s/4, -M_K s/4) = K * code * s/4 = code * ds / 4.
+// half, which holds the code), and dequantized exactly by
+//   y = fma(z, s/4, -M_K s/4) = K * code * s/4 = code * ds / 4.
 // This equals the reference's floor(fp32(p * qm) * 4 + 0.5) except on the measure-zero
 // sets where p * qm * 4 rounds onto, or is exactly, a half-integer (ties round to even
 // here); P itself already differs from torch.exp by a few ulp, so P^ is compared within
@@ -116,10 +118,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ bf16x8 lds_read16(const uint16_t* p) {
-  return *reinterpret_cast<const bf16x8*>(p);
 }
 
 // One 16-byte-per-lane DMA from global memory into LDS: lane l reads 16 bytes at byte
@@ -373,11 +371,6 @@ __device__ __forceinline__ bf16x8 lds_read_at(const uint8_t* base, int byte_off)
   return *reinterpret_cast<const bf16x8*>(base + byte_off);
 }
 
-// kMode & 7 (kMask) 0: masks from the shapes (none, bottom-right causal, ragged tail);
-// 1: key ranges and valid-key bits (a.row_lo, a.row_hi, a.key_bits); 2: key ranges and the
-// logit softcap; 3: a dense additive mask (a.amask); 4: the dense mask and the softcap.
-// kMode & 8 (kDiag): the PV-normalizer probe (a.diag).  One form per
-// instantiation keeps each hot loop within its register budget.
 // kMode & 7 (kMask) 0: masks from the shapes (none, bottom-right causal, ragged tail);
 // 1: key ranges and valid-key bits (a.row_lo, a.row_hi, a.row_blocks, a.key_bits); 2: key
 // ranges and the logit softcap; 3: a dense additive mask (a.amask); 4: the dense mask and
