@@ -135,6 +135,31 @@ def cpu_baseline(cfg, rows):
     }
 
 
+def mfma_probe(dev) -> float:
+    """The device's sustained dense bf16 MFMA rate (TFLOP/s) in the attention kernel's launch
+    shape (faq_mfma_probe: MFMA chains only), timed after the benchmark so the clock is warm:
+    the measured reference point beside the specification peak."""
+    import torch
+    from faquant_amd import _lib
+
+    lib = _lib.load()
+    blocks = torch.cuda.get_device_properties(dev).multi_processor_count
+    iters = 20000
+    out = torch.empty(blocks * 512, device=dev, dtype=torch.float32)
+    stream = _lib.stream_ptr(dev)
+    for _ in range(3):
+        _lib.check(lib.faq_mfma_probe(out.data_ptr(), blocks, iters, stream))
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    reps = 5
+    for _ in range(reps):
+        _lib.check(lib.faq_mfma_probe(out.data_ptr(), blocks, iters, stream))
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    return blocks * 8 * iters * 4 * 32768 / (ms * 1e-3) / 1e12
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -260,6 +285,12 @@ def main():
             "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": MEASURED_TRAFFIC_BYTES.get(args.config),
         },
+    }
+    probe = mfma_probe(dev)
+    result["mfma_probe"] = {
+        "tflops": round(probe, 1),
+        "pct_spec_peak": round(100.0 * probe / MFMA_BF16_PEAK_TFLOPS, 2),
+        "kernel_frac_of_probe": round(achieved / probe, 4),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_rows)

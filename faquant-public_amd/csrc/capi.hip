@@ -10,6 +10,7 @@
 #include "attn_aux.hip"
 #include "hif4_attention.hip"
 #include "hif4_quant.hip"
+#include "mfma_probe.hip"
 
 namespace {
 
@@ -520,6 +521,14 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(faq::kCombineThreads), 0,
                      st, ca);
   return check_launch("faq_attention_fwd_split");
+}
+
+int faq_mfma_probe(float* out, int blocks, int iters, faq_stream_t stream) {
+  if (!out) return fail(FAQ_EINVAL, "faq_mfma_probe: null output");
+  if (blocks < 1 || iters < 1) return fail(FAQ_EINVAL, "faq_mfma_probe: blocks and iters must be positive");
+  hipLaunchKernelGGL(faq::mfma_probe_kernel, dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
+                     static_cast<hipStream_t>(stream), out, iters);
+  return check_launch("faq_mfma_probe");
 }
 
 }  // extern "C"

@@ -70,6 +70,7 @@ _SIGNATURES = {
         _c_int,
     ),
     "faq_attention_split_workspace": ([_c_int, _c_int, _c_int, _c_int, _c_int], _c_i64),
+    "faq_mfma_probe": ([_vp, _c_int, _c_int, _vp], _c_int),
     "faq_attention_fwd_split": (
         [
             _vp, _c_i64, _c_i64, _c_i64,

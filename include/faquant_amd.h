@@ -39,6 +39,8 @@
  *                         the reference appends one position to its QDQ cache,
  *                         simulated_flash_attention.py:243-289, and runs the tile loop)
  *   faq_attention_split_workspace  workspace size of faq_attention_fwd_split
+ *   faq_mfma_probe        no reference counterpart: a measurement helper (the device's
+ *                         sustained bf16 MFMA rate, the reference point of the benchmark)
  */
 #ifndef FAQUANT_AMD_H
 #define FAQUANT_AMD_H
@@ -238,6 +240,15 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                             int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p,
                             int p_levels, int norm_same, float* row_den, int nsplit, void* workspace,
                             int64_t workspace_bytes, const faq_attn_opts* opts, faq_stream_t stream);
+
+/*
+ * Measurement helper with no counterpart in the reference: `blocks` workgroups of the
+ * attention kernel's launch shape (512 threads, two waves per SIMD) each run `iters`
+ * iterations of four independent bf16 32x32x16 MFMA chains per wave, nothing else.
+ * FLOP = blocks * 8 * iters * 4 * 32768.  Timed by the caller; the result is this
+ * device's sustained dense bf16 MFMA rate.  out receives blocks * 512 fp32 values.
+ */
+int faq_mfma_probe(float* out, int blocks, int iters, faq_stream_t stream);
 
 #ifdef __cplusplus
 }
