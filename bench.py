@@ -35,9 +35,9 @@ HBM_PEAK_GBPS = 8000.0
 # profiles/attn_fwd_<config>_counters.md.  None where no counter run was made.
 MEASURED_TRAFFIC_BYTES = {
     "qwen8b_32k": 1.684e9,
-    "qwen32b_16k": 1.101e9,
-    "wan480p": 1.990e10,
-    "wan720p": 1.118e11,
+    "qwen32b_16k": 1.096e9,
+    "wan480p": 1.929e10,
+    "wan720p": 1.081e11,
 }
 
 CONFIGS = {
