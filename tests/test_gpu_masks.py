@@ -211,6 +211,13 @@ def _dense_case(kind, batch, hq, lq, lk, seed):
         m[g.random(m.shape) < 0.05] = np.finfo(np.float32).min
         m[:, :, 3] = -np.inf  # a fully masked row
         return torch.from_numpy(m), m
+    if kind == "f32_min_row":  # test_simulated_flash_attention.py:208-220: finfo.min rows
+        m = np.full((batch, 1, lq, lk), np.finfo(np.float32).min, dtype=np.float32)
+        m[..., 1:, : lk // 3] = 0.0  # row 0 stays fully masked by finfo.min (not -inf)
+        return torch.from_numpy(m), m
+    if kind == "fp16_all_min":  # test_simulated_flash_attention.py:222-233: every row masked
+        m = np.full((batch, 1, lq, lk), np.finfo(np.float16).min, dtype=np.float16)
+        return torch.from_numpy(m), m
     if kind == "fp16_min":
         m = np.where(causal, 0.0, np.finfo(np.float16).min).astype(np.float16)[None, None]
         m = np.broadcast_to(m, (batch, 1, lq, lk)).copy()
@@ -233,7 +240,8 @@ def _dense_case(kind, batch, hq, lq, lk, seed):
 
 @pytest.mark.parametrize("kind,batch,lq,lk", [("bool_causal", 2, 300, 300), ("additive_heads", 1, 200, 260),
                                               ("fp16_min", 1, 256, 300), ("bf16_longer_rows", 1, 130, 300),
-                                              ("one_row", 2, 1, 500), ("three_d", 2, 150, 150)])
+                                              ("one_row", 2, 1, 500), ("three_d", 2, 150, 150),
+                                              ("f32_min_row", 1, 140, 300), ("fp16_all_min", 1, 70, 200)])
 @pytest.mark.parametrize("softcap", [None, 2.5])
 def test_dense_masks_through_drop_in(dev, kind, batch, lq, lk, softcap):
     from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward
@@ -250,8 +258,13 @@ def test_dense_masks_through_drop_in(dev, kind, batch, lq, lk, softcap):
     got = out.float().cpu().numpy()
     assert_close_attention(got, ref, f"dense {kind} softcap={softcap}")
     assert mod.faquant_simulated_attention_stats == stats
+    assert np.isfinite(got).all()
     if kind == "additive_heads":
         assert np.count_nonzero(got[:, 3]) == 0  # fully masked rows give zeros
+    if kind == "f32_min_row":
+        assert np.count_nonzero(got[:, 0]) == 0 and np.count_nonzero(got[:, 1:]) > 0
+    if kind == "fp16_all_min":
+        assert np.count_nonzero(got) == 0
 
 
 def test_attention_core_with_padding_mask_equals_drop_in(dev):
