@@ -130,6 +130,34 @@ def test_padded_batches_through_drop_in(dev, kind, lq, lk, mode):
         assert np.count_nonzero(got[-1]) == 0  # a batch row without any valid key gives zeros
 
 
+@pytest.mark.parametrize("lq,window", [(1, 64), (5, 200)])
+def test_padded_decode_with_window_through_drop_in(dev, lq, window):
+    """Decode steps over a left-padded cache with a sliding window
+    (test_simulated_flash_attention.py:235-265, 329-359)."""
+    q, k, v = _qkv(900 + lq, 3, 8, 2, lq, 777)
+    mask = make_mask("left", 3, 777, seed=lq)
+    got, ref, stats, ref_stats = _run(dev, q, k, v, mask, window=window)
+    assert_close_attention(got, ref, f"padded decode lq={lq} window={window}")
+    assert stats == ref_stats
+
+
+def test_left_padding_position_ids_are_not_mistaken_for_packing(dev):
+    """With a 2-D mask, position ids that restart inside the padding are left-padding ids,
+    not packing (test_simulated_flash_attention.py:380-396): the call equals the call
+    without them.  Without a mask the same ids are rejected as packed (sfa:485-510)."""
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward
+
+    q, k, v = (to_dev(a, dev, torch.bfloat16) for a in _qkv(11, 1, 4, 2, 300, 300))
+    mask = torch.ones((1, 300), dtype=torch.bool)
+    mask[0, :100] = False
+    pos = torch.cat([torch.ones(100, dtype=torch.long), torch.arange(200)])[None].to(dev)
+    a, _ = simulated_flash_attention_forward(module(), q, k, v, mask.to(dev), position_ids=pos)
+    b, _ = simulated_flash_attention_forward(module(), q, k, v, mask.to(dev))
+    assert torch.equal(a, b)
+    with pytest.raises(NotImplementedError):
+        simulated_flash_attention_forward(module(), q, k, v, None, position_ids=pos)
+
+
 @pytest.mark.parametrize("causal,window,lq,lk", [(True, 100, 700, 700), (False, 150, 500, 500),
                                                  (True, 300, 2, 900), (False, 1, 200, 200)])
 def test_sliding_window_through_drop_in(dev, causal, window, lq, lk):
