@@ -153,5 +153,27 @@ def stream_ptr(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+class _ForwardOnly(torch.autograd.Function):
+    """A result of the forward-only HIP path, joined to the autograd graph of its inputs: a
+    backward pass through it raises instead of silently giving those inputs no gradient
+    (the reference's simulator is differentiable; this build implements inference)."""
+
+    @staticmethod
+    def forward(ctx, result, *inputs):
+        return result.view_as(result)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError("the HIP HiF4 path is forward-only: backward is not implemented")
+
+
+def forward_only(result: torch.Tensor, *inputs) -> torch.Tensor:
+    """`result`, tracked by autograd when grad mode is on and an input requires grad."""
+    tracked = [t for t in inputs if isinstance(t, torch.Tensor) and t.requires_grad]
+    if torch.is_grad_enabled() and tracked:
+        return _ForwardOnly.apply(result, *tracked)
+    return result
+
+
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()

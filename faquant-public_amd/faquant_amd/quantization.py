@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
 from .hif4 import HIF4_BLOCK_SIZE, fake_quantize_hif4
 
 
@@ -133,4 +134,4 @@ class FakeQuantLinear(torch.nn.Module):
 
         block = self.online_hadamard_block_size if self.online_hadamard else 0
         xq = _ops.act_qdq_rows(x, levels=HIF4_ACT_SCALE_LEVELS, hadamard=int(block or 0), col_scale=self.input_scale)
-        return torch.nn.functional.linear(xq, self.weight, self.bias)
+        return torch.nn.functional.linear(_lib.forward_only(xq, x), self.weight, self.bias)

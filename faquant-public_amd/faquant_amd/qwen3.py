@@ -20,7 +20,7 @@ from typing import Optional
 
 import torch
 
-from . import _ops
+from . import _lib, _ops
 from .hif4 import HIF4_ACT_SCALE_LEVELS, HIF4_ATTN_OPERAND_SCALE_LEVELS
 from .hif4 import _resolve as resolve_hif4_levels
 from .quantization import check_hif4_arguments, fake_quantize
@@ -161,4 +161,4 @@ def attention_core(
         causal=causal, skip_fully_masked=bool(getattr(module, "faquant_skip_fully_masked_tiles", True)) and not masked,
         qk_quant=qk_quant, pv_quant=pv_quant, qk_group=qk_group, pv_group=pv_group,
     )
-    return out
+    return _lib.forward_only(out, query, key, value)

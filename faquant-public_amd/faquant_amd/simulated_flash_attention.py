@@ -21,7 +21,7 @@ from typing import Optional
 
 import torch
 
-from . import _ops
+from . import _lib, _ops
 from .config import PV_NORMALIZER_MODES
 from .hif4 import HIF4_ATTN_OPERAND_SCALE_LEVELS, HIF4_BLOCK_SIZE
 
@@ -438,4 +438,4 @@ def simulated_flash_attention_forward(
         # every processed P tile counts all its values (sfa:139), as the P QDQ stats do
         _record_probe(diagnostics, probe,
                       module.faquant_simulated_attention_stats["p_quantized_values"] - p_values_before)
-    return output, None
+    return _lib.forward_only(output, query, key, value), None

@@ -23,7 +23,7 @@ from typing import Callable
 
 import torch
 
-from . import _ops
+from . import _lib, _ops
 from .hif4 import fake_quantize_hif4
 
 KEY_TILE = _ops.KEY_TILE
@@ -78,7 +78,7 @@ def hif4_attention(
         _as_bhld(q), _as_bhld(k), vt, lk, causal=False, scale=scale, quant_p=quantize_p,
         p_levels="123", norm_same=quantized_normalizer, out=_as_bhld(out),
     )
-    return out
+    return _lib.forward_only(out, q, k, v)
 
 
 def rotate_heads(x: torch.Tensor, chunk_rows: int = 1 << 16) -> torch.Tensor:
@@ -104,6 +104,7 @@ def make_flash_attention(
                             q_scale=q_scale, causal=causal, window_size=window_size, deterministic=deterministic,
                             dtype=dtype, version=version)
         assert dropout_p == 0 and q_scale is None and not causal and tuple(window_size) == (-1, -1)
+        inputs = (q, k, v)
         batch, lq, lk, out_dtype = q.size(0), q.size(1), k.size(1), q.dtype
         for lens, full in ((q_lens, lq), (k_lens, lk)):
             if lens is not None and any(int(n) != full for n in lens.tolist()):
@@ -129,6 +130,6 @@ def make_flash_attention(
             qh, kh, vt, lk, causal=False, scale=scale, quant_p=True, p_levels="123",
             norm_same=quantized_normalizer, out=_as_bhld(out),
         )
-        return out.type(out_dtype)
+        return _lib.forward_only(out.type(out_dtype), *inputs)
 
     return flash_attention

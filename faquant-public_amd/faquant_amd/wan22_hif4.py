@@ -15,6 +15,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
+from . import _lib
 from .wan22_attention import faquant_qdq
 
 BLOCK_LINEARS = (
@@ -62,7 +63,8 @@ class HiF4Linear(nn.Module):
         rows = x.reshape(-1, self.in_features)
         out = None
         for start in range(0, rows.shape[0], self.chunk_rows):
-            part = self.input_qdq(rows[start:start + self.chunk_rows])
+            chunk = rows[start:start + self.chunk_rows]
+            part = _lib.forward_only(self.input_qdq(chunk), chunk)
             if self.collector is not None:
                 self.collector(self, part, start)
             y = F.linear(part, self.weight, self.bias)

@@ -344,3 +344,40 @@ def test_unsupported_features_raise(dev):
     out_m, _ = simulated_flash_attention_forward(module(), q, k, k, torch.ones(1, 8, dtype=torch.bool, device=dev))
     out_n, _ = simulated_flash_attention_forward(module(), q, k, k, None)
     assert torch.equal(out_m, out_n)
+
+
+def test_forward_only_paths_join_autograd_and_refuse_backward(dev):
+    """The reference's simulator is differentiable (test_simulated_flash_attention.py:818-876);
+    this build implements inference.  With inputs that require grad, each drop-in returns
+    the no-grad result joined to the autograd graph, and a backward pass through it raises
+    instead of silently leaving those inputs without a gradient."""
+    from faquant_amd.quantization import FakeQuantLinear
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward
+    from faquant_amd.wan22_attention import hif4_attention
+
+    g = torch.Generator(device="cpu").manual_seed(3)
+    q, k, v = (torch.randn(1, h, 200, 128, generator=g).to(dev, torch.bfloat16) for h in (4, 2, 2))
+    with torch.no_grad():
+        ref, _ = simulated_flash_attention_forward(module(), q, k, v, None)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out, _ = simulated_flash_attention_forward(module(), qg, kg, vg, None)
+    assert out.requires_grad and torch.equal(out.detach(), ref)
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        out.float().sum().backward()
+
+    ql, kl, vl = (t[0, :2].transpose(0, 1).contiguous().requires_grad_(True) for t in (q, k, v))
+    wan = hif4_attention(ql, kl, vl)
+    assert wan.requires_grad
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        wan.float().sum().backward()
+
+    lin = torch.nn.Linear(128, 64).to(dev, torch.bfloat16)
+    mod = FakeQuantLinear(lin, quant_format="hif4", bits=4, weight_group_size=64, activation_group_size=64,
+                          symmetric=True, clip_ratio=1.0)
+    x = torch.randn(8, 128, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+    y = mod(x)
+    assert y.requires_grad
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        y.float().sum().backward()
+    with torch.no_grad():  # inference mode: plain tensors, nothing tracked
+        assert not simulated_flash_attention_forward(module(), qg, kg, vg, None)[0].requires_grad
