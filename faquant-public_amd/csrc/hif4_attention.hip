@@ -366,6 +366,8 @@ __device__ __forceinline__ void qdq_out_row(float (&val)[4][4][4], int half) {
 constexpr int kRowUnits = 17;
 constexpr int kTileBytes = kKeyTile * kRowUnits * 16;  // 34816
 constexpr int kStageBytes = 2 * kTileBytes;             // K tile, then V^T tile
+constexpr int kOutPitch = 136;  // bf16 elements per staged output row (272 B): 8 waves x 32 rows fit one stage
+static_assert(8 * 32 * kOutPitch * 2 <= kStageBytes, "staged output rows must fit one LDS stage");
 
 __device__ __forceinline__ bf16x8 lds_read_at(const uint8_t* base, int byte_off) {
   return *reinterpret_cast<const bf16x8*>(base + byte_off);
@@ -824,6 +826,15 @@ void attn_fwd_kernel(AttnArgs a) {
     }
 
     // ---- epilogue of the item
+    // bf16 rows go out through LDS: once every wave is done with the last tile's stage, each
+    // wave stages its 32 output rows there (272-byte pitch) and stores whole 256-byte rows,
+    // two per instruction.  Stored straight from the MFMA layout, a lane's 16 pieces of
+    // 8 bytes land in 32 rows a position stride apart, each instruction touching 32
+    // partially written cache lines.  (kernel-uniform condition: every wave takes the
+    // barrier)
+    const bool lds_out = !a.o_f32 && !a.mx_out && !a.part_o;
+    uint16_t* const out_rows = reinterpret_cast<uint16_t*>(lds + ((step + 1) & 1) * kStageBytes) + w * (32 * kOutPitch);
+    if (lds_out) __syncthreads();
     if (row_live && !a.mx_out) {
       if (a.part_o) {
         // partial pass: unnormalized O^T column of this row, its l and running maximum
@@ -892,12 +903,30 @@ void attn_fwd_kernel(AttnArgs a) {
             // the values are bf16 already (rounded above, or HiF4 values): pack the upper halves
             const uint32_t w0 = __builtin_amdgcn_perm(__float_as_uint(v[1]), __float_as_uint(v[0]), 0x07060302u);
             const uint32_t w1 = __builtin_amdgcn_perm(__float_as_uint(v[3]), __float_as_uint(v[2]), 0x07060302u);
-            *reinterpret_cast<uint2*>(orow_p + d * 2) = make_uint2(w0, w1);
+            *reinterpret_cast<uint2*>(out_rows + n * kOutPitch + d + 4 * half) = make_uint2(w0, w1);
           }
         }
       }
       }
 
+    }
+    if (lds_out) {
+      // this wave's rows p0w .. p0w + 31: lane l takes 8 bytes (l % 32) of row 2 it + l / 32,
+      // two whole rows per instruction (output rows need only 8-byte alignment); each wave
+      // reads back only what it wrote, and the LDS wait orders its own accesses.  All reads
+      // come before the stores: an LDS read may alias the in-flight LDS-DMA of the next
+      // tile, so each one waits on the whole vector-memory counter, stores included.
+      uint16_t* const o16 = static_cast<uint16_t*>(a.o) + b * a.o_sb + hq * a.o_sh;
+      const int piece = lane & 31;
+      uint2 rows_v[16];
+#pragma unroll
+      for (int it = 0; it < 16; ++it)
+        rows_v[it] = *reinterpret_cast<const uint2*>(out_rows + (2 * it + (lane >> 5)) * kOutPitch + 4 * piece);
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        const int p = p0w + 2 * it + (lane >> 5);
+        if (p < a.Lq) *reinterpret_cast<uint2*>(o16 + static_cast<int64_t>(p) * a.o_sl + 4 * piece) = rows_v[it];
+      }
     }
     ++k_round;
     item = next_item;
