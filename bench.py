@@ -32,12 +32,13 @@ HBM_PEAK_GBPS = 8000.0
 
 # HBM bytes per attention launch, measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and
 # scaled by the same counters on a 256 MiB device copy (bench.py --calibrate-copy):
-# profiles/attn_fwd_<config>_counters.md.  None where no counter run was made.
+# profiles/attn_fwd_qwen8b_32k_counters.md and the traffic tables of the other configs'
+# profiles/attn_fwd_<config>_kernel_trace.md.  None where no counter run was made.
 MEASURED_TRAFFIC_BYTES = {
-    "qwen8b_32k": 1.684e9,
-    "qwen32b_16k": 1.096e9,
-    "wan480p": 1.929e10,
-    "wan720p": 1.081e11,
+    "qwen8b_32k": 1.686e9,
+    "qwen32b_16k": 1.098e9,
+    "wan480p": 1.718e10,
+    "wan720p": 7.523e10,
 }
 
 CONFIGS = {
