@@ -37,8 +37,8 @@ HBM_PEAK_GBPS = 8000.0
 MEASURED_TRAFFIC_BYTES = {
     "qwen8b_32k": 1.686e9,
     "qwen32b_16k": 1.098e9,
-    "wan480p": 1.718e10,
-    "wan720p": 7.523e10,
+    "wan480p": 3.426e9,
+    "wan720p": 5.638e10,
 }
 
 CONFIGS = {

@@ -380,7 +380,8 @@ __device__ __forceinline__ bf16x8 lds_read_at(const uint8_t* base, int byte_off)
 // instantiation keeps each hot loop within its register budget.
 //
 // Work items: item i = y X + x with x = (b, kvh, hg) and y the position block (causal:
-// the longest blocks first); X = B Hkv (Hq / Hkv / hpw), n_items = X n_pblocks.  Workgroup
+// the longest blocks first; non-causal with P % 8 == 0: i = x n_pblocks + y, one head per
+// XCD and round); X = B Hkv (Hq / Hkv / hpw), n_items = X n_pblocks.  Workgroup
 // wid of P = gridDim.x takes items wid, wid + P, wid + 2P, ... (every second round in
 // reverse inside each XCD's share, so large and small items pair up), and runs them as
 // one stream of key tiles: the DMA of the next item's first tile is issued during the
@@ -415,8 +416,15 @@ void attn_fwd_kernel(AttnArgs a) {
   typedef int i32x4 __attribute__((ext_vector_type(4)));
   typedef const __attribute__((address_space(4))) i32x4 const_i4;
 
+  // Non-causal items all span the same keys, so no pairing of long and short items is
+  // needed: items are numbered head-major (i = x n_pblocks + y) and the P / 8 workgroups of
+  // one XCD (wid % 8) take P / 8 consecutive position blocks of one head per round, so
+  // each XCD's L2 serves the K/V tiles of one head (two where a head's blocks end inside
+  // the chunk) to all of its CUs, which stream them in step.
+  const bool head_major = !a.causal && P % 8 == 0;
   // item of round k for this workgroup (n_items or more: none)
   auto item_of = [&](int k) -> int {
+    if (head_major) return k * P + (wid % 8) * (P / 8) + wid / 8;
     const int r = (k & 1) ? ((P % 8 == 0) ? (wid % 8) + 8 * (P / 8 - 1 - wid / 8) : P - 1 - wid) : wid;
     return k * P + r;
   };
@@ -426,7 +434,7 @@ void attn_fwd_kernel(AttnArgs a) {
   };
   auto geo_of = [&](int i) -> Geo {
     Geo g;
-    const int x = i % X, y = i / X;
+    const int x = head_major ? i / a.n_pblocks : i % X, y = head_major ? i % a.n_pblocks : i / X;
     g.hg = x % hgroups;
     g.kvh = (x / hgroups) % a.Hkv;
     g.b = x / (hgroups * a.Hkv);
