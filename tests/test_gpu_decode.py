@@ -144,6 +144,10 @@ SPLIT_CASES = [
     (1, 32, 8, 1, 5000, True, "quantized_same", True, "123", None),   # Qwen3-8B decode step
     (2, 8, 2, 3, 1000, True, "quantized_same", True, "123", 6),
     (1, 4, 4, 1, 777, False, "quantized_same", True, "12", 3),       # non-causal, ragged
+    # non-causal GQA, 2 position blocks per head group: 16 items in the head-major order,
+    # 16 workgroups per range (one round), then 8 per range (two rounds)
+    (2, 32, 4, 64, 3000, False, "quantized_same", True, "123", 4),
+    (2, 32, 4, 64, 3000, False, "unquantized", True, "12", 32),
     (1, 4, 1, 5, 900, True, "unquantized", True, "123", 4),
     (1, 4, 1, 2, 640, True, "quantized_same", False, "123", 5),
     (1, 2, 1, 1, 300, True, "quantized_same", True, "13", 16),       # more ranges than tiles
