@@ -12,7 +12,7 @@ namespace {
 
 template <int LV, int kMask>
 void launch_lv(const AttnArgs& a, int quant_p, int same, dim3 grid, hipStream_t st) {
-  if (a.diag) {  // the probe exists only with P quantization (validated by the caller)
+  if (a.diag || a.p_dump) {  // the probe form exists only with P quantization (validated by the caller)
     if (same) hipLaunchKernelGGL((attn_fwd_kernel<LV, true, true, kMask | 8>), grid, dim3(512), 0, st, a);
     else hipLaunchKernelGGL((attn_fwd_kernel<LV, true, false, kMask | 8>), grid, dim3(512), 0, st, a);
     return;

@@ -154,6 +154,11 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
     if (opts->dense_mask && (!aligned16(opts->dense_mask) || (opts->dm_sb | opts->dm_sh | opts->dm_sq) & 3))
       return fail(FAQ_EINVAL, "%s: the dense mask needs 16-byte aligned rows", who);
     if (opts->pv_probe && !aligned16(opts->pv_probe)) return fail(FAQ_EINVAL, "%s: misaligned pv_probe", who);
+    if (opts->p_dump && !quant_p) return fail(FAQ_EINVAL, "%s: the P dump needs quant_p", who);
+    if (opts->p_dump && (!aligned16(opts->p_dump) || opts->p_dump_stride % 4 ||
+                         opts->p_dump_stride < 128 * ((static_cast<int64_t>(Lk) + 127) / 128)))
+      return fail(FAQ_EINVAL, "%s: p_dump must be 16-byte aligned with a stride >= 128 * ceil(Lk / 128), a multiple of 4",
+                  who);
   }
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "%s: bad sizes", who);
   if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
@@ -211,6 +216,8 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
     a.softcap = opts->softcap;
     a.softcap_rec = opts->softcap > 0.0f ? static_cast<float>(1.0 / static_cast<double>(opts->softcap)) : 0.0f;
     a.diag = opts->pv_probe;
+    a.p_dump = opts->p_dump;
+    a.p_dump_stride = opts->p_dump_stride;
     a.amask = opts->dense_mask;
     a.am_sb = opts->dm_sb;
     a.am_sh = opts->dm_sh;
@@ -486,7 +493,8 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                                  v_sd, Lpad, o, o_dtype, o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p,
                                  p_levels, row_den, 0, opts, a, grid);
   if (rc != FAQ_OK) return rc == 1 ? FAQ_OK : rc;
-  if (a.diag) return fail(FAQ_EINVAL, "faq_attention_fwd_split: the PV-normalizer probe runs in faq_attention_fwd");
+  if (a.diag || a.p_dump)
+    return fail(FAQ_EINVAL, "faq_attention_fwd_split: the PV-normalizer probe and the P dump run in faq_attention_fwd");
   const SplitLayout L = split_layout(B, Hq, Lq, Lk, nsplit);
   if (L.ntiles > faq::kScanMaxTiles)
     return fail(FAQ_EUNSUP, "faq_attention_fwd_split: %d key tiles, the split path handles at most %d", L.ntiles,
@@ -521,6 +529,20 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(faq::kCombineThreads), 0,
                      st, ca);
   return check_launch("faq_attention_fwd_split");
+}
+
+int faq_pquant_groups(const float* p, float* p_hat, int64_t groups, int levels, faq_stream_t stream) {
+  if (groups < 0) return fail(FAQ_EINVAL, "faq_pquant_groups: negative group count");
+  if (!valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
+  if (groups == 0) return FAQ_OK;
+  if (!p || !p_hat || !aligned16(p) || !aligned16(p_hat))
+    return fail(FAQ_EINVAL, "faq_pquant_groups: null or misaligned pointer");
+  const dim3 grid(static_cast<unsigned>((groups + 255) / 256));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (levels == 123) hipLaunchKernelGGL(faq::pquant_groups_kernel<123>, grid, dim3(256), 0, st, p, p_hat, groups);
+  else if (levels == 12) hipLaunchKernelGGL(faq::pquant_groups_kernel<12>, grid, dim3(256), 0, st, p, p_hat, groups);
+  else hipLaunchKernelGGL(faq::pquant_groups_kernel<13>, grid, dim3(256), 0, st, p, p_hat, groups);
+  return check_launch("faq_pquant_groups");
 }
 
 int faq_mfma_probe(float* out, int blocks, int iters, faq_stream_t stream) {

@@ -41,21 +41,21 @@
 // QK and the PV operand reads conflict-free.
 //
 // P quantization in registers (levels 123 shown; 12 and 13 differ only in the micro
-// exponent rule).  Per lane and tile: the group maximum m1 is exp2 of the lane's largest
+// exponent rule), bit-exact with the reference's arithmetic (hif4.py:91-271) on the
+// kernel's own P.  Per lane and tile: the group maximum m1 is exp2 of the lane's largest
 // scaled score (the same fma and exp2 as that element), giving the E6M2 scale s and
-// rec = bf16(1/s).  Per 4-key group with maximum m3, the micro exponent k in {0,1,2}
-// (hif4.py:200-213) is read off K = 2^k = med3(floor2(m3 rec), 2^e2, 4), where
+// rec = bf16(1/s).  Each p is multiplied once, v = RN(p 4 rec) = 4 RN(p rec); the maximum
+// of v over a 4-key group is 4 RN(m3 rec), from which the micro exponent k in {0,1,2}
+// (hif4.py:200-213) is read off 4K = 4 2^k = med3(floor2(4 t3), 4 2^e2, 16), where
 // floor2(x) = 2^floor(log2 x) is a mask of the exponent bits (the comparisons
-// m3 rec >= 2, >= 4 of the reference are exactly floor2 comparisons).  The code is then
-// one fused multiply-add against the magic constant M_K = 2^(23+k):
-//   z = fma(p, 4 rec, M_K)  ->  z = M_K + K * rint(p * 4 rec / K)
-// (M_K has unit-in-last-place K), clamped at M_K + 7K (a 16-bit min of the pattern's low
-// half, which holds the code), and dequantized exactly by
-//   y = fma(z, s/4, -M_K s/4) = K * code * s/4 = code * ds / 4.
-// This equals the reference's floor(fp32(p * qm) * 4 + 0.5) except on the measure-zero
-// sets where p * qm * 4 rounds onto, or is exactly, a half-integer (ties round to even
-// here); P itself already differs from torch.exp by a few ulp, so P^ is compared within
-// the attention tolerance, while the standalone quantizers stay bit-exact.
+// m3 rec >= 2, >= 4 of the reference are exactly floor2 comparisons).  Then, with the
+// reference's two roundings,
+//   w = fma(v, 1/K, 0.5) = RN(RN(p qm) 4 + 0.5),   code = min(floor(w), 7),
+//   y = code * K s / 4 = code * ds / 4
+// (v / K is exact, so the fma rounds only the add, and floor(w) keeps the reference's
+// round-half-up of ties).  P itself differs from torch.exp by a few ulp, so the output is
+// compared with the simulator within a tolerance, while the codes of the kernel's P are
+// compared bit for bit (the probe form below writes P and P^ per key).
 #pragma once
 #include "hif4_device.h"
 
@@ -105,6 +105,10 @@ struct AttnArgs {
   float softcap;  // > 0 (kMask 2, 4): s -> softcap tanh(scale s / softcap)
   float softcap_rec;  // fp32(1 / softcap)
   float* diag;        // PV-normalizer probe (kMode & 8): [rows_total, 5] per-row sums
+  // P dump (kMode & 8 as well): fp32 [rows_total, 2, p_dump_stride]; for every key k of every
+  // processed tile, P at [row][0][k] and P^ at [row][1][k] (keys of skipped tiles untouched)
+  float* p_dump;
+  int64_t p_dump_stride;
   // Dense additive mask (kMask 3, 4; sfa:430-454): fp32 [b, hq, pos, key] at element strides
   // (am_sb, am_sh, am_sq; 0 broadcasts), -inf = masked, Lpad columns with -inf past Lk.
   // Scores become scale s (+ softcap) + mask; the causal flag is not applied.
@@ -217,10 +221,8 @@ __device__ __forceinline__ float fmax_nonneg(float a, float b) {
 
 // Per-lane constants of the HiF4 QDQ of one 64-key P group (p >= 0) with maximum m1.
 struct PQuant {
-  float rec4;   // 4 rec
-  float rec23;  // rec 2^23: floor2(m3 rec23) = 2^(23 + floor(log2 (m3 rec)))
-  float s4;     // s / 4
-  float ns4;    // -s / 4
+  float rec4;  // 4 rec
+  float s16;   // s / 16
 };
 
 // Same values as hif4_scale (hif4.py:91-115) for m1 >= 0: s0 = bf16(m1 bf16(1/div)),
@@ -236,55 +238,85 @@ __device__ __forceinline__ PQuant pquant_setup(float m1) {
   const float rec = bf16_round_hw(__builtin_amdgcn_rcpf(sc));
   PQuant q;
   q.rec4 = rec * 4.0f;
-  q.rec23 = rec * 8388608.0f;
-  q.s4 = sc * 0.25f;
-  q.ns4 = -q.s4;
+  q.s16 = sc * 0.0625f;
   return q;
 }
 
-// Code clamp at 7 of z = M_K + code ulp: M_K = 2^(23 + k) has a zero low half, and the
-// code is at most 8 (p rec / K < 2 within a 4-key group, and m1 rec < 8 for the group
-// maximum), so the low 16 bits of z's pattern are the code.  One 16-bit min against 7 in
-// place (SDWA; the upper half is preserved) replaces a 32-bit min against a per-group
-// bound.
-__device__ __forceinline__ float clamp_code7(float z) {
-  uint32_t u = __float_as_uint(z);
-  asm("v_min_u16_sdwa %0, %0, 7 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_0" : "+v"(u));
-  return __uint_as_float(u);
-}
+// 4K for the micro exponent k of one 4-key group (K = 2^k), from x = floor2 of its
+// v-maximum 4 t3 and e = 4 2^e2 of its 8-key group (levels 123).  Both are 0 or powers of
+// two; med3 clamps floor2(4 t3) into [4 2^e2, 16], which is the reference's lv2 + lv3 rule
+// (hif4.py:200-213): t3 < 2 gives K = 2^e2, t3 in [2, 4) gives K = 2, t3 >= 4 gives K = 4.
+__device__ __forceinline__ float k4_of(float x, float e) { return __builtin_amdgcn_fmed3f(x, e, 16.0f); }
 
-// HiF4 QDQ in place of one 8-key group g[0..7] (two 4-key groups) of a lane's P group.
+// 1/K of 4K (both exact powers of two): an integer subtraction of the exponent fields,
+// 2^-k = (127 - k) << 23 = (256 << 23) - ((129 + k) << 23).
+__device__ __forceinline__ float inv_k_of(float k4) { return __uint_as_float(0x80000000u - __float_as_uint(k4)); }
+
+// HiF4 QDQ in place of one 8-key group g[0..7] (two 4-key groups) of a lane's P group,
+// with the reference's roundings (hif4.py:255-271):
+//   v = RN(p 4 rec), exactly 4 RN(p rec) (the exact scaling by 4 commutes with rounding);
+//   4 t3 = max of v over the 4-key group (rounding is monotonic, so this is 4 RN(m3 rec),
+//     the product the reference compares for the micro exponents);
+//   u = v / K = RN(p qm 4) with qm = rec / K (K a power of two: exact);
+//   w = RN(u + 0.5): one fma of v, 1/K and 0.5 (v / K is exact, so only the add rounds);
+//   code = min(floor(w), 7), value = code K s / 4.
+// floor(RN(u + 0.5)) rounds ties up and gives 1 at u = 0.5 - 2^-25, as the reference's
+// floor(t + 0.5) does.
 template <int LV>
 __device__ __forceinline__ void pquant8(float* g, const PQuant& q) {
-  const float m3a = fmaxf(fmaxf(g[0], g[1]), fmaxf(g[2], g[3]));
-  const float m3b = fmaxf(fmaxf(g[4], g[5]), fmaxf(g[6], g[7]));
-  const float xa = floor2(m3a * q.rec23);
-  const float xb = floor2(m3b * q.rec23);
-  float mka, mkb;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) g[j] = g[j] * q.rec4;
+  const float ma = fmaxf(fmaxf(g[0], g[1]), fmaxf(g[2], g[3]));
+  const float mb = fmaxf(fmaxf(g[4], g[5]), fmaxf(g[6], g[7]));
+  const float xa = floor2(ma);
+  const float xb = floor2(mb);
+  float k4a, k4b;
   if (LV == 123) {
-    // e2 = [max(t3a, t3b) >= 4]; K = med3(floor2(t3), 2^e2, 4), all scaled by 2^23.
-    // 2^e2 2^23 = med3(max(xa, xb) / 2, 2^23, 2^24); the halving is an exponent decrement
-    // (xa, xb are 0 or normal powers of two; 0 becomes -inf, which med3 clamps).
+    // e2 = [max(t3a, t3b) >= 4] <=> max(xa, xb) >= 16; 4 2^e2 = med3(max(xa, xb) / 2, 4, 8),
+    // the halving an exponent decrement (0 becomes -inf, which med3 clamps)
     const float hm = __uint_as_float(max(__float_as_uint(xa), __float_as_uint(xb)) - 0x00800000u);
-    const float e2 = __builtin_amdgcn_fmed3f(hm, 8388608.0f, 16777216.0f);
-    mka = __builtin_amdgcn_fmed3f(xa, e2, 33554432.0f);
-    mkb = __builtin_amdgcn_fmed3f(xb, e2, 33554432.0f);
+    const float e2 = __builtin_amdgcn_fmed3f(hm, 4.0f, 8.0f);
+    k4a = k4_of(xa, e2);
+    k4b = k4_of(xb, e2);
   } else if (LV == 12) {
-    // e2 = [max(t3a, t3b) >= 2], e3 = 0: 2^e2 2^23 = med3(max(xa, xb), 2^23, 2^24)
-    mka = __builtin_amdgcn_fmed3f(fmax_nonneg(xa, xb), 8388608.0f, 16777216.0f);
-    mkb = mka;
+    // e2 = [max(t3a, t3b) >= 2] <=> max(xa, xb) >= 8, e3 = 0
+    k4a = __builtin_amdgcn_fmed3f(fmax_nonneg(xa, xb), 4.0f, 8.0f);
+    k4b = k4a;
   } else {
-    // e2 = 0, e3 = [t3 >= 2]
-    mka = __builtin_amdgcn_fmed3f(xa, 8388608.0f, 16777216.0f);
-    mkb = __builtin_amdgcn_fmed3f(xb, 8388608.0f, 16777216.0f);
+    // e2 = 0, e3 = [t3 >= 2] <=> x >= 8
+    k4a = __builtin_amdgcn_fmed3f(xa, 4.0f, 8.0f);
+    k4b = __builtin_amdgcn_fmed3f(xb, 4.0f, 8.0f);
   }
-  const float nka = mka * q.ns4;
-  const float nkb = mkb * q.ns4;
+  const float ika = inv_k_of(k4a), ikb = inv_k_of(k4b);
+  const float dqa = k4a * q.s16, dqb = k4b * q.s16;  // K s / 4
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    g[j] = __builtin_fmaf(clamp_code7(__builtin_fmaf(g[j], q.rec4, mka)), q.s4, nka);
-    g[4 + j] = __builtin_fmaf(clamp_code7(__builtin_fmaf(g[4 + j], q.rec4, mkb)), q.s4, nkb);
+    g[j] = fminf(floorf(__builtin_fmaf(g[j], ika, 0.5f)), 7.0f) * dqa;
+    g[4 + j] = fminf(floorf(__builtin_fmaf(g[4 + j], ikb, 0.5f)), 7.0f) * dqb;
   }
+}
+
+// The in-register P quantizer of the attention kernel on given values: one lane per
+// 64-value group of non-negative fp32 p, group maximum m1 = max(p) (in the kernel it is
+// exp2 of the largest scaled score, the same value), then pquant_setup and pquant8 on the
+// eight 8-value groups.  A verification entry point for the kernel's codes.
+template <int LV>
+__global__ __launch_bounds__(256) void pquant_groups_kernel(const float* p, float* p_hat, int64_t groups) {
+  const int64_t gi = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gi >= groups) return;
+  const float* src = p + gi * 64;
+  float v[64];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) *reinterpret_cast<float4*>(&v[4 * i]) = *reinterpret_cast<const float4*>(src + 4 * i);
+  float m1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) m1 = fmaxf(m1, v[i]);
+  const PQuant pq = pquant_setup<LV>(m1);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) pquant8<LV>(&v[8 * c], pq);
+  float* dst = p_hat + gi * 64;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) *reinterpret_cast<float4*>(dst + 4 * i) = *reinterpret_cast<const float4*>(&v[4 * i]);
 }
 
 // Value of x in lane l ^ 32 (v_permlane32_swap of a register with itself gives the
@@ -791,6 +823,16 @@ void attn_fwd_kernel(AttnArgs a) {
                   dg_ref = __builtin_fmaf(pu[j], pu[j], dg_ref);
                   dg_zero += (pc[j] == 0.0f && pu[j] > 0.0f) ? 1.0f : 0.0f;
                 }
+                if (a.p_dump && row_live) {
+                  // this chunk's keys key0 + 64 half + 8c .. + 7 (within the padded row)
+                  float* pd = a.p_dump + row * 2 * a.p_dump_stride + key0 + 64 * half + 8 * c;
+#pragma unroll
+                  for (int u = 0; u < 2; ++u) {
+                    *reinterpret_cast<float4*>(pd + 4 * u) = make_float4(pu[4 * u], pu[4 * u + 1], pu[4 * u + 2], pu[4 * u + 3]);
+                    *reinterpret_cast<float4*>(pd + a.p_dump_stride + 4 * u) =
+                        make_float4(pc[4 * u], pc[4 * u + 1], pc[4 * u + 2], pc[4 * u + 3]);
+                  }
+                }
               }
             } else {
               // Unquantized P is not exact in bf16: it goes in as hi + lo bf16 parts
@@ -863,7 +905,7 @@ void attn_fwd_kernel(AttnArgs a) {
       if (kDiag) {
         // per row: sum P^, sum P, #(P^ = 0 < P), sum (P^ - P)^2, sum P^2
         const float zero = halves_sum(dg_zero), err = halves_sum(dg_err), ref = halves_sum(dg_ref);
-        if (half == 0) {
+        if (half == 0 && a.diag) {
           float* dg = a.diag + row * 5;
           dg[0] = kSame ? l : sh_run;
           dg[1] = kSame ? sh_run : l;

@@ -43,6 +43,8 @@ class AttnOpts(ctypes.Structure):
         ("dm_sb", _c_i64),
         ("dm_sh", _c_i64),
         ("dm_sq", _c_i64),
+        ("p_dump", _vp),
+        ("p_dump_stride", _c_i64),
     ]
 
 
@@ -71,6 +73,7 @@ _SIGNATURES = {
     ),
     "faq_attention_split_workspace": ([_c_int, _c_int, _c_int, _c_int, _c_int], _c_i64),
     "faq_mfma_probe": ([_vp, _c_int, _c_int, _vp], _c_int),
+    "faq_pquant_groups": ([_vp, _vp, _c_i64, _c_int, _vp], _c_int),
     "faq_attention_fwd_split": (
         [
             _vp, _c_i64, _c_i64, _c_i64,

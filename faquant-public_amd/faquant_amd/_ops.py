@@ -146,6 +146,19 @@ def act_qdq_rows(
     return y.view(x.shape)
 
 
+def pquant_groups(p: torch.Tensor, levels: str) -> torch.Tensor:
+    """The attention kernel's in-register P quantizer on given non-negative fp32 values
+    ``p[..., 64 n]`` (contiguous), in 64-value groups along the last axis: the HiF4 QDQ of P
+    along keys (sfa:801-806) through the same device code as attention_fwd."""
+    _lib.require_device(p)
+    if p.dtype != torch.float32 or not p.is_contiguous() or p.ndim == 0 or p.shape[-1] % 64:
+        raise ValueError("pquant_groups needs a contiguous fp32 tensor whose last axis is a multiple of 64")
+    out = torch.empty_like(p)
+    _lib.check(_lib.load().faq_pquant_groups(p.data_ptr(), out.data_ptr(), p.numel() // 64, int(levels),
+                                              _lib.stream_ptr(p.device)))
+    return out
+
+
 def _bhld_strides(x: torch.Tensor) -> tuple[int, int, int]:
     if x.stride(-1) != 1:
         raise ValueError("operands need a unit stride along head_dim")
@@ -312,11 +325,14 @@ def dense_attention_mask(mask: torch.Tensor, batch: int, heads: int, query_lengt
 
 
 def _attn_opts(ranges: KeyRanges | None, softcap: float | None, pv_probe: torch.Tensor | None = None,
-               dense_mask: torch.Tensor | None = None):
-    if ranges is None and not softcap and pv_probe is None and dense_mask is None:
+               dense_mask: torch.Tensor | None = None, p_dump: torch.Tensor | None = None):
+    if ranges is None and not softcap and pv_probe is None and dense_mask is None and p_dump is None:
         return None
     opts = _lib.AttnOpts()
     opts.pv_probe = _lib.ptr(pv_probe)
+    if p_dump is not None:
+        opts.p_dump = p_dump.data_ptr()
+        opts.p_dump_stride = p_dump.shape[-1]
     if dense_mask is not None:
         opts.dense_mask = dense_mask.data_ptr()
         sb, sh, sq = (dense_mask.stride(i) if dense_mask.shape[i] > 1 else 0 for i in range(3))
@@ -350,6 +366,7 @@ def attention_fwd(
     softcap: float | None = None,
     pv_probe: torch.Tensor | None = None,
     dense_mask: torch.Tensor | None = None,
+    p_dump: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention over bf16 operands q [B, Hq, Lq, 128], k [B, Hkv, Lk, 128] and
     vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16).
@@ -360,7 +377,10 @@ def attention_fwd(
     needs ``quant_p``) receives the PV-normalizer probe's per-row sums: sum P^, sum P,
     #(P^ = 0 < P), sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869); it runs one pass.
     ``dense_mask`` (dense_attention_mask) is a 3-D/4-D mask: added to the scaled scores in
-    place of the causal rule (sfa:730-757)."""
+    place of the causal rule (sfa:730-757).  ``p_dump`` (fp32 [B, Hq, Lq, 2, W], W a
+    multiple of 4 and >= 128 * ceil(Lk / 128), needs ``quant_p``) receives the kernel's P
+    and P^ for every key of every key tile a row processes (verification of the in-register
+    quantizer); it runs one pass."""
     _lib.require_device(q, k, vt, out, row_den)
     if softcap is not None and softcap < 0:
         raise ValueError("softcap must be non-negative")
@@ -386,7 +406,14 @@ def attention_fwd(
                 or not pv_probe.is_contiguous():
             raise ValueError("pv_probe must be a contiguous fp32 [B, Hq, Lq, 5] tensor")
         split = 1
-    held = _attn_opts(ranges, softcap, pv_probe, dense_mask)
+    if p_dump is not None:
+        _lib.require_device(p_dump)
+        width = p_dump.shape[-1] if p_dump.ndim == 5 else -1
+        if (p_dump.dtype != torch.float32 or tuple(p_dump.shape[:4]) != (q.shape[0], q.shape[1], q.shape[2], 2)
+                or not p_dump.is_contiguous() or width % 4 or width < _pad_keys(int(key_length))):
+            raise ValueError("p_dump must be a contiguous fp32 [B, Hq, Lq, 2, W] tensor, W >= 128 * ceil(Lk / 128)")
+        split = 1
+    held = _attn_opts(ranges, softcap, pv_probe, dense_mask, p_dump)
     opts = held[0] if held else None
     lib = _lib.load()
     B, Hq, Lq, D = q.shape

@@ -39,6 +39,8 @@
  *                         the reference appends one position to its QDQ cache,
  *                         simulated_flash_attention.py:243-289, and runs the tile loop)
  *   faq_attention_split_workspace  workspace size of faq_attention_fwd_split
+ *   faq_pquant_groups     the in-register P quantizer of faq_attention_fwd on given values
+ *                         (simulated_flash_attention.py:801-806 via hif4.py:143-271)
  *   faq_mfma_probe        no reference counterpart: a measurement helper (the device's
  *                         sustained bf16 MFMA rate, the reference point of the benchmark)
  */
@@ -167,6 +169,13 @@ int faq_operand_prep_vt(const void* x, int in_dtype, int64_t sb, int64_t sh, int
  *                   Per row: sum of P-hat and sum of P (each rescaled like the running
  *                   denominator), #(P-hat = 0 < P), sum (P-hat - P)^2 and sum P^2 over
  *                   every processed key.
+ *   p_dump          fp32 [B, Hq, Lq, 2, p_dump_stride] (faq_attention_fwd with quant_p only),
+ *   p_dump_stride   or NULL: for every key k of every key tile a row processes, the kernel's
+ *                   P at [..., 0, k] and its HiF4 QDQ P-hat at [..., 1, k] (keys of skipped
+ *                   tiles are not written; masked and padding keys hold P = 0).  p_dump_stride
+ *                   is a multiple of 4 and >= 128 * ceil(Lk / 128).  For verification: P-hat of
+ *                   each 128-key tile equals fake_quantize_hif4 (hif4.py:377-390) of that
+ *                   tile's P, bit for bit.
  * faq_attention_mask_bounds computes row_lo / row_hi / key_bits from a 2-D mask (or, with
  * mask = NULL, the plain causal / full ranges).
  */
@@ -180,6 +189,8 @@ typedef struct faq_attn_opts {
   float* pv_probe;
   const float* dense_mask;
   int64_t dm_sb, dm_sh, dm_sq;
+  float* p_dump;
+  int64_t p_dump_stride;
 } faq_attn_opts;
 
 /*
@@ -240,6 +251,16 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                             int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p,
                             int p_levels, int norm_same, float* row_den, int nsplit, void* workspace,
                             int64_t workspace_bytes, const faq_attn_opts* opts, faq_stream_t stream);
+
+/*
+ * The attention kernel's in-register P quantizer (the HiF4 QDQ of P along keys,
+ * simulated_flash_attention.py:801-806 through hif4.py:143-271) applied to `groups`
+ * contiguous 64-value groups of non-negative fp32 values p (group maximum from the
+ * values), writing fp32 p_hat.  The same device code as faq_attention_fwd, exposed so
+ * that its codes can be checked against fake_quantize_hif4 on chosen values (ties of
+ * RN(p qm) 4 + 0.5 included).  levels 123 / 12 / 13.
+ */
+int faq_pquant_groups(const float* p, float* p_hat, int64_t groups, int levels, faq_stream_t stream);
 
 /*
  * Measurement helper with no counterpart in the reference: `blocks` workgroups of the
