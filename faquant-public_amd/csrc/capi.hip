@@ -328,6 +328,29 @@ int faq_hadamard_rows(const void* x, void* y, int64_t rows, int64_t cols, int bl
   return check_launch("faq_hadamard_rows");
 }
 
+int faq_hadamard_rows_native(const void* x, void* y, int64_t rows, int64_t cols, int dtype, faq_stream_t stream) {
+  if (!x || !y) return fail(FAQ_EINVAL, "faq_hadamard_rows_native: null input or output");
+  if (cols < 2 || cols > 512 || (cols & (cols - 1)))
+    return fail(cols > 512 && !(cols & (cols - 1)) ? FAQ_EUNSUP : FAQ_EINVAL,
+                cols > 512 && !(cols & (cols - 1)) ? "faq_hadamard_rows_native: dimension %lld above 512"
+                                                   : "Hadamard dimension must be a power of two, got %lld",
+                static_cast<long long>(cols));
+  if (cols % 8) return fail(FAQ_EUNSUP, "faq_hadamard_rows_native: row width must be a multiple of 8");
+  if (dtype != FAQ_BF16 && dtype != FAQ_F16) return fail(FAQ_EINVAL, "faq_hadamard_rows_native: dtype must be bf16 or fp16");
+  if (rows < 0) return fail(FAQ_EINVAL, "faq_hadamard_rows_native: negative size");
+  if (!aligned16(x) || !aligned16(y)) return fail(FAQ_EINVAL, "faq_hadamard_rows_native: pointers must be 16-byte aligned");
+  if (rows == 0) return FAQ_OK;
+  const int n = static_cast<int>(cols);
+  faq::HadamardRowsArgs a{x, y, rows, cols, n, sqrt_div(n)};
+  const dim3 grid(grid_for(rows * (cols / 8)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FAQ_BF16)
+    hipLaunchKernelGGL((faq::hadamard_rows_kernel<__hip_bfloat16, __hip_bfloat16, true>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((faq::hadamard_rows_kernel<__half, __half, true>), grid, dim3(256), 0, st, a);
+  return check_launch("faq_hadamard_rows_native");
+}
+
 int faq_hif4_unpack_rows(const uint8_t* codes, const uint8_t* scale_byte, const uint8_t* lv2_bits,
                          const uint16_t* lv3_bits, int64_t rows, int64_t cols, int out_dtype, void* y,
                          faq_stream_t stream) {

@@ -415,7 +415,30 @@ struct HadamardRowsArgs {
   SqrtDiv div;    // division by fp32(sqrt(n))
 };
 
-template <typename Tin, typename Tout>
+// The stages of fwht8_lanes with every value rounded to T after each stage: the
+// reference's butterflies on a bf16 / fp16 tensor, where each `left + right` and
+// `left - right` is an fp32 add rounded to the tensor's dtype (rotation.py:21-27).
+template <typename T>
+__device__ __forceinline__ void fwht8_lanes_rounded(float* v, int n) {
+  auto rnd = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(v[i]);
+  };
+  if (n >= 2) { fwht_inlane_stage<1>(v); rnd(); }
+  if (n >= 4) { fwht_inlane_stage<2>(v); rnd(); }
+  if (n >= 8) { fwht_inlane_stage<4>(v); rnd(); }
+  if (n > 8) { fwht_lane_stage<1>(v); rnd(); }
+  if (n > 16) { fwht_lane_stage<2>(v); rnd(); }
+  if (n > 32) { fwht_lane_stage<4>(v); rnd(); }
+  if (n > 64) { fwht_lane_stage<8>(v); rnd(); }
+  if (n > 128) { fwht_lane_stage<16>(v); rnd(); }
+  if (n > 256) { fwht_lane_stage<32>(v); rnd(); }
+}
+
+// kStageRound: the transform in the tensor's own dtype (Tin == Tout, hadamard_transform
+// on a bf16 / fp16 tensor); the division's fp32 quotient is rounded to Tout by the store,
+// as torch rounds its fp32 opmath result.  Otherwise fp32 butterflies and one rounding.
+template <typename Tin, typename Tout, bool kStageRound = false>
 __global__ __launch_bounds__(256) void hadamard_rows_kernel(HadamardRowsArgs a) {
   const int64_t lanes_per_row = a.cols / 8;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -429,7 +452,8 @@ __global__ __launch_bounds__(256) void hadamard_rows_kernel(HadamardRowsArgs a) 
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = 0.0f;
   }
-  fwht8_lanes(v, a.n);
+  if (kStageRound) fwht8_lanes_rounded<Tout>(v, a.n);
+  else fwht8_lanes(v, a.n);
   div_sqrt_n(v, a.div);
   if (live) Io<Tout>::store8(static_cast<Tout*>(a.y) + row * a.cols + c0, v);
 }

@@ -58,6 +58,7 @@ _SIGNATURES = {
         _c_int,
     ),
     "faq_hadamard_rows": ([_vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp], _c_int),
+    "faq_hadamard_rows_native": ([_vp, _vp, _c_i64, _c_i64, _c_int, _vp], _c_int),
     "faq_act_qdq_rows": ([_vp, _vp, _c_i64, _c_i64, _c_int, _vp, _c_int, _c_int, _vp], _c_int),
     "faq_hif4_unpack_rows": ([_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _vp, _vp], _c_int),
     "faq_operand_prep": (

@@ -113,6 +113,20 @@ def hadamard_rows(x: torch.Tensor, block: int, out_dtype: torch.dtype | None = N
     return y
 
 
+def hadamard_rows_native(x: torch.Tensor) -> torch.Tensor:
+    """Normalized Hadamard over the last axis of a bf16 / fp16 tensor computed in that dtype
+    (every butterfly stage rounded to it, rotation.py:14-29 on such a tensor)."""
+    _lib.require_device(x)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("hadamard_rows_native takes bf16 or fp16")
+    xc = x.contiguous()
+    y = torch.empty_like(xc)
+    cols = x.shape[-1]
+    _lib.check(_lib.load().faq_hadamard_rows_native(xc.data_ptr(), y.data_ptr(), xc.numel() // max(cols, 1), cols,
+                                                     _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device)))
+    return y.view(x.shape)
+
+
 def act_qdq_rows(
     x: torch.Tensor,
     *,

@@ -21,6 +21,7 @@ from typing import Optional
 import torch
 
 from . import _lib, _ops
+from .config import PV_NORMALIZER_MODES
 from .hif4 import HIF4_ACT_SCALE_LEVELS, HIF4_ATTN_OPERAND_SCALE_LEVELS
 from .hif4 import _resolve as resolve_hif4_levels
 from .quantization import check_hif4_arguments, fake_quantize
@@ -104,16 +105,23 @@ def attention_core(
     *,
     scaling: Optional[float] = None,
     attention_mask: Optional[torch.Tensor] = None,
+    sliding_window: Optional[int] = None,
+    cache_position: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Post-RoPE Q/K/V -> attention output [B, L, Hq, 128], fused on the GPU.
 
-    Equivalent to the reference's excursion followed by
-    ``simulated_flash_attention_forward(module, q, k, v, attention_mask, scaling=scaling)``
-    (qwen3.py:97-166); a 2-D padding mask runs as per-row key ranges in the same fused
-    launch, anything the fused path does not take goes through that drop-in.  When the module
-    enables the attention-output quantizer (``faquant_attention_output_quant`` and o_proj
-    does not quantize its own input, qwen3.py:167-171), the HiF4 QDQ of the output rows
-    with ``faquant_core_quant_kwargs`` runs in the attention kernel's epilogue.
+    Equivalent to the reference's excursion, the optional Q/K/V input QDQ
+    (``faquant_attention_input_quant`` with ``faquant_core_quant_kwargs``, qwen3.py:132-136)
+    and ``simulated_flash_attention_forward(module, q, k, v, attention_mask, scaling=scaling,
+    sliding_window=sliding_window, cache_position=cache_position)`` (qwen3.py:97-166).  Keys
+    past the valid length (a static cache's backing tensor beyond the mask or
+    ``cache_position``) are dropped first, as the simulator does (sfa:511-520).  A 2-D
+    padding mask and a sliding window run as per-row key ranges in the same fused launch;
+    the input QDQ, the PV-normalizer probe and anything else the fused path does not take go
+    through the drop-in.  When the module enables the attention-output quantizer
+    (``faquant_attention_output_quant`` and o_proj does not quantize its own input,
+    qwen3.py:167-171), the HiF4 QDQ of the output rows with ``faquant_core_quant_kwargs``
+    runs in the attention kernel's epilogue.
     """
     smooth_scale = _smooth(getattr(module, "faquant_qk_smooth_scale", None),
                            getattr(module, "faquant_qk_smooth_delta", None))
@@ -122,14 +130,37 @@ def attention_core(
     block = _block(rotation, getattr(module, "faquant_qk_rotation_block_size", None), query.shape[-1])
     qk_quant = bool(module.faquant_qk_matmul_quant)
     pv_quant = bool(module.faquant_pv_matmul_quant)
-    fused = (query.dtype == torch.bfloat16 and int(module.faquant_attention_key_chunk_size) == _ops.KEY_TILE
+    mode = getattr(module, "faquant_pv_normalizer_mode", "unquantized")
+    if mode not in PV_NORMALIZER_MODES:
+        raise ValueError(f"unsupported pv_normalizer_mode {mode!r}; expected one of {PV_NORMALIZER_MODES}")
+    if sliding_window is not None and sliding_window <= 0:
+        raise ValueError("sliding_window must be positive")
+    valid = key.shape[-2]
+    if attention_mask is not None:
+        valid = min(valid, attention_mask.shape[-1])
+    if isinstance(cache_position, torch.Tensor) and cache_position.numel():
+        valid = min(valid, int(cache_position.max().item()) + 1)
+    if valid < key.shape[-2]:
+        key = key[:, :, :valid]
+        value = value[:, :, :valid]
+    input_quant = bool(getattr(module, "faquant_attention_input_quant", False))
+    probe = pv_quant and isinstance(getattr(module, "faquant_pv_normalizer_diagnostics", None), dict)
+    fused = (not input_quant and not probe and query.dtype == torch.bfloat16
+             and int(module.faquant_attention_key_chunk_size) == _ops.KEY_TILE
              and (attention_mask is None or (attention_mask.ndim == 2 and attention_mask.shape[-1] == key.shape[2])))
     if not fused:
         q, k = post_rope_qk_transform(
             query, key, smooth_scale=smooth_scale, key_offset=key_offset, rotation=rotation,
             rotation_block_size=getattr(module, "faquant_qk_rotation_block_size", None),
         )
-        out = simulated_flash_attention_forward(module, q, k, value, attention_mask, scaling=scaling)[0]
+        v = value
+        if input_quant:
+            # the excursion's output, then the core quantizer, then the simulator's own
+            # operand QDQ (HiF4 QDQ is not idempotent: both run)
+            kwargs = module.faquant_core_quant_kwargs
+            q, k, v = (fake_quantize(t, **kwargs) for t in (q, k, v))
+        out = simulated_flash_attention_forward(module, q, k, v, attention_mask, scaling=scaling,
+                                                sliding_window=sliding_window, cache_position=cache_position)[0]
         if _output_quant_levels(module) is not None:
             out = fake_quantize(out.reshape(*out.shape[:2], -1), **module.faquant_core_quant_kwargs).view(out.shape)
         return out
@@ -149,16 +180,17 @@ def attention_core(
     scale = float(scaling if scaling is not None else D**-0.5)
     causal = bool(getattr(module, "is_causal", True))
     out = torch.empty((B, Lq, Hq, D), device=query.device, dtype=query.dtype)
-    mode = getattr(module, "faquant_pv_normalizer_mode", "unquantized")
     ranges, masked = key_ranges(module, attention_mask, batch=B, query_length=Lq, key_length=Lk, causal=causal,
-                                sliding_window=None, device=query.device)
+                                sliding_window=sliding_window, device=query.device)
     _ops.attention_fwd(q_op, k_op, vt, Lk, causal=causal, scale=scale, quant_p=pv_quant,
                        p_levels=levels["p"], norm_same=mode == "quantized_same", out=out.transpose(1, 2),
                        out_levels=_output_quant_levels(module), ranges=ranges)
     count_tiles(
         module.faquant_simulated_attention_stats, batch=B, query_heads=Hq, query_length=Lq, key_length=Lk,
         head_dim=D, query_chunk=int(module.faquant_attention_query_chunk_size), key_chunk=_ops.KEY_TILE,
-        causal=causal, skip_fully_masked=bool(getattr(module, "faquant_skip_fully_masked_tiles", True)) and not masked,
+        causal=causal,
+        skip_fully_masked=bool(getattr(module, "faquant_skip_fully_masked_tiles", True)) and not masked
+        and sliding_window is None,
         qk_quant=qk_quant, pv_quant=pv_quant, qk_group=qk_group, pv_group=pv_group,
     )
     return _lib.forward_only(out, query, key, value)

@@ -18,14 +18,18 @@ def _is_power_of_two(value: int) -> bool:
 
 
 def hadamard_transform(x: torch.Tensor) -> torch.Tensor:
-    """Normalized Walsh-Hadamard transform over the final axis (fp32 input)."""
+    """Normalized Walsh-Hadamard transform over the final axis, computed in ``x.dtype`` as
+    the reference's butterflies are (rotation.py:14-29): fp32 exactly, bf16 / fp16 with
+    every stage rounded to that dtype.  Sizes up to 512 (the head_dim and Linear-block
+    range of the hot path)."""
     size = x.shape[-1]
     if not _is_power_of_two(size):
         raise ValueError(f"Hadamard dimension must be a power of two, got {size}")
-    if x.dtype != torch.float32:
-        # The reference runs the butterflies in x.dtype; its callers always pass fp32.
-        raise NotImplementedError("hadamard_transform on the MI355X takes fp32 input")
-    return _ops.hadamard_rows(x, size, torch.float32)
+    if x.dtype == torch.float32:
+        return _ops.hadamard_rows(x, size, torch.float32)
+    if x.dtype in (torch.bfloat16, torch.float16):
+        return _ops.hadamard_rows_native(x)
+    raise NotImplementedError(f"hadamard_transform on the MI355X takes fp32, bf16 or fp16 input, got {x.dtype}")
 
 
 def chunked_block_hadamard_transform(x: torch.Tensor, *, block_size: int, chunk_rows: int = 256) -> torch.Tensor:

@@ -10,8 +10,10 @@ Supported on the GPU: head_dim 128, key tiles of 128 (the reference default),
 the HiF4 format with groups of 64 (or no quantization), causal (bottom-right)
 or full attention, 2-D attention masks (padding, in the reference's rank form),
 3-D/4-D masks (boolean or additive), sliding windows, the logit softcap, the
-PV-normalizer probe, bf16 or fp32 inputs.  Everything else the reference accepts
-(int/MXFP8 formats) raises NotImplementedError: there is no fallback path.
+PV-normalizer probe, bf16 or fp32 inputs (fp32 with the matching QK / PV
+quantization enabled: the kernel multiplies bf16 operands, and HiF4 values are exact in
+bf16).  Everything else the reference accepts (int/MXFP8 formats, unquantized fp32
+matmuls) raises NotImplementedError: there is no fallback path.
 """
 
 from __future__ import annotations
@@ -397,6 +399,17 @@ def simulated_flash_attention_forward(
     for t in (query, key, value):
         if t.dtype not in (torch.float32, torch.bfloat16):
             raise NotImplementedError(f"the HIP attention path takes bf16 or fp32 operands, got {t.dtype}")
+    # The kernel multiplies bf16 operands.  Quantized operands are HiF4 values, exact in bf16;
+    # without quantization the reference multiplies the inputs themselves in fp32 (sfa:723-724,
+    # 848-850), which only bf16 inputs reproduce.
+    if not qk_quant and (query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16):
+        raise NotImplementedError(
+            "QK without quantization multiplies bf16 operands on the MI355X: pass bf16 Q/K or enable "
+            "faquant_qk_matmul_quant (fp32 Q/K would be rounded to bf16)")
+    if not pv_quant and value.dtype != torch.bfloat16:
+        raise NotImplementedError(
+            "PV without quantization multiplies bf16 V on the MI355X: pass bf16 V or enable "
+            "faquant_pv_matmul_quant (fp32 V would be rounded to bf16)")
     qk_group = _hif4_group(qk_quant_kwargs, "QK") if qk_quant else 64
     pv_group = _hif4_group(pv_quant_kwargs, "PV") if pv_quant else 64
     diagnostics = getattr(module, "faquant_pv_normalizer_diagnostics", None)

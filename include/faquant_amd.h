@@ -16,6 +16,8 @@
  *                         hif4.py:377-390 fake_quantize_hif4,
  *                         src/faquant/quantization.py:30-57 fake_quantize(quant_format="hif4"),
  *                         src/faquant/wan22_attention.py:97-102 qdq_rows_128
+ *   faq_hadamard_rows_native  src/faquant/rotation.py:14-29 hadamard_transform on a bf16 /
+ *                         fp16 tensor (butterflies rounded to that dtype)
  *   faq_hadamard_rows     src/faquant/rotation.py:14-29 hadamard_transform,
  *                         rotation.py:117-135 chunked_block_hadamard_transform,
  *                         src/faquant/wan22_attention.py:186-192 rotate_heads
@@ -111,6 +113,15 @@ int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_
                      const float* key_offset, int64_t off_sh, const float* smooth, int64_t smooth_sh,
                      int smooth_divide, int hadamard, int round_dtype, void* rotated, void* y, int64_t yb,
                      int64_t yh, int64_t yl, int levels, faq_stream_t stream);
+
+/*
+ * Normalized Walsh-Hadamard transform over rows of `cols` values (cols a power of two in
+ * [8, 512]) computed in the tensor's own dtype (FAQ_BF16 or FAQ_F16), as
+ * src/faquant/rotation.py:14-29 hadamard_transform runs on such a tensor: after every
+ * butterfly stage each fp32 sum or difference is rounded to the dtype, and the division by
+ * fp32(sqrt(cols)) is rounded once more.  y may alias x.
+ */
+int faq_hadamard_rows_native(const void* x, void* y, int64_t rows, int64_t cols, int dtype, faq_stream_t stream);
 
 /*
  * Values of the packed HiF4 storage view written by faq_hif4_qdq_rows (4-bit codes, low

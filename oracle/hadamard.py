@@ -16,7 +16,8 @@ by a Python float scalar rather than multiplying by its reciprocal).
 Parity pins (tests/test_oracle_hadamard.py): the dense Sylvester-matrix closed
 form in float64 (as tests/test_hisq_rotation.py:29-43 builds it), orthogonality
 and self-inverse (tests/test_rotation.py:10-18), chunked-equals-full, the exact
-64-point case, and golden vectors written by the reference.
+64-point case, and golden vectors written by the reference (fp32, and bf16 / fp16
+tensors with their per-stage rounding).
 """
 
 from __future__ import annotations
@@ -32,9 +33,15 @@ def _is_power_of_two(v: int) -> bool:
     return v > 0 and v & (v - 1) == 0
 
 
-def hadamard_transform(x: np.ndarray) -> np.ndarray:
-    """Normalized FWHT over the last axis, computed in x's float32 values."""
+def hadamard_transform(x: np.ndarray, stage_round=None) -> np.ndarray:
+    """Normalized FWHT over the last axis, computed in x's float32 values.
+
+    ``stage_round`` (e.g. ``hif4.bf16_round``) is the transform on a bf16 / fp16 tensor:
+    torch computes each ``left + right``, ``left - right`` and the final division in
+    fp32 and rounds the result to the tensor's dtype (rotation.py:21-28 in that dtype).
+    """
     x = np.asarray(x, dtype=_F32)
+    rnd = stage_round if stage_round is not None else (lambda a: a)
     n = x.shape[-1]
     if not _is_power_of_two(n):
         raise ValueError(f"Hadamard dimension must be a power of two, got {n}")
@@ -45,9 +52,9 @@ def hadamard_transform(x: np.ndarray) -> np.ndarray:
         left = v[:, :, 0, :]
         right = v[:, :, 1, :]
         out = np.concatenate(((left + right)[:, :, None, :], (left - right)[:, :, None, :]), axis=2)
-        out = out.reshape(-1, n).astype(_F32)
+        out = rnd(out.reshape(-1, n).astype(_F32))
         stride *= 2
-    out = (out / _F32(math.sqrt(n))).astype(_F32)
+    out = rnd((out / _F32(math.sqrt(n))).astype(_F32))
     return out.reshape(x.shape)
 
 

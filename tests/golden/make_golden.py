@@ -20,6 +20,10 @@ Fixtures (numpy .npz, float32 unless noted):
                       (block 64) on fp32 rows; Qwen/Wan prologue outputs (bf16).
   attention.npz       simulated_flash_attention_forward with HiF4 Q/K/P/V at the
                       configuration shapes listed in CASES.
+  hadamard_native.npz hadamard_transform on bf16 and fp16 tensors (the butterflies run
+                      in the tensor's dtype, each stage rounded), n = 8, 64, 128, 512.
+
+``python tests/golden/make_golden.py hadamard_native`` writes only that file.
 """
 
 from __future__ import annotations
@@ -194,12 +198,32 @@ def make_attention() -> dict[str, np.ndarray]:
     return out
 
 
+def make_hadamard_native() -> dict[str, np.ndarray]:
+    """hadamard_transform on bf16 / fp16 tensors: torch rounds every `left + right`,
+    `left - right` and the final division to the tensor's dtype (rotation.py:14-29)."""
+    out: dict[str, np.ndarray] = {}
+    g = inputs.rng(23)
+    for n in (8, 64, 128, 512):
+        x = (g.standard_normal((max(4096 // n, 8), n)) * g.uniform(0.01, 100, size=(max(4096 // n, 8), 1)))
+        x = x.astype(np.float32)
+        for name, dt in (("bf16", torch.bfloat16), ("fp16", torch.float16)):
+            t = torch.from_numpy(x).to(dt)
+            out[f"x_{name}_{n}"] = t.float().numpy()
+            out[f"h_{name}_{n}"] = hadamard_transform(t).float().numpy()
+    return out
+
+
 def main() -> None:
     torch.set_num_threads(os.cpu_count() or 1)
+    if sys.argv[1:] == ["hadamard_native"]:
+        np.savez_compressed(os.path.join(HERE, "hadamard_native.npz"), **make_hadamard_native())
+        print("hadamard_native.npz", os.path.getsize(os.path.join(HERE, "hadamard_native.npz")))
+        return
     np.savez_compressed(os.path.join(HERE, "hif4_codec.npz"), **make_codec())
     np.savez_compressed(os.path.join(HERE, "hadamard.npz"), **make_hadamard())
     np.savez_compressed(os.path.join(HERE, "attention.npz"), **make_attention())
-    for name in ("hif4_codec.npz", "hadamard.npz", "attention.npz"):
+    np.savez_compressed(os.path.join(HERE, "hadamard_native.npz"), **make_hadamard_native())
+    for name in ("hif4_codec.npz", "hadamard.npz", "attention.npz", "hadamard_native.npz"):
         print(name, os.path.getsize(os.path.join(HERE, name)))
 
 

@@ -40,7 +40,7 @@ def test_header_lists_the_entry_points():
         ["faq_last_error", "faq_version", "faq_hif4_qdq_rows", "faq_hif4_unpack_rows", "faq_hadamard_rows",
          "faq_act_qdq_rows", "faq_operand_prep", "faq_operand_prep_vt", "faq_attention_fwd",
          "faq_attention_fwd_split", "faq_attention_split_workspace", "faq_attention_mask_bounds",
-         "faq_mfma_probe", "faq_pquant_groups"]
+         "faq_mfma_probe", "faq_pquant_groups", "faq_hadamard_rows_native"]
     )
 
 
@@ -213,3 +213,46 @@ def test_split_count_rule():
     assert _ops._split_count(16, 32, 8, 1, 32768) == 2                    # 128 items: two ranges
     assert _ops._split_count(1, 32, 8, 1, 32768, cus=80) == 10            # fewer CUs, fewer ranges
     assert _ops._split_count(1, 32, 8, 1, (_ops.SPLIT_MAX_TILES + 1) * 128) == 1
+
+
+def test_unquantized_fp32_matmuls_are_refused():
+    """Without QK (PV) quantization the reference multiplies the fp32 inputs themselves
+    (sfa:723-724, 848-850); the kernel multiplies bf16 operands, so fp32 Q/K (V) with that
+    flag off raise NotImplementedError instead of being rounded silently."""
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward as f
+
+    q, k = torch.zeros(1, 2, 3, 128), torch.zeros(1, 1, 3, 128)
+    mod = _module()
+    mod.faquant_qk_matmul_quant = False
+    with pytest.raises(NotImplementedError, match="bf16 Q/K"):
+        f(mod, q, k, k, None)
+    mod = _module()
+    mod.faquant_pv_matmul_quant = False
+    with pytest.raises(NotImplementedError, match="bf16 V"):
+        f(mod, q.bfloat16(), k.bfloat16(), k, None)
+
+
+def test_attention_core_validates_like_the_drop_in():
+    from faquant_amd.qwen3 import attention_core
+
+    q, k = torch.zeros(1, 2, 3, 128, dtype=torch.bfloat16), torch.zeros(1, 1, 3, 128, dtype=torch.bfloat16)
+    mod = _module()
+    mod.faquant_pv_normalizer_mode = "quantized"
+    with pytest.raises(ValueError, match="pv_normalizer_mode"):
+        attention_core(mod, q, k, k)
+    with pytest.raises(ValueError, match="sliding_window must be positive"):
+        attention_core(_module(), q, k, k, sliding_window=0)
+
+
+def test_pquant_groups_validation(lib):
+    from faquant_amd import _lib
+
+    assert lib.faq_pquant_groups(None, None, 1, 123, None) == _lib.EINVAL
+    assert lib.faq_pquant_groups(None, None, 1, 7, None) == _lib.EINVAL
+    assert "levels" in lib.faq_last_error().decode()
+    assert lib.faq_pquant_groups(None, None, 0, 123, None) == _lib.OK
+    assert lib.faq_hadamard_rows_native(None, None, 1, 128, 1, None) == _lib.EINVAL
+    p16 = ctypes.c_void_p(1 << 20)
+    assert lib.faq_hadamard_rows_native(p16, p16, 1, 96, 1, None) == _lib.EINVAL
+    assert lib.faq_hadamard_rows_native(p16, p16, 1, 1024, 1, None) == _lib.EUNSUP
+    assert lib.faq_hadamard_rows_native(p16, p16, 1, 128, 0, None) == _lib.EINVAL

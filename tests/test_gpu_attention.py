@@ -1,13 +1,14 @@
 """GPU parity of the HiF4 QK/PV attention kernel against the oracle and the reference goldens.
 
-Tolerance (fp32 math): the kernel computes P with a
-hardware exp2 on log2-scaled scores and sums in MFMA order, the oracle with
-numpy exp and BLAS order, so a few P codes flip at rounding boundaries.  The
-bar is a relative Frobenius error <= 2e-3 and a max abs error <= 2e-2 of the
-output's max magnitude (the reference measured its own Triton kernel at 4-7e-4
-relative error against its simulator, docs/WAN22.md:172-175).  Identities
-(constant V under P-Reordering, fused == unfused prologue) are checked to a few
-ulps or bitwise.
+Tolerance (fp32 math): the kernel's P-hat codes equal the reference quantizer's on the
+kernel's own P bit for bit (tests/test_gpu_pquant.py), but that P comes from a hardware
+exp2 on log2-scaled scores summed in MFMA order, the oracle's from numpy exp on BLAS-order
+sums, so P differs by a few ulp and a few P codes flip where P lies on a rounding boundary
+(the flip rate is measured in test_gpu_pquant.py).  The bar is a relative Frobenius error
+<= 1e-3 and a max abs error <= 1e-2 of the output's max magnitude (the reference measured
+its own Triton kernel at 4-7e-4 relative error against its simulator,
+docs/WAN22.md:172-175).  Identities (constant V under P-Reordering, fused == unfused
+prologue) are checked to a few ulps or bitwise.
 """
 
 from __future__ import annotations
@@ -26,8 +27,8 @@ from tests.golden.cases import CASES, build_inputs, golden_output
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-FRO_TOL = 2e-3
-MAX_TOL = 2e-2
+FRO_TOL = 1e-3
+MAX_TOL = 1e-2
 
 
 def to_dev(a, dev, dtype=torch.float32):
@@ -269,47 +270,6 @@ def test_qwen_attention_core_equals_two_step(dev):
                                         rotation_block_size=block)
         two, _ = simulated_flash_attention_forward(module(), qr, kr, v, None)
         assert torch.equal(fused, two)
-
-
-@pytest.mark.parametrize("cfg", ["qwen8b_32k", "wan480p"])
-def test_full_size_sampled_rows_match_oracle(dev, cfg):
-    """At the benchmark shapes, rows sampled from the GPU output match the oracle run on
-    just those rows (causal rows [p0, p1) == oracle with Lq = p1 - p0 over keys [0, p1))."""
-    import time
-
-    from faquant_amd import _ops
-
-    if cfg == "qwen8b_32k":
-        B, Hq, Hkv, L, causal = 1, 32, 8, 32768, True
-    else:
-        B, Hq, Hkv, L, causal = 1, 40, 40, 32760, False
-    t0 = time.time()
-    gen = torch.Generator(device=dev).manual_seed(1234)
-    q = torch.randn((B, Hq, L, 128), device=dev, generator=gen).to(torch.bfloat16)
-    k = torch.randn((B, Hkv, L, 128), device=dev, generator=gen).to(torch.bfloat16)
-    v = torch.randn((B, Hkv, L, 128), device=dev, generator=gen).to(torch.bfloat16)
-    qh, _ = _ops.operand_prep(q, levels="123", hadamard=128)
-    kh, _ = _ops.operand_prep(k, levels="123", hadamard=128)
-    vt = _ops.operand_prep_vt(v, levels="123")
-    out = torch.empty((B, L, Hq, 128), device=dev, dtype=torch.float32)
-    _ops.attention_fwd(qh, kh, vt, L, causal=causal, scale=128**-0.5, quant_p=True, p_levels="123",
-                       norm_same=True, out=out.transpose(1, 2))
-    torch.cuda.synchronize()
-    print(f"[full] {cfg} gpu done in {time.time() - t0:.1f}s", flush=True)
-    G = Hq // Hkv
-    heads = [0, Hq - 1]
-    for p0, p1 in ((L - 48, L), (L // 2 - 16, L // 2 + 16)):
-        for h in heads:
-            hk = h // G
-            qs = qh[:, h : h + 1, p0:p1].float().cpu().numpy()
-            kend = p1 if causal else L
-            ks = kh[:, hk : hk + 1, :kend].float().cpu().numpy()
-            # raw V: the oracle quantizes it (HiF4 QDQ is not idempotent)
-            vs = v[:, hk : hk + 1, :kend].float().cpu().numpy()
-            ref = _oracle(qs, ks, vs, causal=causal, qk=False, pv=True, levels="123")
-            got = out[:, p0:p1, h : h + 1].cpu().numpy()
-            assert_close_attention(got, ref, f"{cfg} rows {p0}:{p1} head {h}")
-    print(f"[full] {cfg} checked in {time.time() - t0:.1f}s", flush=True)
 
 
 def test_hif4_sign_symmetry_and_power_of_two_equivariance(dev):

@@ -163,6 +163,26 @@ def test_hadamard_golden_bit_exact(dev, golden_hadamard):
     np.testing.assert_array_equal(bits(chunked_block_hadamard_transform(x, block_size=64)), g["blk64"].view(np.uint32))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("n", [8, 64, 128, 512])
+def test_hadamard_in_tensor_dtype_matches_reference_goldens(dev, dt, n):
+    """hadamard_transform of a bf16 / fp16 tensor runs its butterflies in that dtype
+    (rotation.py:14-29): bitwise the reference's output, and the oracle's stage-rounded form
+    on random rows."""
+    from faquant_amd.rotation import hadamard_transform
+    from tests.conftest import load_golden
+
+    g = load_golden("hadamard_native.npz")
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    got = hadamard_transform(to_dev(g[f"x_{dt}_{n}"], dev, tdt))
+    assert got.dtype == tdt
+    np.testing.assert_array_equal(got.float().cpu().numpy().view(np.uint32), g[f"h_{dt}_{n}"].view(np.uint32))
+    rnd = OQ.bf16_round if dt == "bf16" else OQ.fp16_round
+    x = rnd(np.random.Generator(np.random.PCG64(n + 7)).standard_normal((777, n)).astype(np.float32) * 3)
+    got = hadamard_transform(to_dev(x, dev, tdt)).float().cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), OH.hadamard_transform(x, stage_round=rnd).view(np.uint32))
+
+
 @pytest.mark.parametrize("n", [2, 8, 16, 32, 64, 128, 256, 512])
 def test_hadamard_sizes_bit_exact(dev, n):
     from faquant_amd.rotation import hadamard_transform

@@ -123,3 +123,31 @@ def test_attention_p_hat_bit_exact_per_tile(dev, B, Hq, Hkv, Lq, Lk, causal, lev
           f"max |P - exp(S - m)| {worst_p:.2e}", flush=True)
     assert done.any() and int(bad.sum()) == 0
     assert worst_p < 1e-4
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("causal,levels", [(True, "123"), (False, "12")])
+def test_p_hat_flip_rate_against_the_oracle_softmax(dev, causal, levels):
+    """How many P-hat codes differ from the reference's own tile computation (fp32 S from
+    a float32 matmul, s scale, running max, numpy exp, then the oracle quantizer): the
+    codes only differ where the two P values straddle a rounding boundary."""
+    B, Hq, Hkv, L = 1, 8, 2, 640
+    qh, kh, dump, scale = _p_dump(dev, 77, B, Hq, Hkv, L, L, causal, levels)
+    G = Hq // Hkv
+    nt = L // 128
+    s = np.matmul(qh, np.swapaxes(np.repeat(kh, G, axis=1), -1, -2)).astype(np.float32)
+    s = (s * np.float32(scale)).astype(np.float32)
+    if causal:
+        s = np.where(np.arange(L)[None, :] > np.arange(L)[:, None], -np.inf, s).astype(np.float32)
+    t = s.reshape(B, Hq, L, nt, 128)
+    m = np.maximum.accumulate(t.max(axis=-1), axis=-1).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        p = np.where(np.isfinite(t), np.exp((t - m[..., None]).astype(np.float32)), 0.0).astype(np.float32)
+    ref = OQ.fake_quantize_hif4(p, levels, "float32")
+    ph = dump[:, :, :, 1].reshape(B, Hq, L, nt, 128)
+    done = ~np.isnan(ph).any(axis=-1)
+    flips = int(((ref != ph) & done[..., None]).sum())
+    total = int(done.sum()) * 128
+    rel_p = float(np.nanmax(np.abs(dump[:, :, :, 0].reshape(p.shape) - p)[done]))
+    print(f"P-hat flips vs the oracle's exp: {flips} of {total} ({flips / total:.2e}); max |dP| {rel_p:.2e}", flush=True)
+    assert flips / total < 1e-3

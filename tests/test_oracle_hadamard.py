@@ -4,7 +4,10 @@ import numpy as np
 import pytest
 
 from oracle import hadamard
+from oracle import hadamard as OH
+from oracle import hif4 as OQ
 from oracle.hif4 import bf16_round
+from tests.conftest import load_golden
 
 
 def test_matches_reference_golden_vectors(golden_hadamard):
@@ -71,3 +74,17 @@ def test_rejects_non_power_of_two():
         hadamard.hadamard_transform(np.zeros((1, 12), np.float32))
     with pytest.raises(ValueError, match="divisible"):
         hadamard.block_hadamard_transform(np.zeros((1, 96), np.float32), 64)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("n", [8, 64, 128, 512])
+def test_stage_rounded_transform_matches_reference_goldens(dt, n):
+    """hadamard_transform on a bf16 / fp16 tensor (rotation.py:14-29 in that dtype): every
+    stage rounded, bitwise equal to the reference's output."""
+    g = load_golden("hadamard_native.npz")
+    rnd = OQ.bf16_round if dt == "bf16" else OQ.fp16_round
+    got = OH.hadamard_transform(g[f"x_{dt}_{n}"], stage_round=rnd)
+    assert np.array_equal(got.view(np.uint32), g[f"h_{dt}_{n}"].view(np.uint32))
+    # and the per-stage rounding matters: one rounding at the end differs somewhere
+    once = rnd(OH.hadamard_transform(g[f"x_{dt}_{n}"]))
+    assert not np.array_equal(once, g[f"h_{dt}_{n}"])
