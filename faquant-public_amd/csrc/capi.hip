@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/faquant_amd.h"
@@ -266,6 +267,41 @@ SplitLayout split_layout(int B, int Hq, int Lq, int Lk, int nsplit) {
   s.part_lm = s.part_o + align256(rows * nsplit * 128 * 4);
   s.total = s.part_lm + align256(rows * nsplit * 2 * 4);
   return s;
+}
+
+}  // namespace
+
+// Scratch of faq_attention_fwd_split_noalloc: the split path's workspace (tile maxima, the
+// running maximum before each key range, partial O and (l, m) per range) for callers that
+// cannot allocate.  Each GPU the library runs on holds its own copy for the life of the
+// process.  Host code must not use this name as a device address: the per-device address
+// comes from hipGetSymbolAddress (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[FAQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per device with that
+// device current; nullptr (and the error message set) on failure.
+void* noalloc_scratch() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(FAQ_ELAUNCH, "faq_attention_fwd_split_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(FAQ_ELAUNCH, "faq_attention_fwd_split_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
 }
 
 }  // namespace
@@ -552,6 +588,36 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(faq::kCombineThreads), 0,
                      st, ca);
   return check_launch("faq_attention_fwd_split");
+}
+
+int faq_attention_fwd_split_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
+                                    int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb,
+                                    int64_t v_sh, int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb,
+                                    int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int causal,
+                                    float scale, int quant_p, int p_levels, int norm_same, float* row_den,
+                                    int nsplit, const faq_attn_opts* opts, faq_stream_t stream) {
+  if (nsplit < 1 || nsplit > faq::kCombineMaxSplits)
+    return fail(FAQ_EINVAL, "faq_attention_fwd_split_noalloc: nsplit must be in [1, %d]", faq::kCombineMaxSplits);
+  if (B < 0 || Hq <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "faq_attention_fwd_split_noalloc: bad sizes");
+  const int64_t need = split_layout(B, Hq, Lq, Lk, nsplit).total;
+  if (need > FAQ_NOALLOC_SCRATCH_BYTES)
+    return fail(FAQ_EINVAL,
+                "faq_attention_fwd_split_noalloc: this call needs %lld bytes of scratch, the static buffer holds %lld "
+                "(use faq_attention_fwd_split with a workspace)",
+                static_cast<long long>(need), static_cast<long long>(FAQ_NOALLOC_SCRATCH_BYTES));
+  if (stream) {
+    // the scratch address belongs to the current device: the stream must run there
+    hipDevice_t sdev = -1;
+    int cur = -1;
+    if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess || hipGetDevice(&cur) != hipSuccess ||
+        sdev != cur)
+      return fail(FAQ_EINVAL, "faq_attention_fwd_split_noalloc: the stream's device must be the current device");
+  }
+  void* ws = noalloc_scratch();
+  if (!ws) return FAQ_ELAUNCH;
+  return faq_attention_fwd_split(q, q_sb, q_sh, q_sl, k, k_sb, k_sh, k_sl, vt, v_sb, v_sh, v_sd, Lpad, o, o_dtype,
+                                 o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p, p_levels, norm_same,
+                                 row_den, nsplit, ws, FAQ_NOALLOC_SCRATCH_BYTES, opts, stream);
 }
 
 int faq_pquant_groups(const float* p, float* p_hat, int64_t groups, int levels, faq_stream_t stream) {

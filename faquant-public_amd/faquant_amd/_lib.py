@@ -86,6 +86,17 @@ _SIGNATURES = {
         ],
         _c_int,
     ),
+    "faq_attention_fwd_split_noalloc": (
+        [
+            _vp, _c_i64, _c_i64, _c_i64,
+            _vp, _c_i64, _c_i64, _c_i64,
+            _vp, _c_i64, _c_i64, _c_i64, _c_int,
+            _vp, _c_int, _c_i64, _c_i64, _c_i64,
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp,
+            _c_int, _opts_p, _vp,
+        ],
+        _c_int,
+    ),
     "faq_attention_mask_bounds": (
         [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _vp],
         _c_int,

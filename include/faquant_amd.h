@@ -41,6 +41,8 @@
  *                         the reference appends one position to its QDQ cache,
  *                         simulated_flash_attention.py:243-289, and runs the tile loop)
  *   faq_attention_split_workspace  workspace size of faq_attention_fwd_split
+ *   faq_attention_fwd_split_noalloc  no counterpart in the reference: faq_attention_fwd_split
+ *                         on a static per-GPU scratch array, for callers that cannot allocate
  *   faq_pquant_groups     the in-register P quantizer of faq_attention_fwd on given values
  *                         (simulated_flash_attention.py:801-806 via hif4.py:143-271)
  *   faq_mfma_probe        no reference counterpart: a measurement helper (the device's
@@ -262,6 +264,25 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
                             int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p,
                             int p_levels, int norm_same, float* row_den, int nsplit, void* workspace,
                             int64_t workspace_bytes, const faq_attn_opts* opts, faq_stream_t stream);
+
+/*
+ * faq_attention_fwd_split without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The workspace is a static device array of
+ * FAQ_NOALLOC_SCRATCH_BYTES per GPU, held for the life of the process; the call allocates
+ * and frees nothing.  Calls whose split layout (faq_attention_split_workspace) exceeds it
+ * return FAQ_EINVAL.  The stream must belong to the current device.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (different streams, or threads)
+ * race; calls on one stream are ordered.  Each call writes every scratch byte it reads, so
+ * nothing carries over from the previous call.
+ */
+#define FAQ_NOALLOC_SCRATCH_BYTES (8ll << 20)
+int faq_attention_fwd_split_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
+                                    int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb,
+                                    int64_t v_sh, int64_t v_sd, int Lpad, void* o, int o_dtype, int64_t o_sb,
+                                    int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int causal,
+                                    float scale, int quant_p, int p_levels, int norm_same, float* row_den,
+                                    int nsplit, const faq_attn_opts* opts, faq_stream_t stream);
 
 /*
  * The attention kernel's in-register P quantizer (the HiF4 QDQ of P along keys,

@@ -40,7 +40,7 @@ def test_header_lists_the_entry_points():
         ["faq_last_error", "faq_version", "faq_hif4_qdq_rows", "faq_hif4_unpack_rows", "faq_hadamard_rows",
          "faq_act_qdq_rows", "faq_operand_prep", "faq_operand_prep_vt", "faq_attention_fwd",
          "faq_attention_fwd_split", "faq_attention_split_workspace", "faq_attention_mask_bounds",
-         "faq_mfma_probe", "faq_pquant_groups", "faq_hadamard_rows_native"]
+         "faq_mfma_probe", "faq_pquant_groups", "faq_hadamard_rows_native", "faq_attention_fwd_split_noalloc"]
     )
 
 
