@@ -1,10 +1,17 @@
-"""Plain HiF4 W4A4 Linear for the Wan2.2 DiT blocks: drop-in for faquant.wan22_hif4.
+"""HiF4 W4A4 Linear of the Wan2.2 DiT blocks on the MI355X: drop-in for faquant.wan22_hif4.
 
-Reference: src/faquant/wan22_hif4.py:35-92.  ``HiF4Linear`` keeps the reference's
-constructor and forward: the weight is quantized once (its HiF4 values are exact in the
-Linear's dtype, which is checked), inputs are quantized as they arrive in row chunks,
-then ``F.linear`` on the HiF4-exact operands.  ``faquant_qdq(levels)`` returns the HIP row
-quantizer; the Wan attention drop-in recognizes it and fuses it into its prologue.
+Reference: src/faquant/wan22_hif4.py:35-92 (``BLOCK_LINEARS``, ``faquant_qdq``,
+``HiF4Linear``).  The constructor keeps the reference's arguments and errors; the compute is
+this build's:
+
+- the weight's HiF4 values are produced once by the quantizer the caller passes (the HIP
+  row quantizer for ``faquant_qdq``) and stored in the Linear's own dtype, refusing a dtype
+  that cannot hold them exactly;
+- a forward call quantizes all its rows in one launch of the HIP row quantizer when
+  ``input_qdq`` is ``faquant_qdq`` (its levels are known), or one call of any other
+  ``input_qdq``; the reference's row chunks only bounded the fp32 temporaries of a torch
+  quantizer, which the kernel does not have (``chunk_elements`` is accepted and unused);
+- the product is ``F.linear`` on the HiF4-exact operands (a library GEMM, hipBLASLt).
 """
 
 from __future__ import annotations
@@ -15,7 +22,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from . import _lib
+from . import _lib, _ops
 from .wan22_attention import faquant_qdq
 
 BLOCK_LINEARS = (
@@ -27,8 +34,16 @@ BLOCK_LINEARS = (
 __all__ = ["BLOCK_LINEARS", "HiF4Linear", "faquant_qdq"]
 
 
+def _hif4_rows(qdq: Callable[[torch.Tensor], torch.Tensor], rows: torch.Tensor) -> torch.Tensor:
+    """QDQ of a [rows, in_features] matrix along its rows: one HIP launch for faquant_qdq."""
+    if isinstance(qdq, faquant_qdq) and rows.dtype in (torch.float32, torch.bfloat16, torch.float16):
+        return _ops.act_qdq_rows(rows.contiguous(), levels=qdq.levels)
+    return qdq(rows)
+
+
 class HiF4Linear(nn.Module):
-    """HiF4 weights (quantized once) and HiF4 inputs (quantized per call), wan22_hif4.py:51-92."""
+    """A Linear whose weight holds HiF4 values and whose inputs are HiF4-quantized per call
+    (wan22_hif4.py:51-92)."""
 
     def __init__(
         self,
@@ -41,34 +56,25 @@ class HiF4Linear(nn.Module):
         weight: torch.Tensor | None = None,
     ) -> None:
         super().__init__()
+        del chunk_elements  # the HIP quantizer needs no row chunks
+        w = linear.weight.detach()
         self.in_features, self.out_features = linear.in_features, linear.out_features
-        source = linear.weight.detach()
-        if weight is None:
-            quantized = weight_qdq(source.to(device=device, dtype=torch.float32))
-        elif weight.shape != source.shape:
-            raise ValueError(f"HiF4 weight of shape {tuple(weight.shape)} for a Linear of {tuple(source.shape)}")
-        else:
-            quantized = weight.to(device=device, dtype=torch.float32)
-        stored = quantized.to(source.dtype)
-        if not torch.equal(stored.float(), quantized):
-            raise RuntimeError(f"HiF4 weight is not exactly representable in {source.dtype}")
-        self.weight = nn.Parameter(stored.to(source.device), requires_grad=False)
+        if weight is not None and weight.shape != w.shape:
+            raise ValueError(f"HiF4 weight of shape {tuple(weight.shape)} for a Linear of {tuple(w.shape)}")
+        values = (_hif4_rows(weight_qdq, w.to(device=device, dtype=torch.float32)) if weight is None
+                  else weight.to(device=device, dtype=torch.float32))
+        held = values.to(w.dtype)
+        if not torch.equal(held.float(), values.float()):
+            raise RuntimeError(f"HiF4 weight is not exactly representable in {w.dtype}")
+        self.weight = nn.Parameter(held.to(w.device), requires_grad=False)
         self.bias = None if linear.bias is None else nn.Parameter(linear.bias.detach().clone(), requires_grad=False)
         self.input_qdq = input_qdq
-        self.chunk_rows = max(1, chunk_elements // self.in_features)
-        # called as collector(module, quantized_rows, first_row_index) for every chunk
+        # collector(module, quantized_rows, first_row_index): sees every call's quantized inputs
         self.collector: Callable[[nn.Module, torch.Tensor, int], None] | None = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         rows = x.reshape(-1, self.in_features)
-        out = None
-        for start in range(0, rows.shape[0], self.chunk_rows):
-            chunk = rows[start:start + self.chunk_rows]
-            part = _lib.forward_only(self.input_qdq(chunk), chunk)
-            if self.collector is not None:
-                self.collector(self, part, start)
-            y = F.linear(part, self.weight, self.bias)
-            if out is None:
-                out = y.new_empty(rows.shape[0], y.shape[-1])
-            out[start:start + part.shape[0]] = y
-        return out.reshape(*x.shape[:-1], self.out_features)
+        qx = _lib.forward_only(_hif4_rows(self.input_qdq, rows), rows)
+        if self.collector is not None:
+            self.collector(self, qx, 0)
+        return F.linear(qx, self.weight, self.bias).reshape(*x.shape[:-1], self.out_features)

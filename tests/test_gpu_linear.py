@@ -119,11 +119,23 @@ def test_hif4_linear_equals_quantize_then_linear(dev):
     mod = HiF4Linear(lin, weight_qdq=qdq, input_qdq=qdq, device=dev, chunk_elements=320 * 64)
     w = fake_quantize_hif4(lin.weight.detach().float(), levels="123").to(torch.bfloat16)
     assert torch.equal(mod.weight, w)
-    x = to_dev(g.standard_normal((150, 320)), dev, torch.float32)
+    np.testing.assert_array_equal(mod.weight.float().cpu().numpy(),
+                                  OQ.fake_quantize_hif4(lin.weight.detach().float().cpu().numpy(), "123"))
+    seen = []
+    mod.collector = lambda m, rows, start: seen.append((rows.clone(), start))
+    x = to_dev(g.standard_normal((3, 50, 320)), dev, torch.float32)
     with torch.autocast("cuda", dtype=torch.bfloat16):
         got = mod(x)
-        rows = [torch.nn.functional.linear(fake_quantize_hif4(x[s:s + 64], levels="123"), mod.weight, mod.bias)
-                for s in range(0, 150, 64)]
-    assert torch.equal(got, torch.cat(rows))
-    with pytest.raises(RuntimeError):
+        want = torch.nn.functional.linear(fake_quantize_hif4(x.reshape(-1, 320), levels="123"), mod.weight, mod.bias)
+    assert got.shape == (3, 50, 128)
+    assert torch.equal(got.reshape(-1, 128), want)
+    # the collector sees every quantized input row once, bit-exact with the oracle's QDQ
+    assert len(seen) == 1 and seen[0][1] == 0
+    np.testing.assert_array_equal(seen[0][0].cpu().numpy(), OQ.fake_quantize_hif4(x.reshape(-1, 320).cpu().numpy(), "123"))
+    # and the product is the fp32 product of the HiF4 operands within bf16 GEMM rounding
+    ref = seen[0][0].double() @ mod.weight.double().T + mod.bias.double()
+    assert float((got.reshape(-1, 128).double() - ref).abs().max() / ref.abs().max()) < 1e-2
+    with pytest.raises(RuntimeError, match="exactly representable"):
         HiF4Linear(lin, weight_qdq=lambda w: w * 1.001, input_qdq=qdq, device=dev)
+    with pytest.raises(ValueError, match="HiF4 weight of shape"):
+        HiF4Linear(lin, weight_qdq=qdq, input_qdq=qdq, device=dev, weight=torch.zeros(3, 3))
