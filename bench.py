@@ -10,7 +10,8 @@ attention kernel alone: the same FLOPs / its mean launch time measured with HIP
 events on the stream it runs on, against the 2.5 PFLOP/s dense bf16 MFMA peak.
 ``cpu_baseline`` times the numpy oracle (the CPU restatement of the reference
 simulator) on a bounded sample of the same workload: the last ``rows`` query rows
-of one KV group (``G`` query heads), scaled by its own algorithmic FLOPs.
+of one KV group (``G`` query heads), split over worker processes, scaled by its own
+algorithmic FLOPs.
 One JSON line is printed on rank 0.
 """
 
@@ -31,15 +32,45 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBPS = 8000.0
 
 # HBM bytes per attention launch, measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and
-# scaled by the same counters on a 256 MiB device copy (bench.py --calibrate-copy):
-# profiles/attn_fwd_qwen8b_32k_counters.md and the traffic tables of the other configs'
-# profiles/attn_fwd_<config>_kernel_trace.md.  None where no counter run was made.
-MEASURED_TRAFFIC_BYTES = {
-    "qwen8b_32k": 1.686e9,
-    "qwen32b_16k": 1.098e9,
-    "wan480p": 3.426e9,
-    "wan720p": 5.638e10,
+# scaled by the same counters on a 256 MiB device copy (bench.py --calibrate-copy), each
+# stamped with the hash of the kernel sources it was measured on (KERNEL_SOURCES).  A
+# figure whose stamp differs from the sources in the tree is stale: it is reported as
+# null, with the stamp, instead of being passed off as this kernel's traffic.
+KERNEL_SOURCES = ("faquant-public_amd/csrc/hif4_attention.hip", "faquant-public_amd/csrc/attn_instances.hip",
+                  "faquant-public_amd/csrc/hif4_device.h")
+MEASURED_TRAFFIC = {
+    # config: (bytes per launch, kernel source sha256 prefix, profile)
+    "qwen8b_32k": (1.686e9, "unmeasured", "profiles/attn_fwd_qwen8b_32k_counters.md"),
+    "qwen32b_16k": (1.098e9, "unmeasured", "profiles/attn_fwd_qwen32b_16k_kernel_trace.md"),
+    "wan480p": (3.426e9, "unmeasured", "profiles/attn_fwd_wan480p_kernel_trace.md"),
+    "wan720p": (5.638e10, "unmeasured", "profiles/attn_fwd_wan720p_kernel_trace.md"),
 }
+
+
+def kernel_source_sha() -> str:
+    """sha256 (first 16 hex digits) of the attention kernel's source files."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(REPO, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def traffic_record(config: str) -> tuple[float | None, dict]:
+    """(traffic bytes or None, provenance) for the roofline of `config`."""
+    current = kernel_source_sha()
+    rec = MEASURED_TRAFFIC.get(config)
+    if rec is None:
+        return None, {"kernel_src_sha256": current, "note": "no counter run for this configuration"}
+    nbytes, stamp, profile = rec
+    prov = {"profile": profile, "measured_on_kernel_src_sha256": stamp, "kernel_src_sha256": current}
+    if stamp != current:
+        prov["note"] = "stale: the kernel sources changed since this traffic was measured"
+        return None, prov
+    return nbytes, prov
+
 
 CONFIGS = {
     # name: B, Hq, Hkv, L, causal, hadamard block, levels, key distribution, per-head scale
@@ -94,45 +125,84 @@ def make_inputs(cfg, dev, seed=0):
     return q, k, v
 
 
-def cpu_baseline(cfg, rows):
-    """Time the numpy oracle on the last `rows` query rows of one KV group."""
+def _cpu_worker_init() -> None:
+    """One BLAS / OpenMP thread per worker process (set before the worker imports numpy)."""
+    for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
+        os.environ[var] = "1"
+
+
+def _cpu_worker(job):
+    """Oracle attention (prologue included) for query rows [i0, i1) of the last `rows`
+    rows of one KV group: those rows with the keys they can see (bottom-right causal)."""
     import numpy as np
 
-    from faquant_amd._ops import attention_flops
+    sys.path.insert(0, REPO)
     from oracle import attention as OA
     from oracle import hadamard as OH
     from oracle import hif4 as OQ
     from oracle import inputs as OI
 
-    G = cfg["Hq"] // cfg["Hkv"]
-    L = cfg["L"]
+    G, L, rows, blk, levels, causal, i0, i1 = job
     g = OI.rng(99)
-    q = OQ.bf16_round(g.standard_normal((1, G, rows, 128), dtype=np.float32))
+    q = OQ.bf16_round(g.standard_normal((1, G, rows, 128), dtype=np.float32))[:, :, i0:i1]
     k = OQ.bf16_round(g.standard_normal((1, 1, L, 128), dtype=np.float32))
     v = OQ.bf16_round(g.standard_normal((1, 1, L, 128), dtype=np.float32))
-    blk = cfg["hadamard"]
-    mconf = OA.SimConfig(pv_normalizer_mode="quantized_same", levels=dict.fromkeys("qkpv", cfg["levels"]),
-                         is_causal=cfg["causal"])
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = 1
+    nk = L - rows + i1 if causal else L  # the last key row i1 - 1 sees
+    k, v = k[:, :, :nk], v[:, :, :nk]
+    mconf = OA.SimConfig(pv_normalizer_mode="quantized_same", levels=dict.fromkeys("qkpv", levels), is_causal=causal)
     t0 = time.perf_counter()
     qr = OH.qk_rotation(q, block_size=blk, out_round=OQ.bf16_round)
     kr = OH.qk_rotation(k, block_size=blk, out_round=OQ.bf16_round)
     OA.simulated_flash_attention(qr, kr, v, mconf, dtype="bfloat16")
-    dt = time.perf_counter() - t0
+    return time.perf_counter() - t0
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, rows, workers):
+    """Time the numpy oracle on the last `rows` query rows of one KV group, split into
+    row chunks over `workers` processes (one BLAS thread each).  Runs before the process
+    touches the GPU, so the workers start from a process with no GPU state."""
+    import multiprocessing as mp
+
+    from faquant_amd._ops import attention_flops
+
+    G, L = cfg["Hq"] // cfg["Hkv"], cfg["L"]
+    # one chunk per worker: every chunk re-quantizes the K/V tiles its rows see, so fewer,
+    # larger chunks waste the least (over the last `rows` of a long sequence the causal
+    # spread of work between chunks is small)
+    n_chunks = workers
+    bounds = [round(i * rows / n_chunks) for i in range(n_chunks + 1)]
+    jobs = [(G, L, rows, cfg["hadamard"], cfg["levels"], cfg["causal"], a, b)
+            for a, b in zip(bounds[:-1], bounds[1:]) if b > a]
+    ctx = mp.get_context("spawn")
+    with ctx.Pool(workers, initializer=_cpu_worker_init) as pool:
+        # imports and page-in, untimed: one single-row job per worker
+        pool.map(_cpu_worker, [j[:6] + (0, 1) for j in jobs[:workers]], chunksize=1)
+        t0 = time.perf_counter()
+        busy = sum(pool.map(_cpu_worker, jobs, chunksize=1))
+        dt = time.perf_counter() - t0
     flops = attention_flops(1, G, rows, L, cfg["causal"])
     return {
         "value": flops / dt / 1e12,
         "unit": "TFLOP/s",
-        "cores": threads,
+        "cores": workers,
+        "host_cpus": os.cpu_count(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"numpy oracle (CPU restatement of the reference simulator) on the last {rows} query rows "
-                   f"x {G} query heads of one KV group over {L} keys, prologue included: "
-                   f"{flops / 1e9:.2f} GFLOP in {dt:.2f} s; BLAS threads {threads}, elementwise numpy single-threaded"),
+                   f"x {G} query heads of one KV group over {L} keys, prologue included, in {len(jobs)} row "
+                   f"chunks over {workers} worker processes with one BLAS thread each: {flops / 1e9:.2f} GFLOP in "
+                   f"{dt:.2f} s wall ({busy:.1f} s of worker time)"),
     }
 
 
@@ -168,7 +238,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="qwen8b_32k", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-rows", type=int, default=4096)  # about 10-15 s of CPU work at 32k
+    ap.add_argument("--cpu-rows", type=int, default=16384)  # about 15 s on 16 cores at 32k
+    # the CPU share of one GPU on the GPU boxes is 16 cores
+    ap.add_argument("--cpu-workers", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE scaling)")
@@ -193,6 +265,7 @@ def main():
         return
 
     cfg = CONFIGS[args.config]
+    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg, args.cpu_rows, args.cpu_workers)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     q, k, v = make_inputs(cfg, dev)
@@ -245,6 +318,7 @@ def main():
                  + 2 * (qh.numel() + kh.numel() + B * Hkv * 128 * lpad))
     pro_gbps = pro_bytes / (pro_ms * 1e-3) / 1e9
 
+    traffic, traffic_prov = traffic_record(args.config)
     result = {
         "metric": "HiF4 QK/PV attn TFLOP/s + % MFMA peak, Qwen3-8B causal prefill 32k, 1 GPU",
         "value": round(value, 3),
@@ -284,7 +358,8 @@ def main():
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": MEASURED_TRAFFIC_BYTES.get(args.config),
+            "traffic": traffic,
+            "traffic_provenance": traffic_prov,
         },
     }
     probe = mfma_probe(dev)
@@ -293,8 +368,8 @@ def main():
         "pct_spec_peak": round(100.0 * probe / MFMA_BF16_PEAK_TFLOPS, 2),
         "kernel_frac_of_probe": round(achieved / probe, 4),
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_rows)
+    if cpu is not None:
+        result["cpu_baseline"] = cpu
     print(json.dumps(result), flush=True)
 
 

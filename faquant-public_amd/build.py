@@ -48,10 +48,11 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile the C ABI and the attention instantiations (one object per masking form,
-    in parallel) and link libfaquant_amd.so."""
+    """Compile the C ABI, the decode kernels and the attention instantiations (one object
+    per masking form), in parallel, and link libfaquant_amd.so."""
     with tempfile.TemporaryDirectory(prefix="faq_build_") as tmp:
-        units = [(os.path.join(CSRC, "capi.hip"), [], os.path.join(tmp, "capi.o"))]
+        units = [(os.path.join(CSRC, "capi.hip"), [], os.path.join(tmp, "capi.o")),
+                 (os.path.join(CSRC, "attn_decode.hip"), [], os.path.join(tmp, "attn_decode.o"))]
         for m in range(ATTN_MASK_FORMS):
             units.append((os.path.join(CSRC, "attn_instances.hip"), [f"-DFAQ_ATTN_MASK={m}"],
                           os.path.join(tmp, f"attn_m{m}.o")))

@@ -1,0 +1,50 @@
+// Decode-shaped HiF4 attention (few query rows per KV head): arguments and launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace faq {
+
+// Waves per decode workgroup; every wave is an independent (item, key split).
+constexpr int kDecWaves = 4;
+
+struct DecodeArgs {
+  const uint16_t* q;  // bf16 [B, Hq, Lq, 128] at element strides, last stride 1
+  int64_t q_sb, q_sh, q_sl;
+  // bf16 operands: K [B, Hkv, Lk, 128] and V^T [B, Hkv, 128, >= 128 ntiles] (zero past Lk)
+  const uint16_t* k;
+  int64_t k_sb, k_sh, k_sl;
+  const uint16_t* vt;
+  int64_t v_sb, v_sh, v_sd;
+  // packed HiF4 operands (one 128-value row per key): 16 code words (dims 8u .. 8u + 7 in
+  // word u, dim 8u + i in nibble i, nibble = 8 + signed code) and 2 meta words (per 64-dim
+  // group: E6M2 byte | level-2 bits << 8 | level-3 bits << 16); strides in key rows
+  const uint32_t* kc;
+  const uint32_t* km;
+  int64_t kp_sb, kp_sh;
+  const uint32_t* vc;
+  const uint32_t* vm;
+  int64_t vp_sb, vp_sh;
+  int B, Hq, Hkv, Lq, Lk;
+  int causal;
+  float c1;       // softmax scale * log2(e)
+  int G;          // query heads per KV head (<= 32)
+  int pb;         // positions per 32-row block: 32 / G
+  int n_rb;       // row blocks per KV head: ceil(Lq / pb)
+  int ntiles;     // ceil(Lk / 128)
+  int tps;        // key tiles per split
+  int nsplit;
+  int rows_total;  // B Hq Lq; row r = (b Hq + hq) Lq + pos
+  float* s;        // scores S (masked keys -inf) [rows_total, s_stride], s_stride >= 128 ntiles
+  int64_t s_stride;
+  float* gmx;      // lane maxima of S per tile: [rows_total, ntiles, 2] (keys 0-63, 64-127)
+  float* smx;      // row maximum of S per split: [rows_total, nsplit]
+  float* part_o;   // unnormalized O per split: [nsplit, rows_total, 128]
+  float* part_lm;  // (l, running maximum) per split: [nsplit, rows_total, 2]
+};
+
+// Scores pass, then the values pass (partials per split; the caller combines them).
+void launch_decode(const DecodeArgs& a, int packed, int quant_p, int p_levels, int norm_same, hipStream_t st);
+
+}  // namespace faq

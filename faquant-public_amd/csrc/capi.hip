@@ -9,6 +9,7 @@
 
 #include "../../include/faquant_amd.h"
 #include "attn_aux.hip"
+#include "attn_decode.h"
 #include "hif4_attention.hip"
 #include "hif4_quant.hip"
 #include "mfma_probe.hip"
@@ -267,6 +268,25 @@ SplitLayout split_layout(int B, int Hq, int Lq, int Lk, int nsplit) {
   s.part_lm = s.part_o + align256(rows * nsplit * 128 * 4);
   s.total = s.part_lm + align256(rows * nsplit * 2 * 4);
   return s;
+}
+
+struct DecodeLayout {
+  int64_t s, gmx, smx, part_o, part_lm, total;  // byte offsets and size
+  int ntiles, tps;
+};
+
+DecodeLayout decode_layout(int B, int Hq, int Lq, int Lk, int nsplit) {
+  DecodeLayout d{};
+  const int64_t rows = static_cast<int64_t>(B) * Hq * Lq;
+  d.ntiles = (Lk + 127) / 128;
+  d.tps = nsplit > 0 ? (d.ntiles + nsplit - 1) / nsplit : 0;
+  d.s = 0;
+  d.gmx = align256(rows * d.ntiles * 128 * 4);
+  d.smx = d.gmx + align256(rows * d.ntiles * 2 * 4);
+  d.part_o = d.smx + align256(rows * nsplit * 4);
+  d.part_lm = d.part_o + align256(rows * nsplit * 128 * 4);
+  d.total = d.part_lm + align256(rows * nsplit * 2 * 4);
+  return d;
 }
 
 }  // namespace
@@ -618,6 +638,155 @@ int faq_attention_fwd_split_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_s
   return faq_attention_fwd_split(q, q_sb, q_sh, q_sl, k, k_sb, k_sh, k_sl, vt, v_sb, v_sh, v_sd, Lpad, o, o_dtype,
                                  o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p, p_levels, norm_same,
                                  row_den, nsplit, ws, FAQ_NOALLOC_SCRATCH_BYTES, opts, stream);
+}
+
+int faq_operand_prep_hif4_kv(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
+                             const float* key_offset, int64_t off_sh, const float* smooth, int64_t smooth_sh,
+                             int smooth_divide, int hadamard, int round_dtype, int levels, uint32_t* codes,
+                             uint32_t* meta, int64_t p_sb, int64_t p_sh, faq_stream_t stream) {
+  if (!x || !codes || !meta) return fail(FAQ_EINVAL, "faq_operand_prep_hif4_kv: null input or output");
+  if (B < 0 || H < 0 || L < 0) return fail(FAQ_EINVAL, "faq_operand_prep_hif4_kv: negative size");
+  if (!valid_dtype(in_dtype) || !valid_dtype(round_dtype)) return fail(FAQ_EINVAL, "faq_operand_prep_hif4_kv: bad dtype");
+  if (hadamard != 0 && hadamard != 64 && hadamard != 128)
+    return fail(FAQ_EUNSUP, "faq_operand_prep_hif4_kv: Hadamard block must be 64 or 128, got %d", hadamard);
+  if (!valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
+  if (!aligned16(x)) return fail(FAQ_EINVAL, "faq_operand_prep_hif4_kv: x must be 16-byte aligned");
+  if (!aligned16(codes) || (reinterpret_cast<uintptr_t>(meta) & 7u))
+    return fail(FAQ_EINVAL, "faq_operand_prep_hif4_kv: codes must be 16-byte and meta 8-byte aligned");
+  const int esz = in_dtype == FAQ_F32 ? 4 : 2;
+  if ((sb * esz) % 16 || (sh * esz) % 16 || (sl * esz) % 16)
+    return fail(FAQ_EINVAL, "faq_operand_prep_hif4_kv: strides must keep 16-byte alignment");
+  if (p_sb < 0 || p_sh < 0) return fail(FAQ_EINVAL, "faq_operand_prep_hif4_kv: negative row strides");
+  const int64_t rows = static_cast<int64_t>(B) * H * L;
+  if (rows == 0) return FAQ_OK;
+  if (B > 65535 || H > 65535) return fail(FAQ_EUNSUP, "faq_operand_prep_hif4_kv: at most 65535 batches and heads");
+  faq::OperandPrepArgs a{};
+  a.x = x;
+  a.sb = sb;
+  a.sh = sh;
+  a.sl = sl;
+  a.B = B;
+  a.H = H;
+  a.L = L;
+  a.key_offset = key_offset;
+  a.off_sh = off_sh;
+  a.smooth = smooth;
+  a.smooth_sh = smooth_sh;
+  a.smooth_divide = smooth_divide;
+  a.hadamard = hadamard;
+  a.div = sqrt_div(hadamard);
+  a.quant = 1;
+  a.pk_codes = codes;
+  a.pk_meta = meta;
+  a.pk_sb = p_sb;
+  a.pk_sh = p_sh;
+  const int64_t threads = rows * 16;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (in_dtype == FAQ_F32) launch_prep_in<float>(a, round_dtype, levels, threads, st);
+  else if (in_dtype == FAQ_BF16) launch_prep_in<__hip_bfloat16>(a, round_dtype, levels, threads, st);
+  else launch_prep_in<__half>(a, round_dtype, levels, threads, st);
+  return check_launch("faq_operand_prep_hif4_kv");
+}
+
+int64_t faq_attention_decode_workspace(int B, int Hq, int Lq, int Lk, int nsplit) {
+  if (B < 0 || Hq < 0 || Lq < 0 || Lk < 0 || nsplit < 1) return -1;
+  return decode_layout(B, Hq, Lq, Lk, nsplit).total;
+}
+
+int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
+                         int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
+                         int64_t v_sd, const faq_hif4_kv* kp, const faq_hif4_kv* vp, void* o, int o_dtype,
+                         int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int causal,
+                         float scale, int quant_p, int p_levels, int norm_same, float* row_den, int nsplit,
+                         void* workspace, int64_t workspace_bytes, faq_stream_t stream) {
+  const char* who = "faq_attention_decode";
+  const bool packed = kp != nullptr;
+  if ((kp == nullptr) != (vp == nullptr)) return fail(FAQ_EINVAL, "%s: K and V are both packed or both bf16", who);
+  if (!q || !o) return fail(FAQ_EINVAL, "%s: null operand", who);
+  if (packed ? !(kp->codes && kp->meta && vp->codes && vp->meta) : !(k && vt))
+    return fail(FAQ_EINVAL, "%s: null operand", who);
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "%s: bad sizes", who);
+  if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
+  if (Hq / Hkv > 32) return fail(FAQ_EUNSUP, "%s: at most 32 query heads per key/value head", who);
+  if (nsplit < 1 || nsplit > faq::kCombineMaxSplits)
+    return fail(FAQ_EINVAL, "%s: nsplit must be in [1, %d]", who, faq::kCombineMaxSplits);
+  if (o_dtype != FAQ_F32 && o_dtype != FAQ_BF16) return fail(FAQ_EUNSUP, "%s: output must be fp32 or bf16", who);
+  if (quant_p && !valid_levels(p_levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", p_levels);
+  if (!aligned16(q) || !aligned16(o)) return fail(FAQ_EINVAL, "%s: pointers must be 16-byte aligned", who);
+  if ((q_sb | q_sh | q_sl) & 7) return fail(FAQ_EINVAL, "%s: operand strides must be multiples of 8 elements", who);
+  if ((o_sb | o_sh | o_sl) & 3) return fail(FAQ_EINVAL, "%s: output strides must be multiples of 4 elements", who);
+  const DecodeLayout L = decode_layout(B, Hq, Lq, Lk, nsplit);
+  if (packed) {
+    if (!aligned16(kp->codes) || !aligned16(vp->codes) || (reinterpret_cast<uintptr_t>(kp->meta) & 7u) ||
+        (reinterpret_cast<uintptr_t>(vp->meta) & 7u))
+      return fail(FAQ_EINVAL, "%s: packed codes must be 16-byte and meta 8-byte aligned", who);
+    if (kp->sb < 0 || kp->sh < 0 || vp->sb < 0 || vp->sh < 0) return fail(FAQ_EINVAL, "%s: negative row strides", who);
+  } else {
+    if (!aligned16(k) || !aligned16(vt)) return fail(FAQ_EINVAL, "%s: pointers must be 16-byte aligned", who);
+    if ((k_sb | k_sh | k_sl | v_sb | v_sh | v_sd) & 7)
+      return fail(FAQ_EINVAL, "%s: operand strides must be multiples of 8 elements", who);
+    if (v_sd < static_cast<int64_t>(L.ntiles) * 128) return fail(FAQ_EINVAL, "%s: v_sd must be >= 128 * ceil(Lk / 128)", who);
+  }
+  if (B == 0 || Lq == 0) return FAQ_OK;
+  if (!workspace || !aligned16(workspace)) return fail(FAQ_EINVAL, "%s: null or misaligned workspace", who);
+  if (workspace_bytes < L.total)
+    return fail(FAQ_EINVAL, "%s: workspace of %lld bytes, need %lld", who, static_cast<long long>(workspace_bytes),
+                static_cast<long long>(L.total));
+  const int G = Hq / Hkv;
+  faq::DecodeArgs a{};
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_sl = q_sl;
+  if (packed) {
+    a.kc = kp->codes;
+    a.km = kp->meta;
+    a.kp_sb = kp->sb;
+    a.kp_sh = kp->sh;
+    a.vc = vp->codes;
+    a.vm = vp->meta;
+    a.vp_sb = vp->sb;
+    a.vp_sh = vp->sh;
+  } else {
+    a.k = k;
+    a.k_sb = k_sb;
+    a.k_sh = k_sh;
+    a.k_sl = k_sl;
+    a.vt = vt;
+    a.v_sb = v_sb;
+    a.v_sh = v_sh;
+    a.v_sd = v_sd;
+  }
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.Lq = Lq;
+  a.Lk = Lk;
+  a.causal = causal != 0;
+  a.c1 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  a.G = G;
+  a.pb = 32 / G;
+  a.n_rb = (Lq + a.pb - 1) / a.pb;
+  a.ntiles = L.ntiles;
+  a.tps = L.tps;
+  a.nsplit = nsplit;
+  a.rows_total = B * Hq * Lq;
+  char* ws = static_cast<char*>(workspace);
+  a.s = reinterpret_cast<float*>(ws + L.s);
+  a.s_stride = static_cast<int64_t>(L.ntiles) * 128;
+  a.gmx = reinterpret_cast<float*>(ws + L.gmx);
+  a.smx = reinterpret_cast<float*>(ws + L.smx);
+  a.part_o = reinterpret_cast<float*>(ws + L.part_o);
+  a.part_lm = reinterpret_cast<float*>(ws + L.part_lm);
+  const int64_t waves = static_cast<int64_t>(B) * Hkv * a.n_rb * nsplit;
+  if (waves > static_cast<int64_t>(INT32_MAX) - faq::kDecWaves) return fail(FAQ_EUNSUP, "%s: too many work items", who);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  faq::launch_decode(a, packed ? 1 : 0, quant_p, p_levels, norm_same, st);
+  faq::SplitCombineArgs ca{a.part_o, a.part_lm, a.rows_total, nsplit, Hq, Lq, o, o_sb, o_sh, o_sl,
+                           o_dtype == FAQ_F32, row_den};
+  hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(faq::kCombineThreads), 0,
+                     st, ca);
+  return check_launch(who);
 }
 
 int faq_pquant_groups(const float* p, float* p_hat, int64_t groups, int levels, faq_stream_t stream) {

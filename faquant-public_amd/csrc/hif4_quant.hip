@@ -527,7 +527,46 @@ struct OperandPrepArgs {
   void* y;                       // bf16 output [B, H, L, 128] with strides below
   int64_t yb, yh, yl;
   int quant;                     // 1: HiF4 QDQ after the cast
+  // optional packed HiF4 rows (decode K/V caches; needs quant): per row 16 code words (dims
+  // 8u .. 8u + 7 in word (u & 1) 8 + u / 2) and 2 meta words at row index
+  // b pk_sb + h pk_sh + position; y may then be null
+  uint32_t* pk_codes;
+  uint32_t* pk_meta;
+  int64_t pk_sb, pk_sh;
 };
+
+// Packed HiF4 form of the 8 values a lane quantized with qdq8 (a 64-value group spans the 8
+// lanes part8 = 0..7, dims 8 part8 .. + 7 of the group): the code word (nibble i = 8 + the
+// signed code of value i, so a value is (nibble - 8) 2^k s / 4) and the group's meta word
+// (E6M2 byte ((e + 48) << 2) | m, level-2 bits << 8, level-3 bits << 16, the content of
+// hif4.py:67-79), the same on all 8 lanes.  A group that became NaN gets E6M2 byte 0xFF
+// (no real scale has it: the largest is 49152 = 2^15 1.5, byte 0xFE).
+template <int LV>
+__device__ __forceinline__ void pack_hif4_word(const float* y, uint32_t sm_codes, float s, int ka, int kb,
+                                               int part8, uint32_t& word, uint32_t& meta) {
+  word = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t nib = (sm_codes >> (4 * i)) & 0xFu;  // bit 3 sign, bits 0-2 code
+    const uint32_t mag = nib & 7u;
+    word |= ((nib & 8u) ? 8u - mag : 8u + mag) << (4 * i);
+  }
+  // k = lv2 + lv3 per 4-group (as in qdq_rows_kernel)
+  const int e2 = LV == 123 ? (ka == 2 || kb == 2) : (LV == 12 ? ka : 0);
+  uint32_t b2 = static_cast<uint32_t>(e2) << part8;
+  uint32_t b3 = (static_cast<uint32_t>(ka - e2) | (static_cast<uint32_t>(kb - e2) << 1)) << (2 * part8);
+  b2 |= static_cast<uint32_t>(lane_xor<1>(static_cast<int>(b2)));
+  b2 |= static_cast<uint32_t>(lane_xor<2>(static_cast<int>(b2)));
+  b2 |= static_cast<uint32_t>(lane_xor<4>(static_cast<int>(b2)));
+  b3 |= static_cast<uint32_t>(lane_xor<1>(static_cast<int>(b3)));
+  b3 |= static_cast<uint32_t>(lane_xor<2>(static_cast<int>(b3)));
+  b3 |= static_cast<uint32_t>(lane_xor<4>(static_cast<int>(b3)));
+  const uint32_t sbits = __float_as_uint(s);
+  const int e = static_cast<int>(sbits >> 23) - 127;
+  uint32_t sb = (static_cast<uint32_t>(e + 48) << 2) | ((sbits >> 21) & 3u);
+  if (y[0] != y[0]) sb = 0xFFu;
+  meta = sb | (b2 << 8) | (b3 << 16);
+}
 
 // One lane owns 8 of a row's 128 values; a row spans 16 lanes, and each lane takes
 // kPrepRows rows 16 positions apart (a block covers 16 kPrepRows consecutive positions): the
@@ -586,8 +625,21 @@ __global__ __launch_bounds__(256) void operand_prep_kernel(OperandPrepArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) w[i] = Io<Tround>::round(w[i]);
     if (a.rotated && live) Io<Tround>::store8(static_cast<Tround*>(a.rotated) + r * 128 + d0, w);
-    if (a.quant) qdq8<LV>(w);
-    if (live) {
+    if (a.pk_codes) {
+      float s;
+      int ka, kb;
+      uint32_t sm = 0, word, meta;
+      qdq8<LV>(w, &s, nullptr, &ka, &kb, &sm);
+      pack_hif4_word<LV>(w, sm, s, ka, kb, part & 7, word, meta);
+      if (live) {
+        const int64_t pr = b * a.pk_sb + h * a.pk_sh + l;
+        a.pk_codes[pr * 16 + (part & 1) * 8 + (part >> 1)] = word;  // dims 8 part .. + 7
+        if ((part & 7) == 0) a.pk_meta[pr * 2 + (part >> 3)] = meta;
+      }
+    } else if (a.quant) {
+      qdq8<LV>(w);
+    }
+    if (live && a.y) {
       Io<__hip_bfloat16>::store8(
           reinterpret_cast<__hip_bfloat16*>(static_cast<uint16_t*>(a.y) + b * a.yb + h * a.yh + static_cast<int64_t>(l) * a.yl + d0), w);
     }

@@ -50,6 +50,15 @@ class AttnOpts(ctypes.Structure):
 
 _opts_p = ctypes.POINTER(AttnOpts)
 
+
+class HiF4KV(ctypes.Structure):
+    """``faq_hif4_kv``: a packed HiF4 K or V cache (code and meta words, row strides)."""
+
+    _fields_ = [("codes", _vp), ("meta", _vp), ("sb", _c_i64), ("sh", _c_i64)]
+
+
+_kv_p = ctypes.POINTER(HiF4KV)
+
 _SIGNATURES = {
     "faq_last_error": ([], ctypes.c_char_p),
     "faq_version": ([], ctypes.c_char_p),
@@ -70,6 +79,26 @@ _SIGNATURES = {
     ),
     "faq_operand_prep_vt": (
         [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_int, _vp],
+        _c_int,
+    ),
+    "faq_operand_prep_hif4_kv": (
+        [
+            _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+            _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_i64, _c_i64, _vp,
+        ],
+        _c_int,
+    ),
+    "faq_attention_decode_workspace": ([_c_int, _c_int, _c_int, _c_int, _c_int], _c_i64),
+    "faq_attention_decode": (
+        [
+            _vp, _c_i64, _c_i64, _c_i64,
+            _vp, _c_i64, _c_i64, _c_i64,
+            _vp, _c_i64, _c_i64, _c_i64,
+            _kv_p, _kv_p,
+            _vp, _c_int, _c_i64, _c_i64, _c_i64,
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp,
+            _c_int, _vp, _c_i64, _vp,
+        ],
         _c_int,
     ),
     "faq_attention_split_workspace": ([_c_int, _c_int, _c_int, _c_int, _c_int], _c_i64),

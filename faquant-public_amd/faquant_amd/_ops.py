@@ -229,6 +229,105 @@ def operand_prep(
     return y, rot
 
 
+class PackedHiF4KV:
+    """A packed HiF4 K or V cache (faq_hif4_kv): one row of 128 values per (batch, head,
+    position) at 4.5 bits per value, ``codes`` int32 [B, H, capacity, 16] and ``meta`` int32
+    [B, H, capacity, 2]; rows 0..length-1 are valid.  Written by ``pack_operand``, read by
+    ``attention_decode``; it decodes to the bf16 HiF4 QDQ values of the same prologue."""
+
+    def __init__(self, batch: int, heads: int, capacity: int, device, levels: str) -> None:
+        self.codes = torch.empty((batch, heads, capacity, 16), device=device, dtype=torch.int32)
+        self.meta = torch.empty((batch, heads, capacity, 2), device=device, dtype=torch.int32)
+        self.length = 0
+        self.levels = levels
+
+    @property
+    def shape(self) -> tuple:
+        """Logical shape [B, H, length, 128] of the values held."""
+        return (self.codes.shape[0], self.codes.shape[1], self.length, HEAD_DIM)
+
+    @property
+    def capacity(self) -> int:
+        return self.codes.shape[2]
+
+    @property
+    def device(self) -> torch.device:
+        return self.codes.device
+
+    def nbytes(self) -> int:
+        """Bytes of the valid rows (72 per row: 4.5 bits per value)."""
+        return self.codes.shape[0] * self.codes.shape[1] * self.length * 72
+
+    def grow(self, capacity: int) -> "PackedHiF4KV":
+        """A copy with room for `capacity` rows (the valid rows copied)."""
+        B, H = self.codes.shape[:2]
+        g = PackedHiF4KV(B, H, capacity, self.device, self.levels)
+        g.codes[:, :, : self.length].copy_(self.codes[:, :, : self.length])
+        g.meta[:, :, : self.length].copy_(self.meta[:, :, : self.length])
+        g.length = self.length
+        return g
+
+    def descriptor(self) -> "_lib.HiF4KV":
+        if self.codes.stride(3) != 1 or self.codes.stride(2) != 16 or self.meta.stride(2) != 2:
+            raise ValueError("packed HiF4 rows must be contiguous")
+        rows_b, rows_h = self.codes.stride(0) // 16, self.codes.stride(1) // 16
+        if (self.meta.stride(0) // 2, self.meta.stride(1) // 2) != (rows_b, rows_h):
+            raise ValueError("packed HiF4 codes and meta must share row strides")
+        return _lib.HiF4KV(self.codes.data_ptr(), self.meta.data_ptr(), rows_b, rows_h)
+
+
+def pack_operand(
+    x: torch.Tensor,
+    *,
+    levels: str,
+    out: PackedHiF4KV,
+    start: int = 0,
+    hadamard: int = 0,
+    key_offset: torch.Tensor | None = None,
+    smooth: torch.Tensor | None = None,
+    smooth_divide: bool = False,
+    round_dtype: torch.dtype | None = None,
+) -> PackedHiF4KV:
+    """The operand prologue of ``operand_prep`` on x [B, H, L, 128] with the HiF4 QDQ
+    written packed into rows start .. start + L - 1 of ``out`` (faq_operand_prep_hif4_kv)."""
+    _lib.require_device(x, key_offset, smooth)
+    lib = _lib.load()
+    if x.ndim != 4 or x.shape[-1] != HEAD_DIM:
+        raise NotImplementedError("the HIP operand prologue supports [B, H, L, 128] tensors")
+    B, H, L, _ = x.shape
+    if tuple(out.codes.shape[:2]) != (B, H) or start < 0 or start + L > out.capacity:
+        raise ValueError(f"rows {start}..{start + L} of a packed cache of shape {tuple(out.codes.shape[:3])}")
+    if not levels:
+        raise ValueError("the packed HiF4 form needs HiF4 levels")
+    sb, sh, sl = _bhld_strides(x)
+    rdt = round_dtype or x.dtype
+    off, off_sh = _per_head(key_offset, H, x.device)
+    sm, sm_sh = _per_head(smooth, H, x.device)
+    d = out.descriptor()
+    _lib.check(
+        lib.faq_operand_prep_hif4_kv(
+            x.data_ptr(), _lib.dtype_code(x.dtype), sb, sh, sl, B, H, L,
+            _lib.ptr(off), off_sh, _lib.ptr(sm), sm_sh, int(bool(smooth_divide)), int(hadamard),
+            _lib.dtype_code(rdt), int(levels), d.codes + start * 64, d.meta + start * 8, d.sb, d.sh,
+            _lib.stream_ptr(x.device),
+        )
+    )
+    out.length = max(out.length, start + L)
+    return out
+
+
+def _per_head(t, H: int, device):
+    """A per-dim fp32 tensor of 128 or H*128 values as (tensor, head stride)."""
+    if t is None:
+        return None, 0
+    t = t.to(device=device, dtype=torch.float32).contiguous()
+    if t.numel() == HEAD_DIM:
+        return t.reshape(HEAD_DIM), 0
+    if t.numel() == H * HEAD_DIM:
+        return t.reshape(H, HEAD_DIM), HEAD_DIM
+    raise ValueError(f"per-dim tensor must hold 128 or H*128 values, got shape {tuple(t.shape)}")
+
+
 def operand_prep_vt(v: torch.Tensor, *, levels: str | None) -> torch.Tensor:
     """V [B, H, L, 128] -> HiF4-QDQ'd, transposed bf16 [B, H, 128, Lpad] (zero padded)."""
     _lib.require_device(v)
@@ -444,6 +543,10 @@ def attention_fwd(
     if out.stride(3) != 1:
         raise ValueError("attention output needs a unit stride along head_dim")
     nsplit = _split_count(B, Hq, Hkv, Lq, int(key_length), _device_cus(q.device)) if split is None else int(split)
+    if split is None and nsplit > 1 and not out_levels and opts is None and decode_shaped(Hq, Hkv, Lq):
+        # decode: the query heads of a KV head together, K read once
+        return attention_decode(q, key_length, causal=causal, scale=scale, quant_p=quant_p, p_levels=p_levels,
+                                norm_same=norm_same, out=out, k=k, vt=vt, row_den=row_den)
     if nsplit > 1 and not out_levels:
         ws_bytes = lib.faq_attention_split_workspace(B, Hq, Lq, int(key_length), nsplit)
         ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
@@ -464,6 +567,81 @@ def attention_fwd(
             B, Hq, Hkv, Lq, int(key_length), int(bool(causal)), float(scale),
             int(bool(quant_p)), int(p_levels), int(bool(norm_same)), _lib.ptr(row_den),
             int(out_levels) if out_levels else 0, opts, _lib.stream_ptr(q.device),
+        )
+    )
+    return out
+
+
+def decode_shaped(Hq: int, Hkv: int, Lq: int) -> bool:
+    """Whether faq_attention_decode takes a call: all query rows of a KV head (G heads x Lq
+    positions) fit one wave's 32 MFMA columns, so every K/V tile is read once."""
+    G = Hq // Hkv
+    return G <= 32 and Lq * G <= 32
+
+
+def decode_split_count(B: int, Hkv: int, Lk: int, cus: int = 256) -> int:
+    """Key ranges of faq_attention_decode: about eight waves per CU (two per SIMD) over all
+    (batch, KV head, range) work, at least one key tile per range, no empty range."""
+    ntiles = -(-Lk // KEY_TILE)
+    if ntiles == 0:
+        return 1
+    want = max(1, min(ntiles, 4096, -(-8 * cus // max(1, B * Hkv))))
+    tps = -(-ntiles // want)
+    return -(-ntiles // tps)
+
+
+def attention_decode(
+    q: torch.Tensor,
+    key_length: int,
+    *,
+    causal: bool,
+    scale: float,
+    quant_p: bool,
+    p_levels: str,
+    norm_same: bool,
+    out: torch.Tensor,
+    k: torch.Tensor | None = None,
+    vt: torch.Tensor | None = None,
+    packed: tuple[PackedHiF4KV, PackedHiF4KV] | None = None,
+    row_den: torch.Tensor | None = None,
+    split: int | None = None,
+) -> torch.Tensor:
+    """Decode-shaped attention (faq_attention_decode): q [B, Hq, Lq, 128] bf16 against bf16
+    k [B, Hkv, Lk, 128] and vt [B, Hkv, 128, Lpad], or against ``packed`` = (K cache, V cache)
+    of PackedHiF4KV; masks none or bottom-right causal.  Same results as attention_fwd's
+    split path with the same ``split``, bitwise, for either form of K/V."""
+    tensors = (q, out, row_den) + ((k, vt) if packed is None else (packed[0].codes, packed[1].codes))
+    _lib.require_device(*tensors)
+    lib = _lib.load()
+    B, Hq, Lq, D = q.shape
+    if D != HEAD_DIM or q.dtype != torch.bfloat16:
+        raise NotImplementedError("the decode kernel takes bf16 queries with head_dim 128")
+    if out.dtype not in (torch.float32, torch.bfloat16) or out.stride(3) != 1:
+        raise ValueError("attention output must be fp32 or bf16 with a unit stride along head_dim")
+    Lk = int(key_length)
+    if packed is None:
+        if k is None or vt is None or k.dtype != torch.bfloat16 or vt.dtype != torch.bfloat16:
+            raise TypeError("bf16 k and vt are required without packed K/V")
+        Hkv = k.shape[1]
+        kargs = (k.data_ptr(), *_bhld_strides(k), vt.data_ptr(), *_bhld_strides(vt))
+        kp = vp = None
+    else:
+        kc, vc = packed
+        Hkv = kc.codes.shape[1]
+        if kc.length < Lk or vc.length < Lk or vc.codes.shape[1] != Hkv:
+            raise ValueError("the packed K/V caches must hold key_length rows of the same heads")
+        kargs = (0, 0, 0, 0, 0, 0, 0, 0)
+        kp, vp = kc.descriptor(), vc.descriptor()
+    nsplit = decode_split_count(B, Hkv, Lk, _device_cus(q.device)) if split is None else int(split)
+    ws_bytes = lib.faq_attention_decode_workspace(B, Hq, Lq, Lk, nsplit)
+    ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
+    _lib.check(
+        lib.faq_attention_decode(
+            q.data_ptr(), *_bhld_strides(q), *kargs,
+            None if kp is None else ctypes.byref(kp), None if vp is None else ctypes.byref(vp),
+            out.data_ptr(), _lib.dtype_code(out.dtype), out.stride(0), out.stride(1), out.stride(2),
+            B, Hq, Hkv, Lq, Lk, int(bool(causal)), float(scale), int(bool(quant_p)), int(p_levels),
+            int(bool(norm_same)), _lib.ptr(row_den), nsplit, ws.data_ptr(), ws.numel(), _lib.stream_ptr(q.device),
         )
     )
     return out

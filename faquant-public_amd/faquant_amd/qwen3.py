@@ -27,10 +27,9 @@ from .hif4 import _resolve as resolve_hif4_levels
 from .quantization import check_hif4_arguments, fake_quantize
 from .simulated_flash_attention import (
     _hif4_group,
-    _key_operand,
-    _value_operand,
     count_tiles,
     key_ranges,
+    kv_operands_and_attend,
     simulated_flash_attention_forward,
 )
 
@@ -171,20 +170,20 @@ def attention_core(
     q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None, hadamard=block,
                                 smooth=smooth_scale, round_dtype=torch.bfloat16)
     B, Hq, Lq, D = query.shape
-    # K and V through the decode QDQ cache of the module (sfa:243-289), K with the same
-    # post-RoPE prologue as Q
-    k_op = _key_operand(module, key, enabled=qk_quant, query_length=Lq, levels=levels["k"], hadamard=block,
-                        key_offset=key_offset, smooth=smooth_scale, smooth_divide=True, round_dtype=torch.bfloat16)
-    vt = _value_operand(module, value, enabled=pv_quant, query_length=Lq, levels=levels["v"])
     Lk = key.shape[2]
     scale = float(scaling if scaling is not None else D**-0.5)
     causal = bool(getattr(module, "is_causal", True))
     out = torch.empty((B, Lq, Hq, D), device=query.device, dtype=query.dtype)
     ranges, masked = key_ranges(module, attention_mask, batch=B, query_length=Lq, key_length=Lk, causal=causal,
                                 sliding_window=sliding_window, device=query.device)
-    _ops.attention_fwd(q_op, k_op, vt, Lk, causal=causal, scale=scale, quant_p=pv_quant,
-                       p_levels=levels["p"], norm_same=mode == "quantized_same", out=out.transpose(1, 2),
-                       out_levels=_output_quant_levels(module), ranges=ranges)
+    # K and V through the decode QDQ cache of the module (sfa:243-289), K with the same
+    # post-RoPE prologue as Q
+    k_prep = dict(hadamard=block, key_offset=key_offset, smooth=smooth_scale, smooth_divide=True,
+                  round_dtype=torch.bfloat16)
+    kv_operands_and_attend(module, q_op, key, value, query_length=Lq, qk_quant=qk_quant, pv_quant=pv_quant,
+                           levels=levels, k_prep=k_prep, causal=causal, scale=scale, quant_p=pv_quant,
+                           p_levels=levels["p"], norm_same=mode == "quantized_same", out=out.transpose(1, 2),
+                           out_levels=_output_quant_levels(module), ranges=ranges)
     count_tiles(
         module.faquant_simulated_attention_stats, batch=B, query_heads=Hq, query_length=Lq, key_length=Lk,
         head_dim=D, query_chunk=int(module.faquant_attention_query_chunk_size), key_chunk=_ops.KEY_TILE,

@@ -322,6 +322,70 @@ def _value_operand(module, value: torch.Tensor, *, enabled: bool, query_length: 
     return vt
 
 
+def _packed_cache_enabled(module, qk_quant: bool, pv_quant: bool) -> bool:
+    """Packed HiF4 decode caches: the module attribute ``faquant_kv_cache_packed`` (an
+    extension of this build), with K and V quantization both on."""
+    return bool(getattr(module, "faquant_kv_cache_packed", False)) and qk_quant and pv_quant
+
+
+def _packed_operands(module, key: torch.Tensor, value: torch.Tensor, *, query_length: int, levels, prep: dict):
+    """The decode K/V caches of sfa:243-289 held packed (4.5 bits per value, PackedHiF4KV):
+    ``faquant_k_matmul_qdq_cache`` / ``faquant_v_matmul_qdq_cache`` are PackedHiF4KV objects
+    whose rows decode to the bf16 QDQ values of the unpacked caches.  A decode step packs
+    only the appended position (the same append condition); anything else packs the whole
+    tensor.  K takes the operand prologue ``prep`` (Hadamard, Smooth-QK, key offset)."""
+    states = getattr(module, _KV_STATE, None) or {}
+    states.pop("k", None)  # no bf16 caches beside the packed ones
+    states.pop("v", None)
+    caches = []
+    for name, t, lv, pre in (("k", key, levels["k"], prep), ("v", value, levels["v"], {})):
+        attr = f"faquant_{name}_matmul_qdq_cache"
+        st = states.get("packed_" + name)
+        B, H, L, _ = t.shape
+        if _append_allowed(module, attr, st, t, query_length):
+            cache = st["buf"]
+            if L > cache.capacity:
+                cache = cache.grow(_cache_capacity(L + _KV_GROWTH))
+            _ops.pack_operand(t[:, :, L - 1 :], levels=lv, out=cache, start=L - 1, **pre)
+        else:
+            cache = _ops.PackedHiF4KV(B, H, _cache_capacity(L), t.device, lv)
+            _ops.pack_operand(t, levels=lv, out=cache, **pre)
+        cache.length = L
+        states["packed_" + name] = dict(buf=cache, view=cache, length=L, device=t.device, dtype=t.dtype, lead=(B, H))
+        setattr(module, attr, cache)
+        caches.append(cache)
+    setattr(module, _KV_STATE, states)
+    return caches
+
+
+def kv_operands_and_attend(module, q_op: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, query_length: int,
+                           qk_quant: bool, pv_quant: bool, levels, k_prep: dict, **attn) -> torch.Tensor:
+    """K/V operands through the module's decode caches (sfa:243-289), then the attention
+    kernel (``attn``: the keyword arguments of _ops.attention_fwd).  With packed caches the
+    calls that attention_fwd runs on the decode kernel (decode-shaped, no mask beyond the
+    causal rule) run on the packed rows; any other call takes bf16 operands of the same
+    values, so both cache forms give the same bits."""
+    key_length = key.shape[2]
+    if _packed_cache_enabled(module, qk_quant, pv_quant):
+        kp, vp = _packed_operands(module, key, value, query_length=query_length, levels=levels, prep=k_prep)
+        plain = not (attn.get("ranges") is not None or attn.get("softcap") or attn.get("pv_probe") is not None
+                     or attn.get("dense_mask") is not None or attn.get("out_levels"))
+        B, Hq, Hkv = q_op.shape[0], q_op.shape[1], key.shape[1]
+        # the calls attention_fwd would send to the decode kernel (so both cache forms agree)
+        if (plain and _ops.decode_shaped(Hq, Hkv, query_length)
+                and _ops._split_count(B, Hq, Hkv, query_length, key_length, _ops._device_cus(q_op.device)) > 1):
+            return _ops.attention_decode(
+                q_op, key_length, packed=(kp, vp), causal=attn["causal"], scale=attn["scale"],
+                quant_p=attn["quant_p"], p_levels=attn["p_levels"], norm_same=attn["norm_same"], out=attn["out"],
+                row_den=attn.get("row_den"))
+        k_op, _ = _ops.operand_prep(key, levels=levels["k"], **k_prep)
+        vt = _ops.operand_prep_vt(value, levels=levels["v"])
+    else:
+        k_op = _key_operand(module, key, enabled=qk_quant, query_length=query_length, levels=levels["k"], **k_prep)
+        vt = _value_operand(module, value, enabled=pv_quant, query_length=query_length, levels=levels["v"])
+    return _ops.attention_fwd(q_op, k_op, vt, key_length, **attn)
+
+
 def simulated_flash_attention_forward(
     module: torch.nn.Module,
     query: torch.Tensor,
@@ -417,8 +481,6 @@ def simulated_flash_attention_forward(
 
     levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
     q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None)
-    k_op = _key_operand(module, key, enabled=qk_quant, query_length=query_length, levels=levels["k"])
-    vt = _value_operand(module, value, enabled=pv_quant, query_length=query_length, levels=levels["v"])
 
     dense = None
     if attention_mask is not None and attention_mask.ndim in (3, 4):
@@ -432,9 +494,9 @@ def simulated_flash_attention_forward(
     output = torch.empty((batch, query_length, query_heads, head_dim), device=query.device, dtype=query.dtype)
     probe = (torch.empty((batch, query_heads, query_length, 5), device=query.device, dtype=torch.float32)
              if collect else None)
-    _ops.attention_fwd(
-        q_op, k_op, vt, key_length,
-        causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
+    kv_operands_and_attend(
+        module, q_op, key, value, query_length=query_length, qk_quant=qk_quant, pv_quant=pv_quant, levels=levels,
+        k_prep={}, causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
         norm_same=mode == "quantized_same", out=output.transpose(1, 2), ranges=ranges, softcap=softcap,
         pv_probe=probe, dense_mask=dense,
     )

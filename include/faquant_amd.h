@@ -43,6 +43,15 @@
  *   faq_attention_split_workspace  workspace size of faq_attention_fwd_split
  *   faq_attention_fwd_split_noalloc  no counterpart in the reference: faq_attention_fwd_split
  *                         on a static per-GPU scratch array, for callers that cannot allocate
+ *   faq_operand_prep_hif4_kv  faq_operand_prep writing the packed 4.5-bit HiF4 form (the
+ *                         content of CompactHiF4Parameters, src/faquant/hif4.py:67-79) for
+ *                         decode K/V caches, in place of the reference's QDQ cache tensors
+ *                         (simulated_flash_attention.py:243-289)
+ *   faq_attention_decode  the decode step of simulated_flash_attention.py:457-909 over that
+ *                         cache (sfa:243-289): the recurrence of faq_attention_fwd_split
+ *                         with the query heads of a KV head packed together, from bf16 or
+ *                         packed HiF4 K/V
+ *   faq_attention_decode_workspace  workspace size of faq_attention_decode
  *   faq_pquant_groups     the in-register P quantizer of faq_attention_fwd on given values
  *                         (simulated_flash_attention.py:801-806 via hif4.py:143-271)
  *   faq_mfma_probe        no reference counterpart: a measurement helper (the device's
@@ -283,6 +292,55 @@ int faq_attention_fwd_split_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_s
                                     int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int causal,
                                     float scale, int quant_p, int p_levels, int norm_same, float* row_den,
                                     int nsplit, const faq_attn_opts* opts, faq_stream_t stream);
+
+/*
+ * Packed HiF4 K or V (decode caches): one row of 128 values per key, 4.5 bits per value.
+ * codes: 16 uint32 words per row; dims 8u .. 8u + 7 (u = 0..15) are word (u & 1) * 8 + u / 2,
+ * dim 8u + i in bits 4i .. 4i + 3 as 8 + the signed code (-7 .. 7).  meta: 2 uint32 words per row, one per
+ * 64-dim group: bits 0-7 the E6M2 byte ((e + 48) << 2) | m of the scale 2^e (1 + m/4), bits
+ * 8-15 the level-2 exponents (bit j: 8-dim group j), bits 16-31 the level-3 exponents (bit
+ * j: 4-dim group j).  A value is (nibble - 8) * 2^(lv2 + lv3) * scale / 4, the HiF4 QDQ
+ * value.  A group that held a NaN has E6M2 byte 0xFF and decodes to NaN.  Row r of
+ * (batch b, head h) is codes[(b * sb + h * sh + r) * 16], meta[(b * sb + h * sh + r) * 2].
+ */
+typedef struct faq_hif4_kv {
+  const uint32_t* codes; /* 16-byte aligned */
+  const uint32_t* meta;  /* 8-byte aligned */
+  int64_t sb, sh;        /* batch and head strides in rows */
+} faq_hif4_kv;
+
+/*
+ * faq_operand_prep with the HiF4 QDQ (levels, required) written in the packed form above
+ * instead of bf16: positions 0..L-1 of x [B, H, L, 128] go to rows 0..L-1 of (b, h), rows
+ * b * p_sb + h * p_sh + l.  The same prologue (key offset, Smooth-QK, Hadamard, one cast to
+ * round_dtype) and the same quantizer, so decoding gives bitwise faq_operand_prep's bf16
+ * output.  Rows are token-local: appending a decode position packs one row.
+ */
+int faq_operand_prep_hif4_kv(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
+                             const float* key_offset, int64_t off_sh, const float* smooth, int64_t smooth_sh,
+                             int smooth_divide, int hadamard, int round_dtype, int levels, uint32_t* codes,
+                             uint32_t* meta, int64_t p_sb, int64_t p_sh, faq_stream_t stream);
+
+/*
+ * Decode-shaped attention (few query rows per KV head, long key ranges): the results of
+ * faq_attention_fwd_split with the same nsplit, bitwise, for masks none or bottom-right
+ * causal (no opts, no out_levels), at most 32 query heads per KV head.  K and V come either
+ * as bf16 K [B, Hkv, Lk, 128] and V^T (k, vt with their strides; v_sd >= 128 ceil(Lk / 128),
+ * zero past Lk) or, with kp and vp non-NULL (both), as packed HiF4 rows (k and vt unused);
+ * the packed form decodes to the bf16 operands, so both give the same bits.  The query
+ * heads sharing a KV head are computed together (one pass over each K/V tile for all of
+ * them): a scores pass writes S and tile maxima to the workspace, a values pass runs the
+ * recurrence per key range, and a combine sums the ranges.  `workspace` is device memory of
+ * at least faq_attention_decode_workspace(B, Hq, Lq, Lk, nsplit) bytes, 16-byte aligned;
+ * nsplit is 1..4096.
+ */
+int64_t faq_attention_decode_workspace(int B, int Hq, int Lq, int Lk, int nsplit);
+int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
+                         int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
+                         int64_t v_sd, const faq_hif4_kv* kp, const faq_hif4_kv* vp, void* o, int o_dtype,
+                         int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int causal,
+                         float scale, int quant_p, int p_levels, int norm_same, float* row_den, int nsplit,
+                         void* workspace, int64_t workspace_bytes, faq_stream_t stream);
 
 /*
  * The attention kernel's in-register P quantizer (the HiF4 QDQ of P along keys,

@@ -40,7 +40,8 @@ def test_header_lists_the_entry_points():
         ["faq_last_error", "faq_version", "faq_hif4_qdq_rows", "faq_hif4_unpack_rows", "faq_hadamard_rows",
          "faq_act_qdq_rows", "faq_operand_prep", "faq_operand_prep_vt", "faq_attention_fwd",
          "faq_attention_fwd_split", "faq_attention_split_workspace", "faq_attention_mask_bounds",
-         "faq_mfma_probe", "faq_pquant_groups", "faq_hadamard_rows_native", "faq_attention_fwd_split_noalloc"]
+         "faq_mfma_probe", "faq_pquant_groups", "faq_hadamard_rows_native", "faq_attention_fwd_split_noalloc",
+         "faq_operand_prep_hif4_kv", "faq_attention_decode", "faq_attention_decode_workspace"]
     )
 
 
@@ -256,3 +257,53 @@ def test_pquant_groups_validation(lib):
     assert lib.faq_hadamard_rows_native(p16, p16, 1, 96, 1, None) == _lib.EINVAL
     assert lib.faq_hadamard_rows_native(p16, p16, 1, 1024, 1, None) == _lib.EUNSUP
     assert lib.faq_hadamard_rows_native(p16, p16, 1, 128, 0, None) == _lib.EINVAL
+
+
+def test_decode_and_packed_prep_validation(lib):
+    """faq_attention_decode / faq_operand_prep_hif4_kv refuse bad arguments before any device
+    work (a non-null dummy pointer is never dereferenced on these paths)."""
+    from faquant_amd import _lib
+
+    p16 = ctypes.c_void_p(1 << 20)
+    assert lib.faq_attention_decode_workspace(1, 32, 1, 5000, 0) == -1
+    ws = lib.faq_attention_decode_workspace(1, 32, 1, 5000, 40)
+    # S (32 rows x 40 tiles x 128 keys) + tile maxima + split maxima + partials, 256-aligned
+    assert ws == 655360 + 10240 + 5120 + 655360 + 10240
+
+    def decode(**kw):
+        a = dict(q=p16, k=p16, vt=p16, kp=None, vp=None, o=p16, Hq=32, Hkv=8, Lq=1, Lk=5000, nsplit=40, ws=p16,
+                 wsb=1 << 30, qp=1, lv=123, strides=(0, 0, 0))
+        a.update(kw)
+        s = a["strides"]
+        return lib.faq_attention_decode(a["q"], *s, a["k"], *s, a["vt"], 0, 0, 5120, a["kp"], a["vp"], a["o"], 1,
+                                        *s, 1, a["Hq"], a["Hkv"], a["Lq"], a["Lk"], 1, 0.088, a["qp"], a["lv"], 1,
+                                        None, a["nsplit"], a["ws"], a["wsb"], None)
+
+    kv = _lib.HiF4KV(1 << 20, 1 << 20, 0, 0)
+    assert decode(q=None) == _lib.EINVAL
+    assert decode(kp=ctypes.byref(kv)) == _lib.EINVAL  # K packed, V not
+    assert "both packed" in lib.faq_last_error().decode()
+    assert decode(Hq=33) == _lib.EINVAL
+    assert decode(Hq=64, Hkv=1) == _lib.EUNSUP  # more than 32 query heads per KV head
+    assert decode(nsplit=0) == _lib.EINVAL
+    assert decode(nsplit=5000) == _lib.EINVAL
+    assert decode(lv=7) == _lib.EINVAL
+    assert decode(strides=(1, 0, 0)) == _lib.EINVAL
+    assert decode(wsb=100) == _lib.EINVAL
+    assert "workspace" in lib.faq_last_error().decode()
+    assert decode(ws=None) == _lib.EINVAL
+    bad = _lib.HiF4KV(1 << 20, (1 << 20) + 4, 0, 0)  # meta not 8-byte aligned
+    assert decode(kp=ctypes.byref(bad), vp=ctypes.byref(kv)) == _lib.EINVAL
+    assert decode(Lq=0) == _lib.OK  # nothing to do
+
+    def prep(**kw):
+        a = dict(x=p16, codes=p16, meta=p16, lv=123, had=0, dt=1)
+        a.update(kw)
+        return lib.faq_operand_prep_hif4_kv(a["x"], a["dt"], 0, 0, 128, 1, 1, 4, None, 0, None, 0, 0, a["had"], 1,
+                                            a["lv"], a["codes"], a["meta"], 0, 0, None)
+
+    assert prep(codes=None) == _lib.EINVAL
+    assert prep(lv=0) == _lib.EINVAL  # the packed form needs HiF4 levels
+    assert prep(had=32) == _lib.EUNSUP
+    assert prep(dt=9) == _lib.EINVAL
+    assert prep(meta=ctypes.c_void_p((1 << 20) + 4)) == _lib.EINVAL

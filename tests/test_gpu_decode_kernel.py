@@ -1,0 +1,213 @@
+"""The decode kernel (faq_attention_decode) and packed HiF4 K/V caches.
+
+- ``pack_operand`` rows, decoded by ``unpack_rows`` below (the packed format restated in
+  integer arithmetic: (nibble - 8) (4 + m) 2^(e + lv2 + lv3 - 4)), equal operand_prep's
+  bf16 HiF4 values bitwise: levels 123/12/13, the Qwen post-RoPE prologue (r64 Hadamard,
+  Smooth-QK, key offset), zero rows, tiny negatives (-0), a NaN group;
+- decode over bf16 K/V gives faq_attention_fwd_split's output and row denominators with
+  the same number of key ranges, bitwise (GQA 1..16 heads per KV head, 1..5 positions,
+  ragged and single-key ranges, more ranges than tiles, P quantization off, both
+  normalizer modes);
+- decode over packed K/V gives the bf16 decode's bits;
+- the drop-in with ``faquant_kv_cache_packed`` grows a packed cache over decode steps,
+  with the same output as bf16 caches, bitwise, and matches the oracle.
+The split path these are compared with is itself checked against the oracle
+(test_gpu_decode.py).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import hif4 as OQ
+from oracle import inputs as OI
+from tests.test_gpu_attention import _oracle, assert_close_attention, module, to_dev
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def unpack_rows(codes: np.ndarray, meta: np.ndarray) -> np.ndarray:
+    """Values of packed HiF4 rows: codes uint32 [..., 16], meta uint32 [..., 2] -> fp32
+    [..., 128].  Dims 8u .. 8u + 7 sit in word (u & 1) 8 + u / 2, dim 8u + i in nibble i."""
+    codes = codes.astype(np.int64) & 0xFFFFFFFF
+    meta = meta.astype(np.int64) & 0xFFFFFFFF
+    out = np.empty(codes.shape[:-1] + (128,), dtype=np.float64)
+    for u in range(16):
+        word = codes[..., (u & 1) * 8 + u // 2]
+        m = meta[..., u // 8]
+        sb = m & 0xFF
+        e, mant = (sb >> 2) - 48, sb & 3
+        g8 = u % 8
+        lv2 = (m >> (8 + g8)) & 1
+        for i in range(8):
+            nib = (word >> (4 * i)) & 0xF
+            lv3 = (m >> (16 + 2 * g8 + i // 4)) & 1
+            val = (nib - 8) * (4 + mant) * np.exp2((e + lv2 + lv3 - 4).astype(np.float64))
+            out[..., 8 * u + i] = np.where(sb == 0xFF, np.nan, val)
+    return out.astype(np.float32)
+
+
+def _packed_values(cache) -> np.ndarray:
+    n = cache.length
+    return unpack_rows(cache.codes[:, :, :n].cpu().numpy(), cache.meta[:, :, :n].cpu().numpy())
+
+
+@pytest.mark.parametrize("levels", ["123", "12", "13"])
+@pytest.mark.parametrize("prologue", ["plain", "qwen_r64", "hadamard128"])
+def test_packed_rows_decode_to_operand_prep(dev, levels, prologue):
+    from faquant_amd import _ops
+
+    g = OI.rng(int(levels) + len(prologue))
+    B, H, L = 2, 3, 77
+    x = g.standard_normal((B, H, L, 128)).astype(np.float32) * 3
+    x[0, 1, 5] = 0.0                          # an all-zero row
+    x[1, 0, 9, :64] = -1e-30                  # a group of tiny negatives: codes 0 (-0 in bf16)
+    x[1, 2, 11, 64:] *= 1e4                   # a large group
+    x[0, 0, 13, 70] = np.nan                  # a NaN group (its 64 values become NaN)
+    xt = to_dev(x, dev, torch.bfloat16)
+    prep = {}
+    if prologue == "qwen_r64":
+        prep = dict(hadamard=64, smooth=to_dev(g.uniform(0.5, 2.0, size=(128,)), dev),
+                    key_offset=to_dev(g.standard_normal((H, 1, 128)) * 0.3, dev), smooth_divide=True,
+                    round_dtype=torch.bfloat16)
+    elif prologue == "hadamard128":
+        prep = dict(hadamard=128, round_dtype=torch.bfloat16)
+    want, _ = _ops.operand_prep(xt, levels=levels, **prep)
+    cache = _ops.PackedHiF4KV(B, H, 200, dev, levels)
+    cache.codes.fill_(0x5A5A5A5A)
+    _ops.pack_operand(xt[:, :, :40], levels=levels, out=cache, **prep)
+    _ops.pack_operand(xt[:, :, 40:], levels=levels, out=cache, start=40, **prep)  # rows are token-local
+    assert cache.length == L
+    got = _packed_values(cache)
+    ref = want.float().cpu().numpy()
+    print(f"[pack] levels {levels} {prologue}", flush=True)
+    assert np.array_equal(got, ref, equal_nan=True)
+    # the NaN reaches its Hadamard block, then its 64-value HiF4 group
+    assert np.isnan(got[0, 0, 13]).sum() == (128 if prologue == "hadamard128" else 64)
+    assert (cache.codes[:, :, L:] == 0x5A5A5A5A).all()  # rows past the end untouched
+    assert cache.nbytes() == B * H * L * 72  # 4.5 bits per value
+
+
+DECODE_CASES = [
+    # (B, Hq, Hkv, Lq, Lk, causal, mode, quant_p, levels, nsplit)
+    (1, 32, 8, 1, 5000, True, "quantized_same", True, "123", 40),    # Qwen3-8B decode step
+    (1, 64, 8, 1, 16384, True, "quantized_same", True, "12", 64),    # Qwen3-32B decode step
+    (2, 8, 2, 3, 1000, True, "quantized_same", True, "123", 6),      # G 4 x 3 positions
+    (1, 4, 1, 5, 900, True, "unquantized", True, "123", 4),          # G 4 x 5 positions
+    (1, 16, 1, 2, 3000, True, "quantized_same", True, "123", 7),     # G 16 x 2: 32 columns
+    (1, 40, 40, 1, 2000, False, "quantized_same", True, "123", 8),   # MHA, non-causal
+    (3, 12, 4, 1, 129, True, "quantized_same", True, "13", 2),       # G 3: 30 of 32 columns live
+    (1, 4, 4, 1, 777, False, "quantized_same", True, "12", 3),       # ragged last tile
+    (1, 2, 1, 1, 300, True, "quantized_same", True, "13", 16),       # more ranges than tiles
+    (1, 8, 2, 1, 1, True, "quantized_same", True, "123", 1),         # one key
+    (1, 4, 1, 2, 640, True, "quantized_same", False, "123", 5),      # P not quantized
+]
+
+
+def _decode_inputs(case, dev):
+    from faquant_amd import _ops
+
+    B, Hq, Hkv, Lq, Lk, causal, mode, qp, lv, nsplit = case
+    g = OI.rng(7 * Lk + Lq + Hq)
+    q = OQ.bf16_round(g.standard_normal((B, Hq, Lq, 128), dtype=np.float32) * 2)
+    k = OQ.bf16_round(g.standard_normal((B, Hkv, Lk, 128), dtype=np.float32))
+    v = OQ.bf16_round(g.standard_normal((B, Hkv, Lk, 128), dtype=np.float32))
+    qh, _ = _ops.operand_prep(to_dev(q, dev, torch.bfloat16), levels=lv)
+    kh, _ = _ops.operand_prep(to_dev(k, dev, torch.bfloat16), levels=lv)
+    vt = _ops.operand_prep_vt(to_dev(v, dev, torch.bfloat16), levels=lv if qp else None)
+    kw = dict(causal=causal, scale=128**-0.5, quant_p=qp, p_levels=lv, norm_same=mode == "quantized_same")
+    return (q, k, v), (qh, kh, vt), kw
+
+
+def _run(fn, case, dev, **extra):
+    B, Hq, Hkv, Lq = case[:4]
+    out = torch.empty((B, Lq, Hq, 128), device=dev, dtype=torch.float32)
+    den = torch.empty((B, Hq, Lq), device=dev, dtype=torch.float32)
+    fn(out=out.transpose(1, 2), row_den=den, **extra)
+    return out, den
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"_{c[6]}_{c[8]}_{c[9]}")
+def test_decode_equals_split_path_bitwise(dev, case):
+    from faquant_amd import _ops
+
+    B, Hq, Hkv, Lq, Lk, causal, mode, qp, lv, nsplit = case
+    (q, k, v), (qh, kh, vt), kw = _decode_inputs(case, dev)
+    print(f"[decode] {case}", flush=True)
+    split_o, split_l = _run(lambda **a: _ops.attention_fwd(qh, kh, vt, Lk, split=nsplit, **kw, **a), case, dev)
+    dec_o, dec_l = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, vt=vt, split=nsplit, **kw, **a), case, dev)
+    assert torch.equal(dec_o, split_o)
+    assert torch.equal(dec_l, split_l)
+    if qp:
+        kc = _ops.pack_operand(to_dev(k, dev, torch.bfloat16), levels=lv,
+                               out=_ops.PackedHiF4KV(B, Hkv, Lk + 5, dev, lv))
+        vc = _ops.pack_operand(to_dev(v, dev, torch.bfloat16), levels=lv,
+                               out=_ops.PackedHiF4KV(B, Hkv, Lk + 5, dev, lv))
+        pk_o, pk_l = _run(lambda **a: _ops.attention_decode(qh, Lk, packed=(kc, vc), split=nsplit, **kw, **a),
+                          case, dev)
+        assert torch.equal(pk_o, dec_o)
+        assert torch.equal(pk_l, dec_l)
+    if case[4] == 5000 or Lq > 1:
+        ref = _oracle(q, k, v, causal=causal, levels=lv, mode=mode, qk=True, pv=qp)
+        assert_close_attention(dec_o.cpu().numpy(), ref, f"decode {case}")
+
+
+def test_drop_in_routes_decode_steps_to_the_decode_kernel(dev):
+    """attention_fwd without an explicit split sends a decode-shaped call to the decode
+    kernel (its automatic range count), which matches the oracle."""
+    from faquant_amd import _ops
+
+    case = (1, 32, 8, 1, 5000, True, "quantized_same", True, "123", None)
+    (q, k, v), (qh, kh, vt), kw = _decode_inputs(case, dev)
+    assert _ops.decode_shaped(32, 8, 1) and not _ops.decode_shaped(32, 8, 9)
+    auto_o, _ = _run(lambda **a: _ops.attention_fwd(qh, kh, vt, 5000, **kw, **a), case, dev)
+    n = _ops.decode_split_count(1, 8, 5000, _ops._device_cus(qh.device))
+    dec_o, _ = _run(lambda **a: _ops.attention_decode(qh, 5000, k=kh, vt=vt, split=n, **kw, **a), case, dev)
+    assert torch.equal(auto_o, dec_o)
+    assert_close_attention(auto_o.cpu().numpy(), _oracle(q, k, v, causal=True, levels="123"), "routed decode")
+
+
+@pytest.mark.parametrize("core", [False, True], ids=["sdpa", "qwen_core"])
+def test_packed_cache_decode_steps_match_bf16_cache(dev, core):
+    """Decode steps through the drop-in with packed caches: the packed rows grow by one
+    position per step (and past the capacity), the output equals the bf16 caches' output
+    bitwise at every step, and the last step matches the oracle."""
+    from faquant_amd.qwen3 import attention_core
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward
+
+    g = OI.rng(91)
+    L0, steps = 1020, 6  # crosses the 1024-row capacity of the first packed buffer
+    q, k, v = (OQ.bf16_round(g.standard_normal((1, h, L0 + steps, 128), dtype=np.float32)) for h in (8, 2, 2))
+    qt, kt, vt = (to_dev(a, dev, torch.bfloat16) for a in (q, k, v))
+
+    def mk(packed):
+        m = module()
+        m.faquant_kv_cache_packed = packed
+        if core:
+            m.faquant_qk_rotation = True
+            m.faquant_qk_rotation_block_size = 64
+        return m
+
+    def call(m, lq, lk):
+        if core:
+            return attention_core(m, qt[:, :, lk - lq : lk], kt[:, :, :lk], vt[:, :, :lk])
+        return simulated_flash_attention_forward(m, qt[:, :, lk - lq : lk], kt[:, :, :lk], vt[:, :, :lk], None)[0]
+
+    packed, plain = mk(True), mk(False)
+    a, b = call(packed, L0, L0), call(plain, L0, L0)  # prefill: bf16 operands for both
+    assert torch.equal(a, b)
+    cache0 = packed.faquant_k_matmul_qdq_cache
+    for lk in range(L0 + 1, L0 + steps + 1):
+        print(f"[packed decode] core={core} length {lk}", flush=True)
+        a, b = call(packed, 1, lk), call(plain, 1, lk)
+        assert torch.equal(a, b)
+        kc = packed.faquant_k_matmul_qdq_cache
+        assert kc.length == lk and packed.faquant_v_matmul_qdq_cache.length == lk
+    assert kc is not cache0  # grown past the capacity
+    kb = plain.faquant_k_matmul_qdq_cache.float().cpu().numpy()
+    assert np.array_equal(_packed_values(kc), kb)
+    if not core:
+        ref = _oracle(q[:, :, -1:], k, v, causal=True, levels="123", dtype="bfloat16")  # bf16 output
+        assert_close_attention(a.float().cpu().numpy(), ref, "packed decode step")
