@@ -231,6 +231,74 @@ def mfma_probe(dev) -> float:
     return blocks * 8 * iters * 4 * 32768 / (ms * 1e-3) / 1e12
 
 
+def decode_bench(cfg, context: int, steps: int, warmup: int) -> dict:
+    """One decode step (one new query position per head) of `cfg`'s heads over `context` cached
+    keys, timed three ways with HIP events on the launch stream: the split-key path
+    (faq_attention_fwd_split), the decode kernel over bf16 K/V and over packed HiF4 K/V.
+    The roofline is HBM: algorithmic bytes = the K and V cache bytes one step must read
+    (bf16: 512 per key and KV head, packed: 144) plus Q and the output."""
+    import torch
+
+    from faquant_amd import _ops
+
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, L = cfg["B"], cfg["Hq"], cfg["Hkv"], context
+    lv = cfg["levels"]
+    gen = torch.Generator(device=dev).manual_seed(1)
+    q = torch.randn((B, Hq, 1, 128), device=dev, generator=gen).to(torch.bfloat16)
+    k = torch.randn((B, Hkv, L, 128), device=dev, generator=gen).to(torch.bfloat16)
+    v = torch.randn((B, Hkv, L, 128), device=dev, generator=gen).to(torch.bfloat16)
+    qh, _ = _ops.operand_prep(q, levels=lv, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16)
+    kh, _ = _ops.operand_prep(k, levels=lv, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16)
+    vt = _ops.operand_prep_vt(v, levels=lv)  # the split path's V^T
+    vh, _ = _ops.operand_prep(v, levels=lv)  # the decode cache's natural rows
+    kc = _ops.pack_operand(k, levels=lv, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16,
+                           out=_ops.PackedHiF4KV(B, Hkv, L, dev, lv))
+    vc = _ops.pack_operand(v, levels=lv, out=_ops.PackedHiF4KV(B, Hkv, L, dev, lv))
+    del k, v
+    out = torch.empty((B, 1, Hq, 128), device=dev, dtype=torch.bfloat16)
+    kw = dict(causal=True, scale=128**-0.5, quant_p=True, p_levels=lv, norm_same=True, out=out.transpose(1, 2))
+    cus = _ops._device_cus(dev)
+    n_split = _ops._split_count(B, Hq, Hkv, 1, L, cus)
+    n_dec = _ops.decode_split_count(B, Hkv, L, cus)
+    paths = {
+        "split_path_bf16": (lambda: _ops.attention_fwd(qh, kh, vt, L, split=n_split, **kw), 512, n_split),
+        "decode_bf16": (lambda: _ops.attention_decode(qh, L, k=kh, v=vh, split=n_dec, **kw), 512, n_dec),
+        "decode_packed_hif4": (lambda: _ops.attention_decode(qh, L, packed=(kc, vc), split=n_dec, **kw), 144, n_dec),
+    }
+    res = {}
+    for name, (fn, per_key, nsplit) in paths.items():
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            evs.append((a, b))
+        torch.cuda.synchronize()
+        us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+        mean = sum(us) / len(us)
+        nbytes = B * Hkv * L * per_key + 2 * (q.numel() + out.numel())
+        gbps = nbytes / (mean * 1e-6) / 1e9
+        res[name] = {"us_mean": round(mean, 2), "us_median": round(us[len(us) // 2], 2), "nsplit": nsplit,
+                     "algorithmic_bytes": nbytes, "achieved_gbps": round(gbps, 1),
+                     "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+    return {
+        "metric": "HiF4 decode attention step: HBM GB/s on the K/V cache bytes, 1 GPU",
+        "unit": "GB/s",
+        "higher_is_better": True,
+        "config": {"workload": f"{cfg['workload'].split(' causal')[0]} decode step over {L} cached keys",
+                   "batch": B, "q_heads": Hq, "kv_heads": Hkv, "context": L, "hif4_levels": lv,
+                   "pv_normalizer": "quantized_same"},
+        "steps": steps, "warmup": warmup, "data": "synthetic",
+        "peak_gbps": HBM_PEAK_GBPS,
+        "paths": res,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -242,6 +310,8 @@ def main():
     # the CPU share of one GPU on the GPU boxes is 16 cores
     ap.add_argument("--cpu-workers", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode", type=int, default=0, metavar="CONTEXT",
+                    help="time one decode step over CONTEXT cached keys of --config's heads instead")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE scaling)")
     args = ap.parse_args()
@@ -253,6 +323,10 @@ def main():
     import torch
 
     from faquant_amd import _ops
+
+    if args.decode:
+        print(json.dumps(decode_bench(CONFIGS[args.config], args.decode, args.steps, args.warmup)), flush=True)
+        return
 
     if args.calibrate_copy:
         src = torch.empty(64 << 20, device="cuda:0", dtype=torch.float32).fill_(1.0)

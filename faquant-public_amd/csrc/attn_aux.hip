@@ -74,8 +74,9 @@ __global__ __launch_bounds__(kScanThreads) void split_scan_kernel(SplitScanArgs 
 // O = sum_j 2^(m_j - M) O_j / sum_j 2^(m_j - M) l_j with M the row's final running maximum;
 // the per-split recurrences already used the reference's maxima, so only the fp32 order of
 // the O and l sums differs from one pass.
-constexpr int kCombineThreads = 256;
+constexpr int kCombineThreads = 512;
 constexpr int kCombineMaxSplits = 4096;
+constexpr int kCombineGroups = kCombineThreads / 32;  // split groups: 32 threads cover a row's 128 dims
 
 struct SplitCombineArgs {
   const float* part_o;   // [nsplit, rows_total, 128]
@@ -89,13 +90,13 @@ struct SplitCombineArgs {
 };
 
 // One workgroup per row.  The split weights w_j = 2^(m_j - M) (0 for an empty split) go to
-// LDS; threads (g, d), g = tid / 128, sum w_j O_j[d] over the splits j = g mod 2 with eight
-// loads in flight, and the two halves and the weighted l sums are added in a fixed order
-// (deterministic results).
+// LDS; thread (g, q), g = tid / 32, sums w_j O_j[4q .. 4q + 3] over the splits j = g mod 16
+// in order, eight float4 loads in flight, and the 16 group sums are added in a fixed tree
+// (deterministic results); l is summed the same way.
 __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCombineArgs a) {
   __shared__ float wsh[kCombineMaxSplits];
   __shared__ float red[kCombineThreads];
-  __shared__ float half_acc[kDim];
+  __shared__ float4 gsum[kCombineGroups][32];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   // M: the maximum over the splits
@@ -126,32 +127,54 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCom
     __syncthreads();
   }
   const float l = red[0];
-  // O: split j of parity g, eight loads in flight per thread
-  const int g = tid / kDim, d = tid % kDim;
-  const float* po = a.part_o + static_cast<int64_t>(row) * kDim + d;
-  const int64_t js = static_cast<int64_t>(a.rows_total) * kDim;
-  float acc = 0.0f;
+  // O: splits j = g, g + 16, ... of group g
+  const int g = tid / 32, q = tid % 32;
+  const float4* po = reinterpret_cast<const float4*>(a.part_o + static_cast<int64_t>(row) * kDim) + q;
+  const int64_t js = static_cast<int64_t>(a.rows_total) * (kDim / 4);  // float4 stride of one split
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  auto add = [&](float w, float4 v) {
+    acc.x = __builtin_fmaf(w, v.x, acc.x);
+    acc.y = __builtin_fmaf(w, v.y, acc.y);
+    acc.z = __builtin_fmaf(w, v.z, acc.z);
+    acc.w = __builtin_fmaf(w, v.w, acc.w);
+  };
   int j = g;
-  for (; j + 14 < a.nsplit; j += 16) {
-    float v[8];
+  for (; j + 7 * kCombineGroups < a.nsplit; j += 8 * kCombineGroups) {
+    float4 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = po[static_cast<int64_t>(j + 2 * u) * js];
+    for (int u = 0; u < 8; ++u) v[u] = po[static_cast<int64_t>(j + kCombineGroups * u) * js];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(wsh[j + 2 * u], v[u], acc);
+    for (int u = 0; u < 8; ++u) add(wsh[j + kCombineGroups * u], v[u]);
   }
-  for (; j < a.nsplit; j += 2) acc = __builtin_fmaf(wsh[j], po[static_cast<int64_t>(j) * js], acc);
-  if (g == 1) half_acc[d] = acc;
+  for (; j < a.nsplit; j += kCombineGroups) add(wsh[j], po[static_cast<int64_t>(j) * js]);
+  gsum[g][q] = acc;
   __syncthreads();
+  for (int d = kCombineGroups / 2; d > 0; d >>= 1) {
+    if (g < d) {
+      const float4 o = gsum[g + d][q];
+      float4 m = gsum[g][q];
+      m.x += o.x;
+      m.y += o.y;
+      m.z += o.z;
+      m.w += o.w;
+      gsum[g][q] = m;
+    }
+    __syncthreads();
+  }
   if (g == 0) {
-    acc += half_acc[d];
+    const float4 sum = gsum[0][q];
     const int pos = row % a.Lq;
     const int hq = (row / a.Lq) % a.Hq;
     const int b = row / (a.Lq * a.Hq);
-    if (a.row_den && d == 0) a.row_den[row] = l;
-    const float v = l > 0.0f ? acc / fmaxf(l, 1.17549435e-38f) : 0.0f;
-    const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + d;
-    if (a.o_f32) static_cast<float*>(a.o)[off] = v;
-    else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
+    if (a.row_den && q == 0) a.row_den[row] = l;
+    const float vals[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v = l > 0.0f ? vals[e] / fmaxf(l, 1.17549435e-38f) : 0.0f;
+      const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + 4 * q + e;
+      if (a.o_f32) static_cast<float*>(a.o)[off] = v;
+      else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
+    }
   }
 }
 

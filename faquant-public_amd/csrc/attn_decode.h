@@ -12,13 +12,13 @@ constexpr int kDecWaves = 4;
 struct DecodeArgs {
   const uint16_t* q;  // bf16 [B, Hq, Lq, 128] at element strides, last stride 1
   int64_t q_sb, q_sh, q_sl;
-  // bf16 operands: K [B, Hkv, Lk, 128] and V^T [B, Hkv, 128, >= 128 ntiles] (zero past Lk)
+  // bf16 operands: K and V [B, Hkv, Lk, 128] at element strides, last stride 1
   const uint16_t* k;
   int64_t k_sb, k_sh, k_sl;
-  const uint16_t* vt;
-  int64_t v_sb, v_sh, v_sd;
+  const uint16_t* v;
+  int64_t v_sb, v_sh, v_sl;
   // packed HiF4 operands (one 128-value row per key): 16 code words (dims 8u .. 8u + 7 in
-  // word u, dim 8u + i in nibble i, nibble = 8 + signed code) and 2 meta words (per 64-dim
+  // word (u & 1) 8 + u / 2, dim 8u + i in nibble i, nibble = 8 + signed code) and 2 meta words (per 64-dim
   // group: E6M2 byte | level-2 bits << 8 | level-3 bits << 16); strides in key rows
   const uint32_t* kc;
   const uint32_t* km;

@@ -11,9 +11,10 @@
 // so one wave's 32 MFMA columns hold G heads x 32 / G positions (column n: head n % G,
 // position n / G of the row block).  At one decode position that is G live columns in
 // one wave, where one wave per query head would repeat each tile's QK and PV MFMAs G
-// times.  Each wave is an independent (row block, split); nothing is shared between the
-// waves of a workgroup, so K/V tiles go straight from HBM to registers (non-temporal
-// loads: every byte is read once).
+// times.  Each wave is an independent (row block, split) with its own LDS region: K and V
+// come as natural [key][dim] rows (a tile is 32 KiB of contiguous bf16, or 9 KiB packed),
+// loaded with coalesced row reads and staged half a tile at a time in the layout the MFMA
+// fragments read (V transposed), the next half tile's loads in flight meanwhile.
 //
 // Two passes, so that K is read once:
 //   scores  S = K Q^T per tile (the prefill kernel's MFMA chains, bit for bit), masked
@@ -34,9 +35,7 @@
 // bits << 16; the content of hif4.py:67-79).  A value is (nibble - 8) 2^(lv2 + lv3) s / 4,
 // one fma of the nibble with per-4-group constants (exact: at most six significant
 // bits), so the unpacked operands are bitwise the bf16 operands of the bf16 path and the
-// outputs are bitwise equal.  K unpacks in registers straight into the QK fragments; V is
-// unpacked per half tile into the wave's own LDS region in the transposed layout the PV
-// fragments read (the HiF4 groups of V run along head_dim, the PV contraction along keys).
+// outputs are bitwise equal.  Both unpack per key row on their way into LDS.
 #include "attn_decode.h"
 #include "hif4_attention.hip"
 
@@ -45,15 +44,7 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ u32x4 ld_nt(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
-  bf16x8 r;
-  __builtin_memcpy(&r, &v, 16);
-  return r;
-}
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // The rows of a decode wave and its key tiles.
 struct DecWave {
@@ -88,6 +79,13 @@ __device__ __forceinline__ DecWave dec_wave(const DecodeArgs& a, int wave_id, in
   return w;
 }
 
+// Maximum over the 64 lanes, in every lane.
+__device__ __forceinline__ float wave_max_f32(float x) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+
 __device__ __forceinline__ int dec_wave_id() {
   return __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kDecWaves + static_cast<int>(threadIdx.x >> 6));
 }
@@ -118,67 +116,128 @@ __device__ __forceinline__ void hif4_unpack8(uint32_t word, uint32_t meta, int g
   }
 }
 
+// Orders this wave's LDS accesses around a stage change (the LDS unit runs one wave's
+// accesses in order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Half tiles.  Half tile s of a 128-key tile holds the keys 32 s + 0..31 and 64 + 32 s +
+// 0..31 as local keys r = 0..63: the QK key blocks kb = 2 s, 2 s + 1 (keys pi(kb, m)) and
+// the PV chunks c = 4 s .. 4 s + 3 (keys 64 half + 8 c + 0..7) of the prefill layout.
+__device__ __forceinline__ int stage_key(int r, int s) { return (r & 31) + 32 * s + 64 * (r >> 5); }
+
 // ---------------------------------------------------------------------------------------
-// Scores pass.  The K operand of a tile: bf16 fragments (key krow0 + 16 kb, dims
-// 16 c + 8 half, the prefill kernel's QK A operand) or the packed words they unpack from.
+// Half tiles of K and of V are staged in the wave's LDS region the same way: bf16 rows of the
+// 64 local keys at a pitch of 17 16-byte units, from coalesced row loads: bf16 rows
+// (instruction i, lane l: unit l % 16 of local key 4 i + l / 16, 1 KiB contiguous per
+// instruction) or packed rows (lane l: the 72 bytes of local key l, unpacked in registers).
+// The QK fragments are plain 16-byte reads of that layout (the prefill kernel's
+// conflict-free pitch); the PV fragments are transposing reads (ds_read_b64_tr_b16).
+constexpr int kStageBytes = 64 * kRowUnits * 16;  // 17408
+constexpr int kRowBytes = kRowUnits * 16;
+
+// One operand's rows: bf16 (base, row stride in elements) or packed (codes, meta, row
+// index of key 0 of the (batch, head)).
+struct RowSrc {
+  const uint16_t* base;
+  int64_t sl;
+  const uint32_t* codes;
+  const uint32_t* meta;
+  int64_t row0;
+};
+
 template <bool kPacked>
-struct KTile;
+struct RowsRaw;
 
 template <>
-struct KTile<false> {
-  bf16x8 f[4][8];
+struct RowsRaw<false> {
+  u32x4 x[16];
 };
 
 template <>
-struct KTile<true> {
-  uint32_t w[4][8];  // the lane half's code words: chunk c (dims 16c + 8 half) in w[kb][c]
-  uint32_t m[4][2];  // meta words of the key's two 64-dim groups
+struct RowsRaw<true> {
+  u32x4 c[4];     // the 16 code words of the key
+  uint32_t m[2];  // its two meta words
 };
 
+// Loads of half tile s of tile t; keys past Lk read the last key's row (K: masked later;
+// V: zeroed in LDS by zero_tail_rows).  The loads are unconditional, so the memory counter
+// the waits use sees the same sequence on every iteration (a wait then covers only the
+// loads it needs: the counter completes in order).
 template <bool kPacked>
-__device__ __forceinline__ void load_k_block(const DecodeArgs& a, const DecWave& w, int t, int kb, int krow0,
-                                             int half, KTile<kPacked>& k) {
-  const int key = min(t * kKeyTile + krow0 + 16 * kb, a.Lk - 1);  // ragged tail: masked later
+__device__ __forceinline__ void load_rows(const RowSrc& src, int Lk, int t, int s, int lane, RowsRaw<kPacked>& raw) {
   if constexpr (kPacked) {
-    const int64_t r = w.b * a.kp_sb + w.kvh * a.kp_sh + key;
-    const uint32_t* cw = a.kc + r * 16 + 8 * half;  // slots 8 half + c
-    const u32x4 x0 = ld_nt(cw), x1 = ld_nt(cw + 4);
+    const int key = t * kKeyTile + stage_key(lane, s);
+    const int64_t row = src.row0 + min(key, Lk - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      k.w[kb][i] = x0[i];
-      k.w[kb][4 + i] = x1[i];
+    for (int i = 0; i < 4; ++i) raw.c[i] = ld16(src.codes + row * 16 + 4 * i);
+    const uint2 mm = *reinterpret_cast<const uint2*>(src.meta + row * 2);
+    raw.m[0] = mm.x;
+    raw.m[1] = mm.y;
+  } else {
+    const uint16_t* b = src.base + 8 * (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = t * kKeyTile + stage_key(4 * i + (lane >> 4), s);
+      raw.x[i] = ld16(b + static_cast<int64_t>(min(key, Lk - 1)) * src.sl);
     }
+  }
+}
+
+// Zeros of the staged rows past Lk (the zero padding of the bf16 V^T layout: P is 0 there,
+// and 0 times a repeated NaN must not reach PV).  Lane l clears local key l.
+__device__ __forceinline__ void zero_tail_rows(int Lk, int t, int s, int lane, uint8_t* region) {
+  if (t * kKeyTile + stage_key(lane, s) >= Lk) {
 #pragma unroll
-    for (int g = 0; g < 2; ++g) k.m[kb][g] = __builtin_nontemporal_load(a.km + r * 2 + g);
-  } else {
-    const uint16_t* kp = a.k + w.b * a.k_sb + w.kvh * a.k_sh + static_cast<int64_t>(key) * a.k_sl + 8 * half;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) k.f[kb][c] = as_bf16x8(ld_nt(kp + 16 * c));
+    for (int u = 0; u < 16; ++u) *reinterpret_cast<u32x4*>(region + lane * kRowBytes + u * 16) = u32x4{0u, 0u, 0u, 0u};
   }
 }
 
 template <bool kPacked>
-__device__ __forceinline__ bf16x8 k_fragment(const KTile<kPacked>& k, int kb, int c, int half) {
+__device__ __forceinline__ void store_rows(const RowsRaw<kPacked>& raw, int lane, uint8_t* region) {
   if constexpr (kPacked) {
-    const int g = c >> 2, g8 = 2 * (c & 3) + half;  // 64-dim group, 8-dim group within it
-    float v[8];
-    hif4_unpack8(k.w[kb][c], k.m[kb][g], g8, v);
-    return pack8<true>(v);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int slot = (u & 1) * 8 + (u >> 1);  // dims 8u .. 8u + 7
+      float v[8];
+      hif4_unpack8(raw.c[slot >> 2][slot & 3], raw.m[u >> 3], u & 7, v);
+      *reinterpret_cast<bf16x8*>(region + lane * kRowBytes + u * 16) = pack8<true>(v);
+    }
   } else {
-    return k.f[kb][c];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      *reinterpret_cast<u32x4*>(region + (4 * i + (lane >> 4)) * kRowBytes + (lane & 15) * 16) = raw.x[i];
   }
 }
 
+template <bool kPacked>
+__device__ __forceinline__ RowSrc k_source(const DecodeArgs& a, const DecWave& w) {
+  if constexpr (kPacked) return RowSrc{nullptr, 0, a.kc, a.km, w.b * a.kp_sb + w.kvh * a.kp_sh};
+  else return RowSrc{a.k + w.b * a.k_sb + w.kvh * a.k_sh, a.k_sl, nullptr, nullptr, 0};
+}
+
+template <bool kPacked>
+__device__ __forceinline__ RowSrc v_source(const DecodeArgs& a, const DecWave& w) {
+  if constexpr (kPacked) return RowSrc{nullptr, 0, a.vc, a.vm, w.b * a.vp_sb + w.kvh * a.vp_sh};
+  else return RowSrc{a.v + w.b * a.v_sb + w.kvh * a.v_sh, a.v_sl, nullptr, nullptr, 0};
+}
+
+// Scores pass.
 template <bool kPacked>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dec_scores_kernel(DecodeArgs a) {
+  __shared__ __attribute__((aligned(128))) uint8_t lds[kDecWaves * kStageBytes];
   const int lane = threadIdx.x & 63;
   const int n = lane & 31;
   const int half = lane >> 5;
   const int wave_id = dec_wave_id();
   if (wave_id >= a.B * a.Hkv * a.n_rb * a.nsplit) return;
   const DecWave w = dec_wave(a, wave_id, n);
+  uint8_t* const region = lds + (threadIdx.x >> 6) * kStageBytes;
   const int off = a.Lk - a.Lq;
+  const RowSrc ksrc = k_source<kPacked>(a, w);
 
   bf16x8 qf[8];
   {
@@ -187,25 +246,32 @@ void dec_scores_kernel(DecodeArgs a) {
     for (int c = 0; c < 8; ++c) qf[c] = w.live ? *reinterpret_cast<const bf16x8*>(qp + 16 * c) : bf16x8{};
   }
   // QK A-operand row m of key block kb is key pi(kb, m) = krow0(m) + 16 kb, so lane (n, half)
-  // ends with keys 64 half + 16 kb + i of row n (the prefill kernel's layout)
+  // ends with keys 64 half + 16 kb + i of row n (the prefill kernel's layout); as a local key
+  // of half tile kb / 2 that is (pi & 31) + 32 (pi >> 6)
   const int krow0 = 64 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
   float smax = -INFINITY;
-  KTile<kPacked> k;
-  if (w.t_lo < w.t_hi) {
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) load_k_block<kPacked>(a, w, w.t_lo, kb, krow0, half, k);
-  }
+  RowsRaw<kPacked> raw;
+  if (w.t_lo < w.t_hi) load_rows<kPacked>(ksrc, a.Lk, w.t_lo, 0, lane, raw);
   for (int t = w.t_lo; t < w.t_hi; ++t) {
     const int key0 = t * kKeyTile;
     floatx16 s[4];
-    // each accumulator is the chain c = 0..7 of the prefill kernel; the block's registers
-    // take the next tile's block as soon as its chain has issued
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      s[kb] = floatx16{};
+    for (int st = 0; st < 2; ++st) {
+      wave_lds_order();  // the previous half tile's fragment reads are issued
+      store_rows<kPacked>(raw, lane, region);
+      wave_lds_order();
+      // the next half tile's loads fly during this one's MFMAs
+      // (past the split's last tile: a repeat of its first half, unused)
+      load_rows<kPacked>(ksrc, a.Lk, st == 0 ? t : min(t + 1, w.t_hi - 1), st ^ 1, lane, raw);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) s[kb] = mfma32(k_fragment<kPacked>(k, kb, c, half), qf[c], s[kb]);
-      if (t + 1 < w.t_hi) load_k_block<kPacked>(a, w, t + 1, kb, krow0, half, k);
+      for (int kb = 2 * st; kb < 2 * st + 2; ++kb) {
+        const int pi = krow0 + 16 * kb;
+        const uint8_t* kp = region + (((pi & 31) + 32 * (pi >> 6)) * kRowUnits + half) * 16;
+        // each accumulator is the chain c = 0..7 of the prefill kernel
+        s[kb] = floatx16{};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) s[kb] = mfma32(lds_read_at(kp, 32 * c), qf[c], s[kb]);
+      }
     }
     if (key0 + kKeyTile > a.Lk || (a.causal && key0 + kKeyTile - 1 > w.pmin + off)) {
       const int lim = a.causal ? min(a.Lk - 1, w.pos + off) : a.Lk - 1;
@@ -237,93 +303,105 @@ void dec_scores_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Values pass.
+// Values pass.  The PV A operand of chunk c (V^T rows 32 mb + m, keys 64 half + 8 c + 0..7)
+// comes from the natural half tile by two transposing reads: within each 16-lane group,
+// lane i of ds_read_b64_tr_b16 receives element i % 4 of the 8 bytes addressed by lanes
+// 4k + i / 4, k = 0..3.  Lane jj of group g addresses local key 32 (g / 2) + 8 (c % 4) + jj / 4
+// (+ 4 for the second read), dims 32 mb + 16 (g % 2) + 4 (jj % 4) .. + 3, so lane i receives
+// dim 32 mb + 16 (g % 2) + i of four consecutive keys.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
-// The wave's LDS region for one unpacked half tile of V (packed V): V^T rows d = 0..127 of
-// 64 keys (the keys 32 s + 0..31 and 64 + 32 s + 0..31 of half tile s, as local keys
-// 0..63), a 144-byte pitch (16-byte aligned fragment reads) and rows 64..127 moved by 64
-// bytes, so the two lane halves of a 4-byte store (dims d and d + 64) use other banks.
-constexpr int kVPitch = 144;
-constexpr int kVStageBytes = 18560;
-static_assert(127 * kVPitch + 64 + 128 <= kVStageBytes, "V stage region");
-
-__device__ __forceinline__ int vrow_byte(int d) { return d * kVPitch + (d >= 64 ? 64 : 0); }
-
-// Raw packed V of one half tile for lane (p = lane % 32, h = lane / 32): keys 2p, 2p + 1
-// of the half tile's local keys, dims 64 h .. 64 h + 63 (one group).
-struct VRaw {
-  uint32_t w[2][8];
-  uint32_t m[2];
-};
-
-__device__ __forceinline__ void load_v_raw(const DecodeArgs& a, const DecWave& w, int t, int s, int lane, VRaw& r) {
-  const int p = lane & 31, h = lane >> 5;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int lk = 2 * p + e;  // local key
-    const int key = t * kKeyTile + (lk < 32 ? 32 * s + lk : 64 + 32 * s + lk - 32);
-    const int64_t row = w.b * a.vp_sb + w.kvh * a.vp_sh + min(key, a.Lk - 1);
-    // dims 64 h + 8 u: u even in slots 4 h + u / 2, u odd in slots 8 + 4 h + u / 2
-    const u32x4 x0 = ld_nt(a.vc + row * 16 + 4 * h), x1 = ld_nt(a.vc + row * 16 + 8 + 4 * h);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      r.w[e][2 * i] = x0[i];
-      r.w[e][2 * i + 1] = x1[i];
-    }
-    // keys past Lk are zeros, as the bf16 V^T padding is (their P is 0, and 0 times a
-    // stale value could be NaN)
-    r.m[e] = key < a.Lk ? __builtin_nontemporal_load(a.vm + row * 2 + h) : 0u;
-    if (key >= a.Lk) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) r.w[e][i] = 0x88888888u;
-    }
-  }
-}
-
-// Unpack a half tile into the LDS region: dim d = 64 h + 8 u + i, local keys 2p, 2p + 1 as
-// one 4-byte store.
-__device__ __forceinline__ void store_v_stage(const VRaw& r, int lane, uint8_t* region) {
-  const int p = lane & 31, h = lane >> 5;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    float v0[8], v1[8];
-    hif4_unpack8(r.w[0][u], r.m[0], u, v0);
-    hif4_unpack8(r.w[1][u], r.m[1], u, v1);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t pair = __builtin_amdgcn_perm(__float_as_uint(v1[i]), __float_as_uint(v0[i]), 0x07060302u);
-      *reinterpret_cast<uint32_t*>(region + vrow_byte(64 * h + 8 * u + i) + 4 * p) = pair;
-    }
-  }
-}
-
-// Orders this wave's LDS accesses around a stage change (the LDS unit runs one wave's
-// accesses in order; this keeps the compiler from moving them across).
-__device__ __forceinline__ void wave_lds_order() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  __builtin_amdgcn_wave_barrier();
+__device__ __forceinline__ bf16x8 vt_fragment(const uint8_t* region, int lane, int mb, int cc) {
+  const int g = lane >> 4, jj = lane & 15;
+  const int row = 32 * (g >> 1) + 8 * cc + (jj >> 2);
+  const int dim = 32 * mb + 16 * (g & 1) + 4 * (jj & 3);
+  const uint8_t* p = region + row * kRowBytes + 2 * dim;
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * kRowBytes));
+  bf16x8 r;
+  __builtin_memcpy(&r, &lo, 8);
+  __builtin_memcpy(reinterpret_cast<char*>(&r) + 8, &hi, 8);
+  return r;
 }
 
 template <int LV, bool kQuantP, bool kSame, bool kPacked>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dec_values_kernel(DecodeArgs a) {
-  __shared__ __attribute__((aligned(128))) uint8_t lds[kPacked ? kDecWaves * kVStageBytes : 16];
+  __shared__ __attribute__((aligned(128))) uint8_t lds[kDecWaves * kStageBytes];
   const int lane = threadIdx.x & 63;
   const int n = lane & 31;
   const int half = lane >> 5;
   const int wave_id = dec_wave_id();
   if (wave_id >= a.B * a.Hkv * a.n_rb * a.nsplit) return;
   const DecWave w = dec_wave(a, wave_id, n);
-  uint8_t* const region = lds + (threadIdx.x >> 6) * (kPacked ? kVStageBytes : 0);
+  uint8_t* const region = lds + (threadIdx.x >> 6) * kStageBytes;
+  const RowSrc vsrc = v_source<kPacked>(a, w);
+
+  const float* srow = a.s + w.row * a.s_stride + 64 * half;
+  // S of chunk c (keys 64 half + 8 c .. + 7 of tile t) in a ring of four chunks
+  float sv[4][8];
+  // (unconditional loads: lanes without a row read a row of this KV head and drop it)
+  auto load_s = [&](int t, int c, int slot) {
+    const float* sp = srow + t * kKeyTile + 8 * c;
+    const u32x4 x0 = ld16(sp), x1 = ld16(sp + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sv[slot][i] = w.live ? __uint_as_float(x0[i]) : -INFINITY;
+      sv[slot][4 + i] = w.live ? __uint_as_float(x1[i]) : -INFINITY;
+    }
+  };
+  auto load_g = [&](int t) {
+    const float2 x = *reinterpret_cast<const float2*>(a.gmx + (w.row * a.ntiles + t) * 2);
+    return w.live ? x : make_float2(-INFINITY, -INFINITY);
+  };
+  // the first tile's lane maxima, V half tile and S chunks are in flight (in the order they
+  // are used) while the maximum below is read
+  RowsRaw<kPacked> vr;
+  float2 gnext = make_float2(-INFINITY, -INFINITY);
+  if (w.t_lo < w.t_hi) {
+    gnext = load_g(w.t_lo);
+    load_rows<kPacked>(vsrc, a.Lk, w.t_lo, 0, lane, vr);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) load_s(w.t_lo, c, c);
+  }
 
   // running maximum before the split: the largest split maximum of the splits before it
   // (raw scores; c1 > 0 and rounding is monotonic, so scaling the maximum once equals the
-  // maximum of the c1-scaled tile maxima)
-  float ms = -INFINITY;
-  if (w.live) {
-    for (int jj = half; jj < w.j; jj += 2) ms = fmaxf(ms, a.smx[w.row * a.nsplit + jj]);
+  // maximum of the c1-scaled tile maxima).  The 64 lanes read 64 splits of every live row
+  // at a time, two such chunks per round (all their loads in flight together), then each
+  // row's maximum is reduced across the wave.
+  float m_run = -INFINITY;
+  {
+    const int nrows = min(a.G * a.pb, a.G * (a.Lq - w.pmin));  // live columns 0 .. nrows - 1
+    float mr[32];
+#pragma unroll
+    for (int r = 0; r < 32; ++r) mr[r] = -INFINITY;
+    const int64_t row0 = (static_cast<int64_t>(w.b) * a.Hq + w.kvh * a.G) * a.Lq + w.pmin;
+    for (int j0 = 0; j0 < w.j; j0 += 128) {
+      float x[2][32];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int jj = j0 + 64 * q + lane;
+#pragma unroll
+        for (int r = 0; r < 32; ++r) {
+          // column r: head r % G, position pmin + r / G
+          x[q][r] = -INFINITY;
+          if (r < nrows && jj < w.j)
+            x[q][r] = a.smx[(row0 + static_cast<int64_t>(r % a.G) * a.Lq + r / a.G) * a.nsplit + jj];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 32; ++r) mr[r] = fmaxf(mr[r], fmaxf(x[0][r], x[1][r]));
+    }
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      if (r < nrows) {
+        const float m = wave_max_f32(mr[r]);
+        if (n == r) m_run = m * a.c1;
+      }
+    }
   }
-  float m_run = halves_max(ms) * a.c1;
   float l_run = 0.0f;
   floatx16 acc[4];
 #pragma unroll
@@ -334,49 +412,10 @@ void dec_values_kernel(DecodeArgs a) {
     const uint32_t one2 = 0x3F803F80u;
     __builtin_memcpy(&ones2, &one2, 4);
   }
-  const float* srow = a.s + w.row * a.s_stride + 64 * half;
-  const uint16_t* vbase = a.vt + w.b * a.v_sb + w.kvh * a.v_sh + static_cast<int64_t>(n) * a.v_sd + 64 * half;
-
-  // S of chunk c (keys 64 half + 8 c .. + 7 of tile t) in a ring of four chunks and, with
-  // bf16 V, its V^T fragments in a ring of two (the register budget of two waves per SIMD)
-  float sv[4][8];
-  bf16x8 vv[2][4];
-  auto load_s = [&](int t, int c, int slot) {
-    if (w.live) {
-      const float* sp = srow + t * kKeyTile + 8 * c;
-      const u32x4 x0 = ld_nt(sp), x1 = ld_nt(sp + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sv[slot][i] = __uint_as_float(x0[i]);
-        sv[slot][4 + i] = __uint_as_float(x1[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) sv[slot][i] = -INFINITY;
-    }
-  };
-  auto load_v = [&](int t, int c, int slot) {
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-      vv[slot][mb] = as_bf16x8(ld_nt(vbase + static_cast<int64_t>(32 * mb) * a.v_sd + t * kKeyTile + 8 * c));
-  };
-  VRaw vr;
-  if (w.t_lo < w.t_hi) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) load_s(w.t_lo, c, c);
-    if constexpr (kPacked) {
-      load_v_raw(a, w, w.t_lo, 0, lane, vr);
-    } else {
-      load_v(w.t_lo, 0, 0);
-      load_v(w.t_lo, 1, 1);
-    }
-  }
-  float2 gnext = make_float2(-INFINITY, -INFINITY);
-  if (w.live && w.t_lo < w.t_hi) gnext = *reinterpret_cast<const float2*>(a.gmx + (w.row * a.ntiles + w.t_lo) * 2);
-
   for (int t = w.t_lo; t < w.t_hi; ++t) {
+    const int tn = min(t + 1, w.t_hi - 1);  // the next tile (past the last: a repeat, unused)
     const float2 g = gnext;
-    if (w.live && t + 1 < w.t_hi) gnext = *reinterpret_cast<const float2*>(a.gmx + (w.row * a.ntiles + t + 1) * 2);
+    gnext = load_g(tn);
     // the prefill kernel's tile recurrence: g.x, g.y are the lane maxima of the two halves
     const float mx = half ? g.y : g.x;
     const float mx_row = fmaxf(g.x, g.y);
@@ -399,32 +438,22 @@ void dec_values_kernel(DecodeArgs a) {
     for (int c = 0; c < 8; ++c) {
       const int slot = c & 3;
       bf16x8 va[4];
-      if constexpr (kPacked) {
-        if ((c & 3) == 0) {
-          // unpack half tile c / 4 (the previous one's fragment reads were issued before)
-          wave_lds_order();
-          store_v_stage(vr, lane, region);
-          wave_lds_order();
-          const int s_next = (c >> 2) ^ 1;
-          const int t_next = (c >> 2) ? t + 1 : t;
-          if (t_next < w.t_hi) load_v_raw(a, w, t_next, s_next, lane, vr);
-        }
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-          va[mb] = *reinterpret_cast<const bf16x8*>(region + vrow_byte(32 * mb + n) + 64 * half + 16 * (c & 3));
-      } else {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) va[mb] = vv[c & 1][mb];
-        // the slot takes chunk c + 2 (of this tile or the next)
-        if (c < 6) load_v(t, c + 2, c & 1);
-        else if (t + 1 < w.t_hi) load_v(t + 1, c - 6, c & 1);
+      if ((c & 3) == 0) {
+        // stage half tile c / 4 (the previous one's fragment reads were issued before), then
+        // load the next one
+        wave_lds_order();
+        store_rows<kPacked>(vr, lane, region);
+        if ((t + 1) * kKeyTile > a.Lk) zero_tail_rows(a.Lk, t, c >> 2, lane, region);
+        wave_lds_order();
+        load_rows<kPacked>(vsrc, a.Lk, (c >> 2) ? tn : t, (c >> 2) ^ 1, lane, vr);
       }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) va[mb] = vt_fragment(region, lane, mb, c & 3);
       float pc[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[slot][j], a.c1, nm));
       // the S slot takes chunk c + 4 (of this tile or the next)
-      if (c < 4) load_s(t, c + 4, slot);
-      else if (t + 1 < w.t_hi) load_s(t + 1, c - 4, slot);
+      load_s(c < 4 ? t : tn, (c + 4) & 7, slot);
       if (!(kQuantP && kSame)) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) rowsum += pc[j];

@@ -694,8 +694,8 @@ int64_t faq_attention_decode_workspace(int B, int Hq, int Lq, int Lk, int nsplit
 }
 
 int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
-                         int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
-                         int64_t v_sd, const faq_hif4_kv* kp, const faq_hif4_kv* vp, void* o, int o_dtype,
+                         int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* v, int64_t v_sb, int64_t v_sh,
+                         int64_t v_sl, const faq_hif4_kv* kp, const faq_hif4_kv* vp, void* o, int o_dtype,
                          int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int causal,
                          float scale, int quant_p, int p_levels, int norm_same, float* row_den, int nsplit,
                          void* workspace, int64_t workspace_bytes, faq_stream_t stream) {
@@ -703,7 +703,7 @@ int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t 
   const bool packed = kp != nullptr;
   if ((kp == nullptr) != (vp == nullptr)) return fail(FAQ_EINVAL, "%s: K and V are both packed or both bf16", who);
   if (!q || !o) return fail(FAQ_EINVAL, "%s: null operand", who);
-  if (packed ? !(kp->codes && kp->meta && vp->codes && vp->meta) : !(k && vt))
+  if (packed ? !(kp->codes && kp->meta && vp->codes && vp->meta) : !(k && v))
     return fail(FAQ_EINVAL, "%s: null operand", who);
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Lq < 0 || Lk < 0) return fail(FAQ_EINVAL, "%s: bad sizes", who);
   if (Hq % Hkv) return fail(FAQ_EINVAL, "query heads must be divisible by key/value heads");
@@ -722,10 +722,9 @@ int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t 
       return fail(FAQ_EINVAL, "%s: packed codes must be 16-byte and meta 8-byte aligned", who);
     if (kp->sb < 0 || kp->sh < 0 || vp->sb < 0 || vp->sh < 0) return fail(FAQ_EINVAL, "%s: negative row strides", who);
   } else {
-    if (!aligned16(k) || !aligned16(vt)) return fail(FAQ_EINVAL, "%s: pointers must be 16-byte aligned", who);
-    if ((k_sb | k_sh | k_sl | v_sb | v_sh | v_sd) & 7)
+    if (!aligned16(k) || !aligned16(v)) return fail(FAQ_EINVAL, "%s: pointers must be 16-byte aligned", who);
+    if ((k_sb | k_sh | k_sl | v_sb | v_sh | v_sl) & 7)
       return fail(FAQ_EINVAL, "%s: operand strides must be multiples of 8 elements", who);
-    if (v_sd < static_cast<int64_t>(L.ntiles) * 128) return fail(FAQ_EINVAL, "%s: v_sd must be >= 128 * ceil(Lk / 128)", who);
   }
   if (B == 0 || Lq == 0) return FAQ_OK;
   if (!workspace || !aligned16(workspace)) return fail(FAQ_EINVAL, "%s: null or misaligned workspace", who);
@@ -752,10 +751,10 @@ int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t 
     a.k_sb = k_sb;
     a.k_sh = k_sh;
     a.k_sl = k_sl;
-    a.vt = vt;
+    a.v = v;
     a.v_sb = v_sb;
     a.v_sh = v_sh;
-    a.v_sd = v_sd;
+    a.v_sl = v_sl;
   }
   a.B = B;
   a.Hq = Hq;

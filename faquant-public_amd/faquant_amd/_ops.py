@@ -543,10 +543,6 @@ def attention_fwd(
     if out.stride(3) != 1:
         raise ValueError("attention output needs a unit stride along head_dim")
     nsplit = _split_count(B, Hq, Hkv, Lq, int(key_length), _device_cus(q.device)) if split is None else int(split)
-    if split is None and nsplit > 1 and not out_levels and opts is None and decode_shaped(Hq, Hkv, Lq):
-        # decode: the query heads of a KV head together, K read once
-        return attention_decode(q, key_length, causal=causal, scale=scale, quant_p=quant_p, p_levels=p_levels,
-                                norm_same=norm_same, out=out, k=k, vt=vt, row_den=row_den)
     if nsplit > 1 and not out_levels:
         ws_bytes = lib.faq_attention_split_workspace(B, Hq, Lq, int(key_length), nsplit)
         ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
@@ -601,16 +597,17 @@ def attention_decode(
     norm_same: bool,
     out: torch.Tensor,
     k: torch.Tensor | None = None,
-    vt: torch.Tensor | None = None,
+    v: torch.Tensor | None = None,
     packed: tuple[PackedHiF4KV, PackedHiF4KV] | None = None,
     row_den: torch.Tensor | None = None,
     split: int | None = None,
 ) -> torch.Tensor:
     """Decode-shaped attention (faq_attention_decode): q [B, Hq, Lq, 128] bf16 against bf16
-    k [B, Hkv, Lk, 128] and vt [B, Hkv, 128, Lpad], or against ``packed`` = (K cache, V cache)
-    of PackedHiF4KV; masks none or bottom-right causal.  Same results as attention_fwd's
-    split path with the same ``split``, bitwise, for either form of K/V."""
-    tensors = (q, out, row_den) + ((k, vt) if packed is None else (packed[0].codes, packed[1].codes))
+    k and v [B, Hkv, Lk, 128] (natural rows, any strides with a unit last stride), or against
+    ``packed`` = (K cache, V cache) of PackedHiF4KV; masks none or bottom-right causal.  Same
+    results as attention_fwd's split path with the same ``split``, bitwise, for either form
+    of K/V."""
+    tensors = (q, out, row_den) + ((k, v) if packed is None else (packed[0].codes, packed[1].codes))
     _lib.require_device(*tensors)
     lib = _lib.load()
     B, Hq, Lq, D = q.shape
@@ -620,10 +617,12 @@ def attention_decode(
         raise ValueError("attention output must be fp32 or bf16 with a unit stride along head_dim")
     Lk = int(key_length)
     if packed is None:
-        if k is None or vt is None or k.dtype != torch.bfloat16 or vt.dtype != torch.bfloat16:
-            raise TypeError("bf16 k and vt are required without packed K/V")
+        if k is None or v is None or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+            raise TypeError("bf16 k and v are required without packed K/V")
+        if k.shape[-2] < Lk or v.shape[-2] < Lk or k.shape[-1] != HEAD_DIM or v.shape[-1] != HEAD_DIM:
+            raise ValueError("k and v must be [B, Hkv, >= key_length, 128]")
         Hkv = k.shape[1]
-        kargs = (k.data_ptr(), *_bhld_strides(k), vt.data_ptr(), *_bhld_strides(vt))
+        kargs = (k.data_ptr(), *_bhld_strides(k), v.data_ptr(), *_bhld_strides(v))
         kp = vp = None
     else:
         kc, vc = packed

@@ -293,33 +293,40 @@ def _key_operand(module, key: torch.Tensor, *, enabled: bool, query_length: int,
 
 
 def _value_operand(module, value: torch.Tensor, *, enabled: bool, query_length: int, levels: str) -> torch.Tensor:
-    """Transposed bf16 V operand [B, Hkv, 128, Lpad] (keys >= Lk zero); with V quantization
-    ``faquant_v_matmul_qdq_cache`` is its [B, Hkv, Lk, 128] view and a decode step
-    quantizes only the appended position (sfa:243-289)."""
+    """bf16 V operand [B, Hkv, Lk, 128] in natural rows; with V quantization it doubles as
+    the decode QDQ cache ``faquant_v_matmul_qdq_cache`` (sfa:243-289), a capacity-padded
+    buffer where a decode step quantizes only the appended position.  The prefill kernels
+    take a transposed copy (transposed_values)."""
     name = "faquant_v_matmul_qdq_cache"
     states = getattr(module, _KV_STATE, None) or {}
     if not enabled:
         setattr(module, name, None)
         states.pop("v", None)
         setattr(module, _KV_STATE, states)
-        return _ops.operand_prep_vt(value, levels=None)
+        return value
     B, H, L, D = value.shape
     st = states.get("v")
     if _append_allowed(module, name, st, value, query_length):
-        vt = st["buf"]
-        if L > vt.shape[-1]:
-            grown = torch.zeros((B, H, D, _cache_capacity(L + _KV_GROWTH)), device=value.device, dtype=torch.bfloat16)
-            grown[..., : L - 1].copy_(vt[..., : L - 1])
-            vt = grown
-        tail = _ops.operand_prep_vt(value[:, :, L - 1 :], levels=levels)
-        vt[..., L - 1 : L].copy_(tail[..., :1])
+        buf = st["buf"]
+        if L > buf.shape[2]:
+            grown = torch.empty((B, H, _cache_capacity(L + _KV_GROWTH), D), device=value.device, dtype=torch.bfloat16)
+            grown[:, :, : L - 1].copy_(buf[:, :, : L - 1])
+            buf = grown
+        _ops.operand_prep(value[:, :, L - 1 :], levels=levels, out=buf[:, :, L - 1 : L])
     else:
-        vt = _ops.operand_prep_vt(value, levels=levels)
-    view = vt.transpose(-1, -2)[..., :L, :]
-    states["v"] = dict(buf=vt, view=view, length=L, device=value.device, dtype=value.dtype, lead=(B, H))
+        buf = torch.empty((B, H, _cache_capacity(L), D), device=value.device, dtype=torch.bfloat16)
+        _ops.operand_prep(value, levels=levels, out=buf[:, :, :L])
+    view = buf[:, :, :L]
+    states["v"] = dict(buf=buf, view=view, length=L, device=value.device, dtype=value.dtype, lead=(B, H))
     setattr(module, _KV_STATE, states)
     setattr(module, name, view)
-    return vt
+    return view
+
+
+def transposed_values(v: torch.Tensor) -> torch.Tensor:
+    """V^T [B, H, 128, Lpad] (zero padded) of bf16 V values, the prefill kernels' operand (an
+    exact copy: HiF4 values are bf16, and unquantized V must be bf16)."""
+    return _ops.operand_prep_vt(v, levels=None)
 
 
 def _packed_cache_enabled(module, qk_quant: bool, pv_quant: bool) -> bool:
@@ -366,24 +373,27 @@ def kv_operands_and_attend(module, q_op: torch.Tensor, key: torch.Tensor, value:
     causal rule) run on the packed rows; any other call takes bf16 operands of the same
     values, so both cache forms give the same bits."""
     key_length = key.shape[2]
+    B, Hq, Hkv = q_op.shape[0], q_op.shape[1], key.shape[1]
+    plain = not (attn.get("ranges") is not None or attn.get("softcap") or attn.get("pv_probe") is not None
+                 or attn.get("dense_mask") is not None or attn.get("out_levels"))
+    # decode steps (too few query rows to fill the GPU, all of a KV head's rows in one MFMA
+    # tile, no mask beyond the causal rule) run on the decode kernel: K and V read once
+    decode = (plain and _ops.decode_shaped(Hq, Hkv, query_length)
+              and _ops._split_count(B, Hq, Hkv, query_length, key_length, _ops._device_cus(q_op.device)) > 1)
+    dkw = dict(causal=attn["causal"], scale=attn["scale"], quant_p=attn["quant_p"], p_levels=attn["p_levels"],
+               norm_same=attn["norm_same"], out=attn["out"], row_den=attn.get("row_den"))
     if _packed_cache_enabled(module, qk_quant, pv_quant):
         kp, vp = _packed_operands(module, key, value, query_length=query_length, levels=levels, prep=k_prep)
-        plain = not (attn.get("ranges") is not None or attn.get("softcap") or attn.get("pv_probe") is not None
-                     or attn.get("dense_mask") is not None or attn.get("out_levels"))
-        B, Hq, Hkv = q_op.shape[0], q_op.shape[1], key.shape[1]
-        # the calls attention_fwd would send to the decode kernel (so both cache forms agree)
-        if (plain and _ops.decode_shaped(Hq, Hkv, query_length)
-                and _ops._split_count(B, Hq, Hkv, query_length, key_length, _ops._device_cus(q_op.device)) > 1):
-            return _ops.attention_decode(
-                q_op, key_length, packed=(kp, vp), causal=attn["causal"], scale=attn["scale"],
-                quant_p=attn["quant_p"], p_levels=attn["p_levels"], norm_same=attn["norm_same"], out=attn["out"],
-                row_den=attn.get("row_den"))
+        if decode:
+            return _ops.attention_decode(q_op, key_length, packed=(kp, vp), **dkw)
         k_op, _ = _ops.operand_prep(key, levels=levels["k"], **k_prep)
         vt = _ops.operand_prep_vt(value, levels=levels["v"])
-    else:
-        k_op = _key_operand(module, key, enabled=qk_quant, query_length=query_length, levels=levels["k"], **k_prep)
-        vt = _value_operand(module, value, enabled=pv_quant, query_length=query_length, levels=levels["v"])
-    return _ops.attention_fwd(q_op, k_op, vt, key_length, **attn)
+        return _ops.attention_fwd(q_op, k_op, vt, key_length, **attn)
+    k_op = _key_operand(module, key, enabled=qk_quant, query_length=query_length, levels=levels["k"], **k_prep)
+    v_op = _value_operand(module, value, enabled=pv_quant, query_length=query_length, levels=levels["v"])
+    if decode:
+        return _ops.attention_decode(q_op, key_length, k=k_op, v=v_op, **dkw)
+    return _ops.attention_fwd(q_op, k_op, transposed_values(v_op), key_length, **attn)
 
 
 def simulated_flash_attention_forward(

@@ -325,9 +325,10 @@ int faq_operand_prep_hif4_kv(const void* x, int in_dtype, int64_t sb, int64_t sh
  * Decode-shaped attention (few query rows per KV head, long key ranges): the results of
  * faq_attention_fwd_split with the same nsplit, bitwise, for masks none or bottom-right
  * causal (no opts, no out_levels), at most 32 query heads per KV head.  K and V come either
- * as bf16 K [B, Hkv, Lk, 128] and V^T (k, vt with their strides; v_sd >= 128 ceil(Lk / 128),
- * zero past Lk) or, with kp and vp non-NULL (both), as packed HiF4 rows (k and vt unused);
- * the packed form decodes to the bf16 operands, so both give the same bits.  The query
+ * as bf16 K and V [B, Hkv, Lk, 128] at element strides (natural [key][dim] rows, as a decode
+ * cache grows; not the V^T of faq_attention_fwd) or, with kp and vp non-NULL (both), as
+ * packed HiF4 rows (k and v unused); the packed form decodes to the bf16 operands, so both
+ * give the same bits.  The query
  * heads sharing a KV head are computed together (one pass over each K/V tile for all of
  * them): a scores pass writes S and tile maxima to the workspace, a values pass runs the
  * recurrence per key range, and a combine sums the ranges.  `workspace` is device memory of
@@ -336,8 +337,8 @@ int faq_operand_prep_hif4_kv(const void* x, int in_dtype, int64_t sb, int64_t sh
  */
 int64_t faq_attention_decode_workspace(int B, int Hq, int Lq, int Lk, int nsplit);
 int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
-                         int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* vt, int64_t v_sb, int64_t v_sh,
-                         int64_t v_sd, const faq_hif4_kv* kp, const faq_hif4_kv* vp, void* o, int o_dtype,
+                         int64_t k_sb, int64_t k_sh, int64_t k_sl, const uint16_t* v, int64_t v_sb, int64_t v_sh,
+                         int64_t v_sl, const faq_hif4_kv* kp, const faq_hif4_kv* vp, void* o, int o_dtype,
                          int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int causal,
                          float scale, int quant_p, int p_levels, int norm_same, float* row_den, int nsplit,
                          void* workspace, int64_t workspace_bytes, faq_stream_t stream);

@@ -116,9 +116,10 @@ def _decode_inputs(case, dev):
     v = OQ.bf16_round(g.standard_normal((B, Hkv, Lk, 128), dtype=np.float32))
     qh, _ = _ops.operand_prep(to_dev(q, dev, torch.bfloat16), levels=lv)
     kh, _ = _ops.operand_prep(to_dev(k, dev, torch.bfloat16), levels=lv)
-    vt = _ops.operand_prep_vt(to_dev(v, dev, torch.bfloat16), levels=lv if qp else None)
+    vh, _ = _ops.operand_prep(to_dev(v, dev, torch.bfloat16), levels=lv if qp else None)  # natural rows
+    vt = _ops.operand_prep_vt(to_dev(v, dev, torch.bfloat16), levels=lv if qp else None)  # the split path's V^T
     kw = dict(causal=causal, scale=128**-0.5, quant_p=qp, p_levels=lv, norm_same=mode == "quantized_same")
-    return (q, k, v), (qh, kh, vt), kw
+    return (q, k, v), (qh, kh, vh, vt), kw
 
 
 def _run(fn, case, dev, **extra):
@@ -134,10 +135,10 @@ def test_decode_equals_split_path_bitwise(dev, case):
     from faquant_amd import _ops
 
     B, Hq, Hkv, Lq, Lk, causal, mode, qp, lv, nsplit = case
-    (q, k, v), (qh, kh, vt), kw = _decode_inputs(case, dev)
+    (q, k, v), (qh, kh, vh, vt), kw = _decode_inputs(case, dev)
     print(f"[decode] {case}", flush=True)
     split_o, split_l = _run(lambda **a: _ops.attention_fwd(qh, kh, vt, Lk, split=nsplit, **kw, **a), case, dev)
-    dec_o, dec_l = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, vt=vt, split=nsplit, **kw, **a), case, dev)
+    dec_o, dec_l = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, v=vh, split=nsplit, **kw, **a), case, dev)
     assert torch.equal(dec_o, split_o)
     assert torch.equal(dec_l, split_l)
     if qp:
@@ -154,19 +155,22 @@ def test_decode_equals_split_path_bitwise(dev, case):
         assert_close_attention(dec_o.cpu().numpy(), ref, f"decode {case}")
 
 
-def test_drop_in_routes_decode_steps_to_the_decode_kernel(dev):
-    """attention_fwd without an explicit split sends a decode-shaped call to the decode
-    kernel (its automatic range count), which matches the oracle."""
+def test_drop_in_runs_decode_steps_on_the_decode_kernel(dev):
+    """A decode step through the drop-in (no mask beyond the causal rule) is the decode
+    kernel with its automatic range count, bitwise, and matches the oracle."""
     from faquant_amd import _ops
+    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward
 
     case = (1, 32, 8, 1, 5000, True, "quantized_same", True, "123", None)
-    (q, k, v), (qh, kh, vt), kw = _decode_inputs(case, dev)
+    (q, k, v), (qh, kh, vh, _), kw = _decode_inputs(case, dev)
     assert _ops.decode_shaped(32, 8, 1) and not _ops.decode_shaped(32, 8, 9)
-    auto_o, _ = _run(lambda **a: _ops.attention_fwd(qh, kh, vt, 5000, **kw, **a), case, dev)
+    got, _ = simulated_flash_attention_forward(module(), *(to_dev(a, dev, torch.bfloat16) for a in (q, k, v)), None)
     n = _ops.decode_split_count(1, 8, 5000, _ops._device_cus(qh.device))
-    dec_o, _ = _run(lambda **a: _ops.attention_decode(qh, 5000, k=kh, vt=vt, split=n, **kw, **a), case, dev)
-    assert torch.equal(auto_o, dec_o)
-    assert_close_attention(auto_o.cpu().numpy(), _oracle(q, k, v, causal=True, levels="123"), "routed decode")
+    out = torch.empty((1, 1, 32, 128), device=dev, dtype=torch.bfloat16)
+    _ops.attention_decode(qh, 5000, k=kh, v=vh, split=n, out=out.transpose(1, 2), **kw)
+    assert torch.equal(got, out)
+    ref = _oracle(q, k, v, causal=True, levels="123", dtype="bfloat16")
+    assert_close_attention(got.float().cpu().numpy(), ref, "drop-in decode step")
 
 
 @pytest.mark.parametrize("core", [False, True], ids=["sdpa", "qwen_core"])
