@@ -40,10 +40,11 @@ KERNEL_SOURCES = ("faquant-public_amd/csrc/hif4_attention.hip", "faquant-public_
                   "faquant-public_amd/csrc/hif4_device.h")
 MEASURED_TRAFFIC = {
     # config: (bytes per launch, kernel source sha256 prefix, profile)
-    "qwen8b_32k": (1.686e9, "unmeasured", "profiles/attn_fwd_qwen8b_32k_counters.md"),
-    "qwen32b_16k": (1.098e9, "unmeasured", "profiles/attn_fwd_qwen32b_16k_kernel_trace.md"),
-    "wan480p": (3.426e9, "unmeasured", "profiles/attn_fwd_wan480p_kernel_trace.md"),
-    "wan720p": (5.638e10, "unmeasured", "profiles/attn_fwd_wan720p_kernel_trace.md"),
+    "qwen8b_32k": (1.676e9, "9cbc55ea932e01e9", "profiles/attn_fwd_qwen8b_32k_counters.md"),
+    "qwen8b_8k": (2.141e8, "9cbc55ea932e01e9", "profiles/attn_fwd_qwen8b_8k_kernel_trace.md"),
+    "qwen32b_16k": (1.097e9, "9cbc55ea932e01e9", "profiles/attn_fwd_qwen32b_16k_kernel_trace.md"),
+    "wan480p": (3.367e9, "9cbc55ea932e01e9", "profiles/attn_fwd_wan480p_kernel_trace.md"),
+    "wan720p": (5.617e10, "9cbc55ea932e01e9", "profiles/attn_fwd_wan720p_kernel_trace.md"),
 }
 
 
@@ -299,6 +300,32 @@ def decode_bench(cfg, context: int, steps: int, warmup: int) -> dict:
     }
 
 
+def stream_reference() -> dict:
+    """This device's practical HBM rate for plain streams (torch's copy and sum over 1 GiB of
+    fp32, beyond the 256 MiB last-level cache): the measured reference point beside the
+    8 TB/s specification for the HBM-bound decode kernels."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    n = (1 << 30) // 4
+    x = torch.randn(n, device=dev)
+    y = torch.empty_like(x)
+    res = {}
+    for name, fn, nbytes in (("copy", lambda: y.copy_(x), 8 * n), ("sum", lambda: x.sum(), 4 * n)):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(20):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / 20
+        res[name] = {"bytes": nbytes, "us": round(ms * 1e3, 1), "gbps": round(nbytes / ms / 1e6, 1)}
+    return {"stream_reference": "1 GiB fp32 through torch copy_ (read + write) and sum (read)", **res}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -312,6 +339,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode", type=int, default=0, metavar="CONTEXT",
                     help="time one decode step over CONTEXT cached keys of --config's heads instead")
+    ap.add_argument("--stream-reference", action="store_true",
+                    help="measure only the device's practical HBM stream rate (torch copy and sum over 1 GiB)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE scaling)")
     args = ap.parse_args()
@@ -323,6 +352,10 @@ def main():
     import torch
 
     from faquant_amd import _ops
+
+    if args.stream_reference:
+        print(json.dumps(stream_reference()), flush=True)
+        return
 
     if args.decode:
         print(json.dumps(decode_bench(CONFIGS[args.config], args.decode, args.steps, args.warmup)), flush=True)
