@@ -300,6 +300,65 @@ def decode_bench(cfg, context: int, steps: int, warmup: int) -> dict:
     }
 
 
+# Linear layers of one Wan2.2-A14B DiT block (wan22_hif4.py BLOCK_LINEARS): (name, in, out)
+WAN_BLOCK_LINEARS = (
+    ("self_attn.q", 5120, 5120), ("self_attn.k", 5120, 5120), ("self_attn.v", 5120, 5120),
+    ("self_attn.o", 5120, 5120), ("cross_attn.q", 5120, 5120), ("cross_attn.o", 5120, 5120),
+    ("ffn.0", 5120, 13824), ("ffn.2", 13824, 5120),
+)
+
+
+def linear_bench(tokens: int, steps: int, warmup: int) -> dict:
+    """HiF4 W4A4 Linear (HiF4Linear: one HIP launch for the input QDQ, then the library bf16
+    GEMM on the HiF4-exact operands) at the Wan2.2 DiT block shapes over `tokens` rows: per
+    layer the QDQ and the GEMM timed with HIP events, the GEMM against the 2.5 PFLOP/s dense
+    bf16 peak and the QDQ against the 8 TB/s HBM peak (it reads and writes the activations
+    once).  The cross-attention K/V projections act on the text context, not on `tokens`."""
+    import torch
+    from torch.nn import functional as F
+
+    from faquant_amd import _ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(2)
+    layers = []
+    for name, k, n in WAN_BLOCK_LINEARS:
+        x = torch.randn((tokens, k), device=dev, generator=gen).to(torch.bfloat16)
+        w = _ops.act_qdq_rows(torch.randn((n, k), device=dev, generator=gen).to(torch.bfloat16) * 0.02, levels="123")
+        qx = torch.empty_like(x)
+
+        def timed(fn):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(steps):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / steps
+
+        q_ms = timed(lambda: _ops.act_qdq_rows(x, levels="123", out=qx))
+        g_ms = timed(lambda: F.linear(qx, w))
+        flops = 2.0 * tokens * k * n
+        qbytes = 2 * 2 * tokens * k
+        layers.append({"layer": name, "in": k, "out": n, "qdq_us": round(q_ms * 1e3, 1),
+                       "qdq_hbm_frac": round(qbytes / (q_ms * 1e-3) / (HBM_PEAK_GBPS * 1e9), 3),
+                       "gemm_us": round(g_ms * 1e3, 1), "gemm_tflops": round(flops / (g_ms * 1e-3) / 1e12, 1),
+                       "gemm_frac": round(flops / (g_ms * 1e-3) / (MFMA_BF16_PEAK_TFLOPS * 1e12), 3),
+                       "qdq_share": round(q_ms / (q_ms + g_ms), 3)})
+        del x, w, qx
+    tq = sum(l["qdq_us"] for l in layers)
+    tg = sum(l["gemm_us"] for l in layers)
+    fl = sum(2.0 * tokens * l["in"] * l["out"] for l in layers)
+    return {"metric": "HiF4 W4A4 Linear (Wan2.2 DiT block shapes): input QDQ + bf16 GEMM, 1 GPU",
+            "tokens": tokens, "steps": steps, "warmup": warmup, "layers": layers,
+            "block": {"qdq_us": round(tq, 1), "gemm_us": round(tg, 1), "qdq_share": round(tq / (tq + tg), 3),
+                      "tflops": round(fl / ((tq + tg) * 1e-6) / 1e12, 1),
+                      "frac": round(fl / ((tq + tg) * 1e-6) / (MFMA_BF16_PEAK_TFLOPS * 1e12), 3)}}
+
+
 def stream_reference() -> dict:
     """This device's practical HBM rate for plain streams (torch's copy and sum over 1 GiB of
     fp32, beyond the 256 MiB last-level cache): the measured reference point beside the
@@ -339,6 +398,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode", type=int, default=0, metavar="CONTEXT",
                     help="time one decode step over CONTEXT cached keys of --config's heads instead")
+    ap.add_argument("--linear", type=int, default=0, metavar="TOKENS",
+                    help="time the HiF4 W4A4 Linear at the Wan2.2 DiT block shapes over TOKENS rows instead")
     ap.add_argument("--stream-reference", action="store_true",
                     help="measure only the device's practical HBM stream rate (torch copy and sum over 1 GiB)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -352,6 +413,10 @@ def main():
     import torch
 
     from faquant_amd import _ops
+
+    if args.linear:
+        print(json.dumps(linear_bench(args.linear, args.steps, args.warmup)), flush=True)
+        return
 
     if args.stream_reference:
         print(json.dumps(stream_reference()), flush=True)
