@@ -314,7 +314,10 @@ typedef struct faq_hif4_kv {
  * instead of bf16: positions 0..L-1 of x [B, H, L, 128] go to rows 0..L-1 of (b, h), rows
  * b * p_sb + h * p_sh + l.  The same prologue (key offset, Smooth-QK, Hadamard, one cast to
  * round_dtype) and the same quantizer, so decoding gives bitwise faq_operand_prep's bf16
- * output.  Rows are token-local: appending a decode position packs one row.
+ * output.  Rows are token-local: appending a decode position packs one row.  Replaces the
+ * K/V QDQ of src/faquant/simulated_flash_attention.py:592-611 (with the qwen3.py:97-136
+ * prologue) where its result is kept as a decode cache (sfa:243-289), stored in the
+ * compact form of hif4.py:67-79.
  */
 int faq_operand_prep_hif4_kv(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
                              const float* key_offset, int64_t off_sh, const float* smooth, int64_t smooth_sh,
@@ -333,7 +336,9 @@ int faq_operand_prep_hif4_kv(const void* x, int in_dtype, int64_t sb, int64_t sh
  * them): a scores pass writes S and tile maxima to the workspace, a values pass runs the
  * recurrence per key range, and a combine sums the ranges.  `workspace` is device memory of
  * at least faq_attention_decode_workspace(B, Hq, Lq, Lk, nsplit) bytes, 16-byte aligned;
- * nsplit is 1..4096.
+ * nsplit is 1..4096.  Replaces, for the decode steps of a KV cache
+ * (src/faquant/simulated_flash_attention.py:243-289), the attention of
+ * simulated_flash_attention.py:457-909.
  */
 int64_t faq_attention_decode_workspace(int B, int Hq, int Lq, int Lk, int nsplit);
 int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_sl, const uint16_t* k,
