@@ -216,6 +216,24 @@ def test_split_count_rule():
     assert _ops._split_count(1, 32, 8, 1, (_ops.SPLIT_MAX_TILES + 1) * 128) == 1
 
 
+def test_decode_split_count_rule():
+    """Key ranges of the decode kernel: about eight waves per CU, one tile per range at
+    short contexts, two tiles per range where four waves per CU remain, no empty range."""
+    from faquant_amd import _ops
+
+    # Qwen3-8B heads (8 KV heads) on 256 CUs
+    assert _ops.decode_split_count(1, 8, 8192) == 64        # 64 tiles, one each
+    assert _ops.decode_split_count(1, 8, 32768) == 128      # 256 tiles, two each: 1024 waves
+    assert _ops.decode_split_count(1, 8, 131072) == 256     # 1024 tiles, four each
+    assert _ops.decode_split_count(1, 8, 5000) == 40        # 40 tiles (ragged last), one each
+    assert _ops.decode_split_count(1, 8, 0) == 1
+    for b, lk in ((1, 300), (4, 32768), (32, 131072), (1, 2_000_000)):
+        n = _ops.decode_split_count(b, 8, lk)
+        tiles = -(-lk // 128)
+        tps = -(-tiles // n)
+        assert 1 <= n <= 4096 and (n - 1) * tps < tiles  # every range holds a tile
+
+
 def test_unquantized_fp32_matmuls_are_refused():
     """Without QK (PV) quantization the reference multiplies the fp32 inputs themselves
     (sfa:723-724, 848-850); the kernel multiplies bf16 operands, so fp32 Q/K (V) with that
