@@ -262,10 +262,12 @@ def decode_bench(cfg, context: int, steps: int, warmup: int) -> dict:
     cus = _ops._device_cus(dev)
     n_split = _ops._split_count(B, Hq, Hkv, 1, L, cus)
     n_dec = _ops.decode_split_count(B, Hkv, L, cus)
+    n_dec_packed = _ops.decode_split_count(B, Hkv, L, cus, packed=True)
     paths = {
         "split_path_bf16": (lambda: _ops.attention_fwd(qh, kh, vt, L, split=n_split, **kw), 512, n_split),
         "decode_bf16": (lambda: _ops.attention_decode(qh, L, k=kh, v=vh, split=n_dec, **kw), 512, n_dec),
-        "decode_packed_hif4": (lambda: _ops.attention_decode(qh, L, packed=(kc, vc), split=n_dec, **kw), 144, n_dec),
+        "decode_packed_hif4": (lambda: _ops.attention_decode(qh, L, packed=(kc, vc), split=n_dec_packed, **kw), 144,
+                               n_dec_packed),
     }
     res = {}
     for name, (fn, per_key, nsplit) in paths.items():

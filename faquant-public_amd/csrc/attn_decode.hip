@@ -25,7 +25,10 @@
 //           HiF4 P^, l and acc = alpha acc + P^ V (same operations in the same order), and
 //           the partial (acc, l, m) of the split.
 // S costs 8 bytes per live row and key of HBM traffic, against 512 bytes per key of bf16
-// K and V (144 packed), where a second K pass would cost 256 (72).
+// K and V (144 packed), where a second K pass would cost 256 (72).  With at most 4 or 8
+// live columns (a decode step) and P summed as P^, the values pass computes P and P^ in
+// a compact layout (dec_values_compact_kernel) and moves P^ into the MFMA layout through
+// LDS, with the same results.
 //
 // Packed HiF4 K/V (4.5 bits per value): per key row of 128 values, 16 code words (dims
 // 8u .. 8u + 7 in slot (u & 1) 8 + u / 2, dim 8u + i in nibble i as 8 + the signed code: a
@@ -325,6 +328,45 @@ __device__ __forceinline__ bf16x8 vt_fragment(const uint8_t* region, int lane, i
   return r;
 }
 
+// Running maximum before split w.j of column n, c1-scaled: the largest split maximum of
+// the splits before it (raw scores; c1 > 0 and rounding is monotonic, so scaling the
+// maximum once equals the maximum of the c1-scaled tile maxima).  The 64 lanes read 64
+// splits of every live column (at most kCols) at a time, two such chunks per round (all
+// their loads in flight together), then each column's maximum is reduced across the wave.
+template <int kCols>
+__device__ __forceinline__ float running_max_before(const DecodeArgs& a, const DecWave& w, int lane, int n) {
+  float m_run = -INFINITY;
+  const int nrows = min(min(a.G * a.pb, a.G * (a.Lq - w.pmin)), kCols);  // live columns 0 .. nrows - 1
+  float mr[kCols];
+#pragma unroll
+  for (int r = 0; r < kCols; ++r) mr[r] = -INFINITY;
+  const int64_t row0 = (static_cast<int64_t>(w.b) * a.Hq + w.kvh * a.G) * a.Lq + w.pmin;
+  for (int j0 = 0; j0 < w.j; j0 += 128) {
+    float x[2][kCols];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int jj = j0 + 64 * q + lane;
+#pragma unroll
+      for (int r = 0; r < kCols; ++r) {
+        // column r: head r % G, position pmin + r / G
+        x[q][r] = -INFINITY;
+        if (r < nrows && jj < w.j)
+          x[q][r] = a.smx[(row0 + static_cast<int64_t>(r % a.G) * a.Lq + r / a.G) * a.nsplit + jj];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kCols; ++r) mr[r] = fmaxf(mr[r], fmaxf(x[0][r], x[1][r]));
+  }
+#pragma unroll
+  for (int r = 0; r < kCols; ++r) {
+    if (r < nrows) {
+      const float m = wave_max_f32(mr[r]);
+      if (n == r) m_run = m * a.c1;
+    }
+  }
+  return m_run;
+}
+
 template <int LV, bool kQuantP, bool kSame, bool kPacked>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dec_values_kernel(DecodeArgs a) {
@@ -366,42 +408,8 @@ void dec_values_kernel(DecodeArgs a) {
     for (int c = 0; c < 4; ++c) load_s(w.t_lo, c, c);
   }
 
-  // running maximum before the split: the largest split maximum of the splits before it
-  // (raw scores; c1 > 0 and rounding is monotonic, so scaling the maximum once equals the
-  // maximum of the c1-scaled tile maxima).  The 64 lanes read 64 splits of every live row
-  // at a time, two such chunks per round (all their loads in flight together), then each
-  // row's maximum is reduced across the wave.
-  float m_run = -INFINITY;
-  {
-    const int nrows = min(a.G * a.pb, a.G * (a.Lq - w.pmin));  // live columns 0 .. nrows - 1
-    float mr[32];
-#pragma unroll
-    for (int r = 0; r < 32; ++r) mr[r] = -INFINITY;
-    const int64_t row0 = (static_cast<int64_t>(w.b) * a.Hq + w.kvh * a.G) * a.Lq + w.pmin;
-    for (int j0 = 0; j0 < w.j; j0 += 128) {
-      float x[2][32];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int jj = j0 + 64 * q + lane;
-#pragma unroll
-        for (int r = 0; r < 32; ++r) {
-          // column r: head r % G, position pmin + r / G
-          x[q][r] = -INFINITY;
-          if (r < nrows && jj < w.j)
-            x[q][r] = a.smx[(row0 + static_cast<int64_t>(r % a.G) * a.Lq + r / a.G) * a.nsplit + jj];
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 32; ++r) mr[r] = fmaxf(mr[r], fmaxf(x[0][r], x[1][r]));
-    }
-#pragma unroll
-    for (int r = 0; r < 32; ++r) {
-      if (r < nrows) {
-        const float m = wave_max_f32(mr[r]);
-        if (n == r) m_run = m * a.c1;
-      }
-    }
-  }
+  // running maximum before the split (the first tile's loads fly meanwhile)
+  float m_run = running_max_before<32>(a, w, lane, n);
   float l_run = 0.0f;
   floatx16 acc[4];
 #pragma unroll
@@ -504,6 +512,166 @@ void dec_values_kernel(DecodeArgs a) {
   }
 }
 
+// Values pass for at most kCols = 4 or 8 live columns (G x query positions <= kCols: a
+// decode step of up to eight heads per KV head), P quantized and summed as P^ (the
+// quantized-same normalizer).  The recurrence of the full values pass, with P and P^
+// computed in a compact layout: unit u = l + 64 i (i < kCols / 4) of lane l holds the 8
+// keys 64 h + 8 c .. + 7 of column u / 16 (h = (u / 8) & 1, c = u & 7), kCols / 4 pquant8
+// per lane and tile instead of eight for 32 columns of which 32 - kCols are empty.  The
+// P^ chunks go through LDS into the PV B operand layout of the full pass (lane (n, half),
+// chunk c), where the row sum and PV run as there, so every output bit is the same.
+template <int LV, bool kPacked, int kCols>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void dec_values_compact_kernel(DecodeArgs a) {
+  static_assert(kCols == 4 || kCols == 8, "compact columns");
+  constexpr int kUnits = kCols / 4;                   // compact units per lane
+  constexpr int kRegion = kStageBytes + kCols * 256;  // V half tile, then 16 kCols P^ chunks
+  __shared__ __attribute__((aligned(128))) uint8_t lds[kDecWaves * kRegion];
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31;
+  const int half = lane >> 5;
+  const int wave_id = dec_wave_id();
+  if (wave_id >= a.B * a.Hkv * a.n_rb * a.nsplit) return;
+  const DecWave w = dec_wave(a, wave_id, n);
+  uint8_t* const region = lds + (threadIdx.x >> 6) * kRegion;
+  uint8_t* const pslots = region + kStageBytes;
+  const RowSrc vsrc = v_source<kPacked>(a, w);
+
+  // this lane's compact units: columns cr + 4 i, key half ch, chunk cc
+  const int cr = lane >> 4, ch = (lane >> 3) & 1, cc = lane & 7;
+  bool clive[kUnits];
+  const float* sc[kUnits];
+#pragma unroll
+  for (int i = 0; i < kUnits; ++i) {
+    const DecWave wc = dec_wave(a, wave_id, cr + 4 * i);
+    clive[i] = wc.live;
+    sc[i] = a.s + wc.row * a.s_stride + 64 * ch + 8 * cc;
+  }
+  auto load_sc = [&](int t, float (&x)[kUnits][8]) {
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      const u32x4 x0 = ld16(sc[u] + t * kKeyTile), x1 = ld16(sc[u] + t * kKeyTile + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[u][i] = clive[u] ? __uint_as_float(x0[i]) : -INFINITY;
+        x[u][4 + i] = clive[u] ? __uint_as_float(x1[i]) : -INFINITY;
+      }
+    }
+  };
+  auto load_g = [&](int t) {
+    const float2 x = *reinterpret_cast<const float2*>(a.gmx + (w.row * a.ntiles + t) * 2);
+    return w.live ? x : make_float2(-INFINITY, -INFINITY);
+  };
+  RowsRaw<kPacked> vr;
+  float2 gnext = make_float2(-INFINITY, -INFINITY);
+  float snext[kUnits][8];
+  if (w.t_lo < w.t_hi) {
+    gnext = load_g(w.t_lo);
+    load_rows<kPacked>(vsrc, a.Lk, w.t_lo, 0, lane, vr);
+    load_sc(w.t_lo, snext);
+  }
+  float m_run = running_max_before<kCols>(a, w, lane, n);
+  float l_run = 0.0f;
+  floatx16 acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = floatx16{};
+  bf16x2_t ones2;
+  {
+    const uint32_t one2 = 0x3F803F80u;
+    __builtin_memcpy(&ones2, &one2, 4);
+  }
+  for (int t = w.t_lo; t < w.t_hi; ++t) {
+    const int tn = min(t + 1, w.t_hi - 1);  // the next tile (past the last: a repeat, unused)
+    const float2 g = gnext;
+    gnext = load_g(tn);
+    float sx[kUnits][8];
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sx[u][j] = snext[u][j];
+    load_sc(tn, snext);
+    // the full pass's tile recurrence, per column n
+    const float mx_row = fmaxf(g.x, g.y);
+    const float m_new = fmaxf(m_run, mx_row * a.c1);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float nm = -m_use;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    if (__ballot(alpha != 1.0f) != 0) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
+      l_run *= alpha;
+    }
+    wave_lds_order();  // the previous tile's chunk reads are issued
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      // P and P^ of this unit's chunk, with its column's offset and group maximum
+      const int col = cr + 4 * u;
+      const float nmc = __shfl(nm, col, 64);
+      const float gx = __shfl(g.x, col, 64), gy = __shfl(g.y, col, 64);
+      const PQuant pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(ch ? gy : gx, a.c1, nmc)));
+      float pc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sx[u][j], a.c1, nmc));
+      pquant8<LV>(pc, pq);
+      *reinterpret_cast<bf16x8*>(pslots + (lane + 64 * u) * 16) = pack8<true>(pc);
+    }
+    wave_lds_order();
+    // the PV B operand of lane (n, half), chunk c: column n's chunk (zero past the compact
+    // columns), and the row sum over it in the full pass's order
+    bf16x8 pb[8];
+    float rowsum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(pslots + (16 * (n & (kCols - 1)) + 8 * half + c) * 16);
+      pb[c] = n < kCols ? x : bf16x8{};
+      uint32_t wv[4];
+      __builtin_memcpy(wv, &pb[c], 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bf16x2_t pr;
+        __builtin_memcpy(&pr, &wv[i], 4);
+        rowsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, rowsum, false);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if ((c & 3) == 0) {
+        // stage half tile c / 4 (the previous one's fragment reads were issued before), then
+        // load the next one
+        wave_lds_order();
+        store_rows<kPacked>(vr, lane, region);
+        if ((t + 1) * kKeyTile > a.Lk) zero_tail_rows(a.Lk, t, c >> 2, lane, region);
+        wave_lds_order();
+        load_rows<kPacked>(vsrc, a.Lk, (c >> 2) ? tn : t, (c >> 2) ^ 1, lane, vr);
+      }
+      bf16x8 va[4];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) va[mb] = vt_fragment(region, lane, mb, c & 3);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma32(va[mb], pb[c], acc[mb]);
+    }
+    l_run += halves_sum(rowsum);
+  }
+
+  if (w.live) {
+    float* po = a.part_o + (static_cast<int64_t>(w.j) * a.rows_total + w.row) * kDim;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<float4*>(po + 32 * mb + 8 * j + 4 * half) =
+            make_float4(acc[mb][4 * j], acc[mb][4 * j + 1], acc[mb][4 * j + 2], acc[mb][4 * j + 3]);
+    if (half == 0) {
+      float* lm = a.part_lm + (static_cast<int64_t>(w.j) * a.rows_total + w.row) * 2;
+      lm[0] = l_run;
+      lm[1] = m_run;
+    }
+  }
+}
+
 template <int LV, bool kQuantP, bool kSame>
 void launch_values(const DecodeArgs& a, int packed, dim3 grid, hipStream_t st) {
   if (packed) hipLaunchKernelGGL((dec_values_kernel<LV, kQuantP, kSame, true>), grid, dim3(256), 0, st, a);
@@ -512,6 +680,16 @@ void launch_values(const DecodeArgs& a, int packed, dim3 grid, hipStream_t st) {
 
 template <int LV>
 void launch_values_lv(const DecodeArgs& a, int packed, int quant_p, int same, dim3 grid, hipStream_t st) {
+  if (quant_p && same && a.G * a.Lq <= 4) {
+    if (packed) hipLaunchKernelGGL((dec_values_compact_kernel<LV, true, 4>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((dec_values_compact_kernel<LV, false, 4>), grid, dim3(256), 0, st, a);
+    return;
+  }
+  if (quant_p && same && a.G * a.Lq <= 8) {
+    if (packed) hipLaunchKernelGGL((dec_values_compact_kernel<LV, true, 8>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((dec_values_compact_kernel<LV, false, 8>), grid, dim3(256), 0, st, a);
+    return;
+  }
   if (quant_p && same) launch_values<LV, true, true>(a, packed, grid, st);
   else if (quant_p) launch_values<LV, true, false>(a, packed, grid, st);
   else launch_values<123, false, false>(a, packed, grid, st);

@@ -575,20 +575,21 @@ def decode_shaped(Hq: int, Hkv: int, Lq: int) -> bool:
     return G <= 32 and Lq * G <= 32
 
 
-def decode_split_count(B: int, Hkv: int, Lk: int, cus: int = 256) -> int:
+def decode_split_count(B: int, Hkv: int, Lk: int, cus: int = 256, packed: bool = False) -> int:
     """Key ranges of faq_attention_decode: about eight waves per CU (two per SIMD) over all
-    (batch, KV head, range) work, at least one key tile per range, no empty range.  A range
-    of one tile becomes two where that still leaves four waves per CU: the second tile's
-    loads then fly during the first one's work (measured at 32k keys, Qwen3-8B heads:
-    45.7 us against 52.3 us for bf16 K/V, 43.2 against 46.0 packed; at 8k, with two waves
-    per CU left, one tile per range stays faster)."""
+    (batch, KV head, range) work, at least one key tile per range, no empty range.  For
+    bf16 K/V a range of one tile becomes two where that still leaves four waves per CU: the
+    second tile's loads then fly during the first one's work.  Packed K/V (a quarter of the
+    bytes per tile) keep one tile per range.  Measured at 32k keys, Qwen3-8B heads: bf16
+    36.6 us with two tiles per range against 42.7 with one; packed 31.5 us with one against
+    34.3 with two; at 8k, with two waves per CU left, one tile per range stays faster."""
     ntiles = -(-Lk // KEY_TILE)
     if ntiles == 0:
         return 1
     work = max(1, B * Hkv)
     want = max(1, min(ntiles, 4096, -(-8 * cus // work)))
     tps = -(-ntiles // want)
-    if tps == 1 and work * -(-ntiles // 2) >= 4 * cus:
+    if not packed and tps == 1 and work * -(-ntiles // 2) >= 4 * cus:
         tps = 2
     return -(-ntiles // tps)
 
@@ -638,7 +639,7 @@ def attention_decode(
             raise ValueError("the packed K/V caches must hold key_length rows of the same heads")
         kargs = (0, 0, 0, 0, 0, 0, 0, 0)
         kp, vp = kc.descriptor(), vc.descriptor()
-    nsplit = decode_split_count(B, Hkv, Lk, _device_cus(q.device)) if split is None else int(split)
+    nsplit = decode_split_count(B, Hkv, Lk, _device_cus(q.device), packed is not None) if split is None else int(split)
     ws_bytes = lib.faq_attention_decode_workspace(B, Hq, Lq, Lk, nsplit)
     ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
     _lib.check(

@@ -218,7 +218,8 @@ def test_split_count_rule():
 
 def test_decode_split_count_rule():
     """Key ranges of the decode kernel: about eight waves per CU, one tile per range at
-    short contexts, two tiles per range where four waves per CU remain, no empty range."""
+    short contexts, two tiles per range where four waves per CU remain (bf16 K/V), no empty
+    range."""
     from faquant_amd import _ops
 
     # Qwen3-8B heads (8 KV heads) on 256 CUs
@@ -227,6 +228,9 @@ def test_decode_split_count_rule():
     assert _ops.decode_split_count(1, 8, 131072) == 256     # 1024 tiles, four each
     assert _ops.decode_split_count(1, 8, 5000) == 40        # 40 tiles (ragged last), one each
     assert _ops.decode_split_count(1, 8, 0) == 1
+    # packed K/V keep one tile per range
+    assert _ops.decode_split_count(1, 8, 32768, packed=True) == 256
+    assert _ops.decode_split_count(1, 8, 131072, packed=True) == 256
     for b, lk in ((1, 300), (4, 32768), (32, 131072), (1, 2_000_000)):
         n = _ops.decode_split_count(b, 8, lk)
         tiles = -(-lk // 128)

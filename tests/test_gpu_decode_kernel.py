@@ -103,6 +103,8 @@ DECODE_CASES = [
     (1, 2, 1, 1, 300, True, "quantized_same", True, "13", 16),       # more ranges than tiles
     (1, 8, 2, 1, 1, True, "quantized_same", True, "123", 1),         # one key
     (1, 4, 1, 2, 640, True, "quantized_same", False, "123", 5),      # P not quantized
+    (1, 8, 2, 2, 2000, True, "quantized_same", True, "123", 9),      # G 4 x 2 positions: 8 columns
+    (2, 4, 2, 3, 1500, True, "quantized_same", True, "12", 5),       # G 2 x 3 positions: 6 of 8 live
 ]
 
 
