@@ -92,45 +92,67 @@ struct SplitCombineArgs {
 // One workgroup per row.  The split weights w_j = 2^(m_j - M) (0 for an empty split) go to
 // LDS; thread (g, q), g = tid / 32, sums w_j O_j[4q .. 4q + 3] over the splits j = g mod 16
 // in order, eight float4 loads in flight, and the 16 group sums are added in a fixed tree
-// (deterministic results); l is summed the same way.
+// (deterministic results); l is summed the same way.  The first eight O loads of each
+// thread and its first (l, m) are issued before the reductions that need M, so one memory
+// round trip serves up to 128 splits (512 for l and m).
 __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCombineArgs a) {
   __shared__ float wsh[kCombineMaxSplits];
   __shared__ float red[kCombineThreads];
   __shared__ float4 gsum[kCombineGroups][32];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
+  const int g = tid / 32, q = tid % 32;
+  const float4* po = reinterpret_cast<const float4*>(a.part_o + static_cast<int64_t>(row) * kDim) + q;
+  const int64_t js = static_cast<int64_t>(a.rows_total) * (kDim / 4);  // float4 stride of one split
+  float4 v0[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int jj = g + kCombineGroups * u;
+    v0[u] = jj < a.nsplit ? po[static_cast<int64_t>(jj) * js] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  const float2 lm0 = tid < a.nsplit ? *reinterpret_cast<const float2*>(a.part_lm + (static_cast<int64_t>(tid) * a.rows_total + row) * 2)
+                                    : make_float2(0.0f, -INFINITY);
   // M: the maximum over the splits
   float mloc = -INFINITY;
-  for (int j = tid; j < a.nsplit; j += kCombineThreads)
+  if (tid < a.nsplit) mloc = fmaxf(mloc, lm0.y);
+  for (int j = tid + kCombineThreads; j < a.nsplit; j += kCombineThreads)
     mloc = fmaxf(mloc, a.part_lm[(static_cast<int64_t>(j) * a.rows_total + row) * 2 + 1]);
-  red[tid] = mloc;
+  // (a maximum is exact: any reduction order gives the same value)
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, d, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = mloc;
   __syncthreads();
-  for (int d = kCombineThreads / 2; d > 0; d >>= 1) {
-    if (tid < d) red[tid] = fmaxf(red[tid], red[tid + d]);
-    __syncthreads();
-  }
-  const float mmax = red[0];
+  float mmax = red[0];
+#pragma unroll
+  for (int w = 1; w < kCombineThreads / 64; ++w) mmax = fmaxf(mmax, red[w]);
   __syncthreads();
   // weights and the weighted l terms
   float lloc = 0.0f;
   for (int j = tid; j < a.nsplit; j += kCombineThreads) {
     const int64_t r = static_cast<int64_t>(j) * a.rows_total + row;
-    const float lj = a.part_lm[r * 2];
-    const float w = (mmax == -INFINITY || lj == 0.0f) ? 0.0f : __builtin_amdgcn_exp2f(a.part_lm[r * 2 + 1] - mmax);
+    const float2 lm = j == tid ? lm0 : make_float2(a.part_lm[r * 2], a.part_lm[r * 2 + 1]);
+    const float w = (mmax == -INFINITY || lm.x == 0.0f) ? 0.0f : __builtin_amdgcn_exp2f(lm.y - mmax);
     wsh[j] = w;
-    lloc = __builtin_fmaf(w, lj, lloc);
+    lloc = __builtin_fmaf(w, lm.x, lloc);
   }
+  // l: the fixed tree red[i] += red[i + d] for d = 256, 128, ..., 1 (the steps below 64 as
+  // shuffles within the first wave, same pairs)
   red[tid] = lloc;
   __syncthreads();
-  for (int d = kCombineThreads / 2; d > 0; d >>= 1) {
+#pragma unroll
+  for (int d = kCombineThreads / 2; d >= 128; d >>= 1) {
     if (tid < d) red[tid] += red[tid + d];
     __syncthreads();
   }
-  const float l = red[0];
+  if (tid < 64) {
+    float x = red[tid] + red[tid + 64];
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) x += __shfl_down(x, d, 64);
+    if (tid == 0) red[kCombineThreads - 1] = x;
+  }
+  __syncthreads();
+  const float l = red[kCombineThreads - 1];
   // O: splits j = g, g + 16, ... of group g
-  const int g = tid / 32, q = tid % 32;
-  const float4* po = reinterpret_cast<const float4*>(a.part_o + static_cast<int64_t>(row) * kDim) + q;
-  const int64_t js = static_cast<int64_t>(a.rows_total) * (kDim / 4);  // float4 stride of one split
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   auto add = [&](float w, float4 v) {
     acc.x = __builtin_fmaf(w, v.x, acc.x);
@@ -138,7 +160,11 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCom
     acc.z = __builtin_fmaf(w, v.z, acc.z);
     acc.w = __builtin_fmaf(w, v.w, acc.w);
   };
-  int j = g;
+  // the first eight splits of the group from the loads issued at the start
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (g + kCombineGroups * u < a.nsplit) add(wsh[g + kCombineGroups * u], v0[u]);
+  int j = g + 8 * kCombineGroups;
   for (; j + 7 * kCombineGroups < a.nsplit; j += 8 * kCombineGroups) {
     float4 v[8];
 #pragma unroll
@@ -147,9 +173,12 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCom
     for (int u = 0; u < 8; ++u) add(wsh[j + kCombineGroups * u], v[u]);
   }
   for (; j < a.nsplit; j += kCombineGroups) add(wsh[j], po[static_cast<int64_t>(j) * js]);
+  // the fixed tree gsum[g] += gsum[g + d] for d = 8, 4, 2, 1 (the last step, groups 0 and
+  // 1 of the first wave, as a shuffle)
   gsum[g][q] = acc;
   __syncthreads();
-  for (int d = kCombineGroups / 2; d > 0; d >>= 1) {
+#pragma unroll
+  for (int d = kCombineGroups / 2; d >= 2; d >>= 1) {
     if (g < d) {
       const float4 o = gsum[g + d][q];
       float4 m = gsum[g][q];
@@ -161,8 +190,13 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCom
     }
     __syncthreads();
   }
-  if (g == 0) {
-    const float4 sum = gsum[0][q];
+  if (g < 2) {
+    float4 sum = gsum[g][q];
+    sum.x += __shfl_down(sum.x, 32, 64);
+    sum.y += __shfl_down(sum.y, 32, 64);
+    sum.z += __shfl_down(sum.z, 32, 64);
+    sum.w += __shfl_down(sum.w, 32, 64);
+    if (g == 0) {
     const int pos = row % a.Lq;
     const int hq = (row / a.Lq) % a.Hq;
     const int b = row / (a.Lq * a.Hq);
@@ -174,6 +208,7 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCom
       const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + 4 * q + e;
       if (a.o_f32) static_cast<float*>(a.o)[off] = v;
       else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
+    }
     }
   }
 }
