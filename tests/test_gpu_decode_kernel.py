@@ -157,6 +157,33 @@ def test_decode_equals_split_path_bitwise(dev, case):
         assert_close_attention(dec_o.cpu().numpy(), ref, f"decode {case}")
 
 
+def test_packed_nan_groups_match_bf16_rows(dev):
+    """A NaN in K or V makes its 64-value HiF4 group NaN (E6M2 byte 0xFF in the packed
+    rows): the packed decode gives NaN exactly where the bf16 rows do, and the same bits
+    elsewhere."""
+    from faquant_amd import _ops
+
+    case = (1, 32, 8, 1, 1000, True, "quantized_same", True, "123", 8)
+    B, Hq, Hkv, Lq, Lk = case[:5]
+    (q, k, v), _, kw = _decode_inputs(case, dev)
+    k = k.copy()
+    v = v.copy()
+    k[0, 2, 300, 17] = np.nan   # K group of KV head 2: its query heads' scores at key 300
+    v[0, 5, 700, 100] = np.nan  # V group of KV head 5: its rows once key 700 has weight
+    kd, vd = to_dev(k, dev, torch.bfloat16), to_dev(v, dev, torch.bfloat16)
+    qh, _ = _ops.operand_prep(to_dev(q, dev, torch.bfloat16), levels="123")
+    kh, _ = _ops.operand_prep(kd, levels="123")
+    vh, _ = _ops.operand_prep(vd, levels="123")
+    kc = _ops.pack_operand(kd, levels="123", out=_ops.PackedHiF4KV(B, Hkv, Lk, dev, "123"))
+    vc = _ops.pack_operand(vd, levels="123", out=_ops.PackedHiF4KV(B, Hkv, Lk, dev, "123"))
+    bf_o, _ = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, v=vh, split=8, **kw, **a), case, dev)
+    pk_o, _ = _run(lambda **a: _ops.attention_decode(qh, Lk, packed=(kc, vc), split=8, **kw, **a), case, dev)
+    nan = torch.isnan(bf_o)
+    assert nan.any() and not nan.all()
+    assert torch.equal(nan, torch.isnan(pk_o))
+    assert torch.equal(bf_o[~nan], pk_o[~nan])
+
+
 def test_drop_in_runs_decode_steps_on_the_decode_kernel(dev):
     """A decode step through the drop-in (no mask beyond the causal rule) is the decode
     kernel with its automatic range count, bitwise, and matches the oracle."""
