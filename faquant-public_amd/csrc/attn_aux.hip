@@ -74,9 +74,11 @@ __global__ __launch_bounds__(kScanThreads) void split_scan_kernel(SplitScanArgs 
 // O = sum_j 2^(m_j - M) O_j / sum_j 2^(m_j - M) l_j with M the row's final running maximum;
 // the per-split recurrences already used the reference's maxima, so only the fp32 order of
 // the O and l sums differs from one pass.
-constexpr int kCombineThreads = 512;
+constexpr int kCombineThreads = 128;
 constexpr int kCombineMaxSplits = 4096;
-constexpr int kCombineGroups = kCombineThreads / 32;  // split groups: 32 threads cover a row's 128 dims
+constexpr int kCombineGroups = 16;  // split groups
+constexpr int kCombineSlots = 512;  // l partial sums
+constexpr int kCombineQuarters = 4; // workgroups per row, 32 dims each
 
 struct SplitCombineArgs {
   const float* part_o;   // [nsplit, rows_total, 128]
@@ -89,70 +91,62 @@ struct SplitCombineArgs {
   float* row_den;        // optional [rows_total]
 };
 
-// One workgroup per row.  The split weights w_j = 2^(m_j - M) (0 for an empty split) go to
-// LDS; thread (g, q), g = tid / 32, sums w_j O_j[4q .. 4q + 3] over the splits j = g mod 16
-// in order, eight float4 loads in flight, and the 16 group sums are added in a fixed tree
-// (deterministic results); l is summed the same way.  The first eight O loads of each
-// thread and its first (l, m) are issued before the reductions that need M, so one memory
-// round trip serves up to 128 splits (512 for l and m).
+// Workgroup (row, quarter k) of 128 threads writes dims 32 k .. 32 k + 31 of the row.  The
+// split weights w_j = 2^(m_j - M) (0 for an empty split) go to LDS.  Thread (g, qq),
+// g = tid / 8, sums w_j O_j[4 q .. 4 q + 3], q = 8 k + qq, over the splits j = g mod 16 in
+// order, and the 16 group sums are added in the fixed tree g += g + d, d = 8, 4, 2, 1.  l is
+// the fixed tree over 512 slots (slot s sums w_j l_j over j = s mod 512 in order, then
+// slot s += slot s + d, d = 256, ..., 1), which every quarter computes the same way.  The
+// results do not depend on the launch shape: the same pairs are added in the same order.
+// The first eight O loads of each thread and its first (l, m) pairs are issued before the
+// reductions that need M.
 __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCombineArgs a) {
   __shared__ float wsh[kCombineMaxSplits];
-  __shared__ float red[kCombineThreads];
-  __shared__ float4 gsum[kCombineGroups][32];
+  __shared__ float red[kCombineSlots];
+  __shared__ float wmax[kCombineThreads / 64];
+  __shared__ float4 gsum[kCombineGroups][8];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
-  const int g = tid / 32, q = tid % 32;
+  const int g = tid / 8, qq = tid % 8, q = 8 * static_cast<int>(blockIdx.y) + qq;
   const float4* po = reinterpret_cast<const float4*>(a.part_o + static_cast<int64_t>(row) * kDim) + q;
   const int64_t js = static_cast<int64_t>(a.rows_total) * (kDim / 4);  // float4 stride of one split
+  const float2* plm = reinterpret_cast<const float2*>(a.part_lm) + row;  // split j at plm[j * rows_total]
   float4 v0[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int jj = g + kCombineGroups * u;
     v0[u] = jj < a.nsplit ? po[static_cast<int64_t>(jj) * js] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
-  const float2 lm0 = tid < a.nsplit ? *reinterpret_cast<const float2*>(a.part_lm + (static_cast<int64_t>(tid) * a.rows_total + row) * 2)
-                                    : make_float2(0.0f, -INFINITY);
-  // M: the maximum over the splits
-  float mloc = -INFINITY;
-  if (tid < a.nsplit) mloc = fmaxf(mloc, lm0.y);
-  for (int j = tid + kCombineThreads; j < a.nsplit; j += kCombineThreads)
-    mloc = fmaxf(mloc, a.part_lm[(static_cast<int64_t>(j) * a.rows_total + row) * 2 + 1]);
-  // (a maximum is exact: any reduction order gives the same value)
+  float2 lm0[4];  // splits tid + 128 r
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int j = tid + kCombineThreads * r;
+    lm0[r] = j < a.nsplit ? plm[static_cast<int64_t>(j) * a.rows_total] : make_float2(0.0f, -INFINITY);
+  }
+  // M: the maximum over the splits (a maximum is exact: any reduction order gives the same value)
+  float mloc = fmaxf(fmaxf(lm0[0].y, lm0[1].y), fmaxf(lm0[2].y, lm0[3].y));
+  for (int j = tid + kCombineSlots; j < a.nsplit; j += kCombineThreads)
+    mloc = fmaxf(mloc, plm[static_cast<int64_t>(j) * a.rows_total].y);
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, d, 64));
-  if ((tid & 63) == 0) red[tid >> 6] = mloc;
+  if ((tid & 63) == 0) wmax[tid >> 6] = mloc;
   __syncthreads();
-  float mmax = red[0];
+  const float mmax = fmaxf(wmax[0], wmax[1]);
+  // weights, and slot s = tid + 128 r of the l tree: sum of w_j l_j over j = s mod 512
 #pragma unroll
-  for (int w = 1; w < kCombineThreads / 64; ++w) mmax = fmaxf(mmax, red[w]);
-  __syncthreads();
-  // weights and the weighted l terms
-  float lloc = 0.0f;
-  for (int j = tid; j < a.nsplit; j += kCombineThreads) {
-    const int64_t r = static_cast<int64_t>(j) * a.rows_total + row;
-    const float2 lm = j == tid ? lm0 : make_float2(a.part_lm[r * 2], a.part_lm[r * 2 + 1]);
-    const float w = (mmax == -INFINITY || lm.x == 0.0f) ? 0.0f : __builtin_amdgcn_exp2f(lm.y - mmax);
-    wsh[j] = w;
-    lloc = __builtin_fmaf(w, lm.x, lloc);
-  }
-  // l: the fixed tree red[i] += red[i + d] for d = 256, 128, ..., 1 (the steps below 64 as
-  // shuffles within the first wave, same pairs)
-  red[tid] = lloc;
-  __syncthreads();
-#pragma unroll
-  for (int d = kCombineThreads / 2; d >= 128; d >>= 1) {
-    if (tid < d) red[tid] += red[tid + d];
-    __syncthreads();
-  }
-  if (tid < 64) {
-    float x = red[tid] + red[tid + 64];
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) x += __shfl_down(x, d, 64);
-    if (tid == 0) red[kCombineThreads - 1] = x;
+  for (int r = 0; r < 4; ++r) {
+    const int s = tid + kCombineThreads * r;
+    float lloc = 0.0f;
+    for (int j = s; j < a.nsplit; j += kCombineSlots) {
+      const float2 lm = j == s ? lm0[r] : plm[static_cast<int64_t>(j) * a.rows_total];
+      const float w = (mmax == -INFINITY || lm.x == 0.0f) ? 0.0f : __builtin_amdgcn_exp2f(lm.y - mmax);
+      wsh[j] = w;
+      lloc = __builtin_fmaf(w, lm.x, lloc);
+    }
+    red[s] = lloc;
   }
   __syncthreads();
-  const float l = red[kCombineThreads - 1];
-  // O: splits j = g, g + 16, ... of group g
+  // O: splits j = g, g + 16, ... of group g (the first eight from the loads issued at the start)
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   auto add = [&](float w, float4 v) {
     acc.x = __builtin_fmaf(w, v.x, acc.x);
@@ -160,7 +154,6 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCom
     acc.z = __builtin_fmaf(w, v.z, acc.z);
     acc.w = __builtin_fmaf(w, v.w, acc.w);
   };
-  // the first eight splits of the group from the loads issued at the start
 #pragma unroll
   for (int u = 0; u < 8; ++u)
     if (g + kCombineGroups * u < a.nsplit) add(wsh[g + kCombineGroups * u], v0[u]);
@@ -173,44 +166,67 @@ __global__ __launch_bounds__(kCombineThreads) void split_combine_kernel(SplitCom
     for (int u = 0; u < 8; ++u) add(wsh[j + kCombineGroups * u], v[u]);
   }
   for (; j < a.nsplit; j += kCombineGroups) add(wsh[j], po[static_cast<int64_t>(j) * js]);
-  // the fixed tree gsum[g] += gsum[g + d] for d = 8, 4, 2, 1 (the last step, groups 0 and
-  // 1 of the first wave, as a shuffle)
-  gsum[g][q] = acc;
+  gsum[g][qq] = acc;
+  // the first step of each tree (l: d = 256, two slots per thread; O: d = 8)
+  red[tid] += red[tid + 256];
+  red[tid + 128] += red[tid + 384];
+  __syncthreads();
+  red[tid] += red[tid + 128];  // d = 128
+  if (g < 8) {
+    const float4 o = gsum[g + 8][qq];
+    float4 m = gsum[g][qq];
+    m.x += o.x;
+    m.y += o.y;
+    m.z += o.z;
+    m.w += o.w;
+    gsum[g][qq] = m;
+  }
   __syncthreads();
 #pragma unroll
-  for (int d = kCombineGroups / 2; d >= 2; d >>= 1) {
+  for (int d = 4; d >= 2; d >>= 1) {
     if (g < d) {
-      const float4 o = gsum[g + d][q];
-      float4 m = gsum[g][q];
+      const float4 o = gsum[g + d][qq];
+      float4 m = gsum[g][qq];
       m.x += o.x;
       m.y += o.y;
       m.z += o.z;
       m.w += o.w;
-      gsum[g][q] = m;
+      gsum[g][qq] = m;
     }
     __syncthreads();
   }
-  if (g < 2) {
-    float4 sum = gsum[g][q];
-    sum.x += __shfl_down(sum.x, 32, 64);
-    sum.y += __shfl_down(sum.y, 32, 64);
-    sum.z += __shfl_down(sum.z, 32, 64);
-    sum.w += __shfl_down(sum.w, 32, 64);
-    if (g == 0) {
-    const int pos = row % a.Lq;
-    const int hq = (row / a.Lq) % a.Hq;
-    const int b = row / (a.Lq * a.Hq);
-    if (a.row_den && q == 0) a.row_den[row] = l;
-    const float vals[4] = {sum.x, sum.y, sum.z, sum.w};
+  if (tid < 64) {
+    // l: d = 64 from LDS, then d = 32 .. 1 as shuffles (lane 0 ends with the sum)
+    float x = red[tid] + red[tid + 64];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v = l > 0.0f ? vals[e] / fmaxf(l, 1.17549435e-38f) : 0.0f;
-      const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + 4 * q + e;
-      if (a.o_f32) static_cast<float*>(a.o)[off] = v;
-      else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
-    }
+    for (int d = 32; d > 0; d >>= 1) x += __shfl_down(x, d, 64);
+    const float l = __shfl(x, 0, 64);
+    // O: d = 1, groups 0 and 1 (lanes 0..7 and 8..15)
+    float4 sum = gsum[g < 2 ? g : 0][qq];
+    sum.x += __shfl_down(sum.x, 8, 64);
+    sum.y += __shfl_down(sum.y, 8, 64);
+    sum.z += __shfl_down(sum.z, 8, 64);
+    sum.w += __shfl_down(sum.w, 8, 64);
+    if (g == 0) {
+      const int pos = row % a.Lq;
+      const int hq = (row / a.Lq) % a.Hq;
+      const int b = row / (a.Lq * a.Hq);
+      if (a.row_den && q == 0) a.row_den[row] = l;
+      const float vals[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = l > 0.0f ? vals[e] / fmaxf(l, 1.17549435e-38f) : 0.0f;
+        const int64_t off = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(pos) * a.o_sl + 4 * q + e;
+        if (a.o_f32) static_cast<float*>(a.o)[off] = v;
+        else static_cast<uint16_t*>(a.o)[off] = f32_to_bf16_bits_rne(v);
+      }
     }
   }
+}
+
+inline void launch_split_combine(const SplitCombineArgs& ca, hipStream_t st) {
+  hipLaunchKernelGGL(split_combine_kernel, dim3(static_cast<unsigned>(ca.rows_total), kCombineQuarters),
+                     dim3(kCombineThreads), 0, st, ca);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -153,14 +153,12 @@ __device__ __forceinline__ int stage_key(int r, int s) { return (r & 31) + 32 * 
 constexpr int kStageBytes = 64 * kRowUnits * 16;  // 17408
 constexpr int kRowBytes = kRowUnits * 16;
 
-// One operand's rows: bf16 (base, row stride in elements) or packed (codes, meta, row
-// index of key 0 of the (batch, head)).
+// One operand's rows of a (batch, KV head): bf16 rows (key 0's row, row stride in bytes) or
+// packed rows (key 0's 16 code words and its 2 meta words).
 struct RowSrc {
-  const uint16_t* base;
-  int64_t sl;
-  const uint32_t* codes;
-  const uint32_t* meta;
-  int64_t row0;
+  const uint8_t* base;
+  const uint8_t* meta;
+  uint32_t row_bytes;
 };
 
 template <bool kPacked>
@@ -177,27 +175,75 @@ struct RowsRaw<true> {
   uint32_t m[2];  // its two meta words
 };
 
-// Loads of half tile s of tile t; keys past Lk read the last key's row (K: masked later;
-// V: zeroed in LDS by zero_tail_rows).  The loads are unconditional, so the memory counter
-// the waits use sees the same sequence on every iteration (a wait then covers only the
-// loads it needs: the counter completes in order).
+// Per-lane byte offsets of the row loads from a half tile's first key (loop-invariant).  bf16
+// rows: instruction i, lane l reads unit l % 16 of local row 4 i + l / 16, which is key
+// 4 i + l / 16 + 32 [i >= 8] of the half tile; packed rows: lane l reads local key l, key
+// (l % 32) + 64 (l / 32).
 template <bool kPacked>
-__device__ __forceinline__ void load_rows(const RowSrc& src, int Lk, int t, int s, int lane, RowsRaw<kPacked>& raw) {
+struct RowOffs;
+
+template <>
+struct RowOffs<false> {
+  uint32_t v[16];
+};
+
+template <>
+struct RowOffs<true> {
+  uint32_t c, m;
+};
+
+template <bool kPacked>
+__device__ __forceinline__ RowOffs<kPacked> row_offsets(const RowSrc& src, int lane) {
+  RowOffs<kPacked> o;
   if constexpr (kPacked) {
-    const int key = t * kKeyTile + stage_key(lane, s);
-    const int64_t row = src.row0 + min(key, Lk - 1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) raw.c[i] = ld16(src.codes + row * 16 + 4 * i);
-    const uint2 mm = *reinterpret_cast<const uint2*>(src.meta + row * 2);
-    raw.m[0] = mm.x;
-    raw.m[1] = mm.y;
+    const uint32_t k = static_cast<uint32_t>((lane & 31) + 64 * (lane >> 5));
+    o.c = 64u * k;
+    o.m = 8u * k;
   } else {
-    const uint16_t* b = src.base + 8 * (lane & 15);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = t * kKeyTile + stage_key(4 * i + (lane >> 4), s);
-      raw.x[i] = ld16(b + static_cast<int64_t>(min(key, Lk - 1)) * src.sl);
-    }
+    for (int i = 0; i < 16; ++i)
+      o.v[i] = static_cast<uint32_t>(4 * i + (lane >> 4) + (i >= 8 ? 32 : 0)) * src.row_bytes + 16u * (lane & 15);
+  }
+  return o;
+}
+
+// Raw buffer resource over the `keys` rows of `row_bytes` each from `base` (empty when keys
+// <= 0).  32-bit arithmetic: one head's rows span less than 4 GiB.  The arguments are
+// wave-uniform; they are read from the first lane so that the resource is built in scalar
+// registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const uint8_t* base, int keys, uint32_t row_bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32));
+  const uint32_t bytes = __builtin_amdgcn_readfirstlane(keys > 0 ? static_cast<uint32_t>(keys) * row_bytes : 0u);
+  return make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo), bytes);
+}
+
+// Loads of half tile s of tile t (local keys 0..31 are keys 32 s + 0..31 of the tile, local keys
+// 32..63 keys 64 + 32 s + 0..31) through buffer resources that start at the half tile's first
+// key and end at key Lk: the address arithmetic is scalar, and rows past Lk read as zeros
+// without a memory access (K: masked later; V: zeroed in LDS by zero_tail_rows, since packed
+// zeros do not decode to zero).  `valid` false (wave-uniform: a prefetch past the split's last
+// tile) gives an empty resource.  The loads are unconditional, so the memory counter the
+// waits use sees the same sequence on every iteration (a wait then covers only the loads it
+// needs: the counter completes in order).
+template <bool kPacked>
+__device__ __forceinline__ void load_rows(const RowSrc& src, const RowOffs<kPacked>& off, int Lk, int t, int s,
+                                          RowsRaw<kPacked>& raw, bool valid = true) {
+  const int key0 = valid ? t * kKeyTile + 32 * s : 0;
+  const int keys = valid ? Lk - key0 : 0;
+  if constexpr (kPacked) {
+    const __amdgpu_buffer_rsrc_t rc = rows_rsrc(src.base + static_cast<int64_t>(key0) * 64, keys, 64u);
+    const __amdgpu_buffer_rsrc_t rm = rows_rsrc(src.meta + static_cast<int64_t>(key0) * 8, keys, 8u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw.c[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, off.c + 16u * i, 0, 0);
+    const auto mm = __builtin_amdgcn_raw_buffer_load_b64(rm, off.m, 0, 0);
+    raw.m[0] = mm[0];
+    raw.m[1] = mm[1];
+  } else {
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(src.base + static_cast<int64_t>(key0) * src.row_bytes, keys, src.row_bytes);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) raw.x[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off.v[i], 0, 0);
   }
 }
 
@@ -230,14 +276,24 @@ __device__ __forceinline__ void store_rows(const RowsRaw<kPacked>& raw, int lane
 
 template <bool kPacked>
 __device__ __forceinline__ RowSrc k_source(const DecodeArgs& a, const DecWave& w) {
-  if constexpr (kPacked) return RowSrc{nullptr, 0, a.kc, a.km, w.b * a.kp_sb + w.kvh * a.kp_sh};
-  else return RowSrc{a.k + w.b * a.k_sb + w.kvh * a.k_sh, a.k_sl, nullptr, nullptr, 0};
+  if constexpr (kPacked) {
+    const int64_t row0 = w.b * a.kp_sb + w.kvh * a.kp_sh;
+    return RowSrc{reinterpret_cast<const uint8_t*>(a.kc + row0 * 16), reinterpret_cast<const uint8_t*>(a.km + row0 * 2), 0u};
+  } else {
+    return RowSrc{reinterpret_cast<const uint8_t*>(a.k + w.b * a.k_sb + w.kvh * a.k_sh), nullptr,
+                  static_cast<uint32_t>(2 * a.k_sl)};
+  }
 }
 
 template <bool kPacked>
 __device__ __forceinline__ RowSrc v_source(const DecodeArgs& a, const DecWave& w) {
-  if constexpr (kPacked) return RowSrc{nullptr, 0, a.vc, a.vm, w.b * a.vp_sb + w.kvh * a.vp_sh};
-  else return RowSrc{a.v + w.b * a.v_sb + w.kvh * a.v_sh, a.v_sl, nullptr, nullptr, 0};
+  if constexpr (kPacked) {
+    const int64_t row0 = w.b * a.vp_sb + w.kvh * a.vp_sh;
+    return RowSrc{reinterpret_cast<const uint8_t*>(a.vc + row0 * 16), reinterpret_cast<const uint8_t*>(a.vm + row0 * 2), 0u};
+  } else {
+    return RowSrc{reinterpret_cast<const uint8_t*>(a.v + w.b * a.v_sb + w.kvh * a.v_sh), nullptr,
+                  static_cast<uint32_t>(2 * a.v_sl)};
+  }
 }
 
 // Scores pass.
@@ -254,6 +310,7 @@ void dec_scores_kernel(DecodeArgs a) {
   uint8_t* const region = lds + (threadIdx.x >> 6) * kStageBytes;
   const int off = a.Lk - a.Lq;
   const RowSrc ksrc = k_source<kPacked>(a, w);
+  const RowOffs<kPacked> koff = row_offsets<kPacked>(ksrc, lane);
 
   bf16x8 qf[8];
   {
@@ -267,7 +324,7 @@ void dec_scores_kernel(DecodeArgs a) {
   const int krow0 = 64 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
   float smax = -INFINITY;
   RowsRaw<kPacked> raw;
-  if (w.t_lo < w.t_hi) load_rows<kPacked>(ksrc, a.Lk, w.t_lo, 0, lane, raw);
+  if (w.t_lo < w.t_hi) load_rows<kPacked>(ksrc, koff, a.Lk, w.t_lo, 0, raw);
   for (int t = w.t_lo; t < w.t_hi; ++t) {
     const int key0 = t * kKeyTile;
     floatx16 s[4];
@@ -276,9 +333,9 @@ void dec_scores_kernel(DecodeArgs a) {
       wave_lds_order();  // the previous half tile's fragment reads are issued
       store_rows<kPacked>(raw, lane, region);
       wave_lds_order();
-      // the next half tile's loads fly during this one's MFMAs
-      // (past the split's last tile: a repeat of its first half, unused)
-      load_rows<kPacked>(ksrc, a.Lk, st == 0 ? t : min(t + 1, w.t_hi - 1), st ^ 1, lane, raw);
+      // the next half tile's loads fly during this one's MFMAs (past the split's last tile:
+      // an empty resource)
+      load_rows<kPacked>(ksrc, koff, a.Lk, t + st, st ^ 1, raw, st == 0 || t + 1 < w.t_hi);
 #pragma unroll
       for (int kb = 2 * st; kb < 2 * st + 2; ++kb) {
         const int pi = krow0 + 16 * kb;
@@ -392,6 +449,7 @@ void dec_values_kernel(DecodeArgs a) {
   const DecWave w = dec_wave(a, wave_id, n);
   uint8_t* const region = lds + (threadIdx.x >> 6) * kStageBytes;
   const RowSrc vsrc = v_source<kPacked>(a, w);
+  const RowOffs<kPacked> voff = row_offsets<kPacked>(vsrc, lane);
 
   const float* srow = a.s + w.row * a.s_stride + 64 * half;
   // S of chunk c (keys 64 half + 8 c .. + 7 of tile t) in a ring of four chunks
@@ -416,7 +474,7 @@ void dec_values_kernel(DecodeArgs a) {
   float2 gnext = make_float2(-INFINITY, -INFINITY);
   if (w.t_lo < w.t_hi) {
     gnext = load_g(w.t_lo);
-    load_rows<kPacked>(vsrc, a.Lk, w.t_lo, 0, lane, vr);
+    load_rows<kPacked>(vsrc, voff, a.Lk, w.t_lo, 0, vr);
 #pragma unroll
     for (int c = 0; c < 4; ++c) load_s(w.t_lo, c, c);
   }
@@ -466,7 +524,7 @@ void dec_values_kernel(DecodeArgs a) {
         store_rows<kPacked>(vr, lane, region);
         if ((t + 1) * kKeyTile > a.Lk) zero_tail_rows(a.Lk, t, c >> 2, lane, region);
         wave_lds_order();
-        load_rows<kPacked>(vsrc, a.Lk, (c >> 2) ? tn : t, (c >> 2) ^ 1, lane, vr);
+        load_rows<kPacked>(vsrc, voff, a.Lk, t + (c >> 2), (c >> 2) ^ 1, vr, c == 0 || t + 1 < w.t_hi);
       }
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) va[mb] = vt_fragment(region, lane, mb, c & 3);
@@ -549,6 +607,7 @@ void dec_values_compact_kernel(DecodeArgs a) {
   uint8_t* const region = lds + (threadIdx.x >> 6) * kRegion;
   uint8_t* const pslots = region + kStageBytes;
   const RowSrc vsrc = v_source<kPacked>(a, w);
+  const RowOffs<kPacked> voff = row_offsets<kPacked>(vsrc, lane);
 
   // this lane's compact units: columns cr + 4 i, key half ch, chunk cc
   const int cr = lane >> 4, ch = (lane >> 3) & 1, cc = lane & 7;
@@ -580,7 +639,7 @@ void dec_values_compact_kernel(DecodeArgs a) {
   float snext[kUnits][8];
   if (w.t_lo < w.t_hi) {
     gnext = load_g(w.t_lo);
-    load_rows<kPacked>(vsrc, a.Lk, w.t_lo, 0, lane, vr);
+    load_rows<kPacked>(vsrc, voff, a.Lk, w.t_lo, 0, vr);
     load_sc(w.t_lo, snext);
   }
   float m_run = running_max_before<kCols>(a, w, lane, n);
@@ -658,7 +717,7 @@ void dec_values_compact_kernel(DecodeArgs a) {
         store_rows<kPacked>(vr, lane, region);
         if ((t + 1) * kKeyTile > a.Lk) zero_tail_rows(a.Lk, t, c >> 2, lane, region);
         wave_lds_order();
-        load_rows<kPacked>(vsrc, a.Lk, (c >> 2) ? tn : t, (c >> 2) ^ 1, lane, vr);
+        load_rows<kPacked>(vsrc, voff, a.Lk, t + (c >> 2), (c >> 2) ^ 1, vr, c == 0 || t + 1 < w.t_hi);
       }
       bf16x8 va[4];
 #pragma unroll

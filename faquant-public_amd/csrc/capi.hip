@@ -605,8 +605,7 @@ int faq_attention_fwd_split(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64
   launch_attention(ap, quant_p, p_levels, norm_same, grid, st);
   // 4. combine
   faq::SplitCombineArgs ca{ap.part_o, ap.part_lm, a.rows_total, nsplit, Hq, Lq, o, o_sb, o_sh, o_sl, a.o_f32, row_den};
-  hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(faq::kCombineThreads), 0,
-                     st, ca);
+  faq::launch_split_combine(ca, st);
   return check_launch("faq_attention_fwd_split");
 }
 
@@ -783,8 +782,7 @@ int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t 
   faq::launch_decode(a, packed ? 1 : 0, quant_p, p_levels, norm_same, st);
   faq::SplitCombineArgs ca{a.part_o, a.part_lm, a.rows_total, nsplit, Hq, Lq, o, o_sb, o_sh, o_sl,
                            o_dtype == FAQ_F32, row_den};
-  hipLaunchKernelGGL(faq::split_combine_kernel, dim3(static_cast<unsigned>(a.rows_total)), dim3(faq::kCombineThreads), 0,
-                     st, ca);
+  faq::launch_split_combine(ca, st);
   return check_launch(who);
 }
 
