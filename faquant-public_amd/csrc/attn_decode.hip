@@ -82,11 +82,26 @@ __device__ __forceinline__ DecWave dec_wave(const DecodeArgs& a, int wave_id, in
   return w;
 }
 
-// Maximum over the 64 lanes, in every lane.
+// One DPP step of a maximum: x and lane (ctrl's source lane) of x.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_max(float x) {
+  const int y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false);
+  return fmaxf(x, __int_as_float(y));
+}
+
+// Maximum over the 64 lanes, wave-uniform: within each row of 16 lanes by DPP (lane pairs,
+// quads, the two halves of a row mirrored, the row mirrored), then the four row maxima read
+// from lanes 0, 16, 32, 48.  No LDS round trips; a maximum does not depend on the order.
 __device__ __forceinline__ float wave_max_f32(float x) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
-  return x;
+  x = dpp_max<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x = dpp_max<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x = dpp_max<0x141>(x);  // row_half_mirror
+  x = dpp_max<0x140>(x);  // row_mirror
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 __device__ __forceinline__ int dec_wave_id() {
@@ -437,6 +452,64 @@ __device__ __forceinline__ float running_max_before(const DecodeArgs& a, const D
   return m_run;
 }
 
+// The same maximum in two steps, for a few columns: rmax_issue loads the maxima of splits
+// 0..127 (unconditional loads of clamped indices) before the first tile's loads are issued,
+// so that waiting for them does not wait for the tile; rmax_finish drops the lanes outside
+// [0, w.j), reads the splits from 128 on, and reduces each live column across the wave.
+template <int kCols>
+__device__ __forceinline__ const float* rmax_row(const DecodeArgs& a, const DecWave& w, int r, int nrows) {
+  const int rr = min(r, nrows - 1);  // column rr: head rr % G, position pmin + rr / G
+  const int64_t row0 = (static_cast<int64_t>(w.b) * a.Hq + w.kvh * a.G) * a.Lq + w.pmin;
+  return a.smx + (row0 + static_cast<int64_t>(rr % a.G) * a.Lq + rr / a.G) * a.nsplit;
+}
+
+template <int kCols>
+__device__ __forceinline__ int rmax_rows(const DecodeArgs& a, const DecWave& w) {
+  return min(min(a.G * a.pb, a.G * (a.Lq - w.pmin)), kCols);  // live columns 0 .. nrows - 1
+}
+
+template <int kCols>
+__device__ __forceinline__ void rmax_issue(const DecodeArgs& a, const DecWave& w, int lane, uint32_t (&x)[2][kCols]) {
+  const int nrows = rmax_rows<kCols>(a, w);
+  const int jmax = max(w.j - 1, 0);
+#pragma unroll
+  for (int r = 0; r < kCols; ++r) {
+    const float* sm = rmax_row<kCols>(a, w, r, nrows);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) x[q][r] = __float_as_uint(sm[min(64 * q + lane, jmax)]);
+  }
+}
+
+template <int kCols>
+__device__ __forceinline__ float rmax_finish(const DecodeArgs& a, const DecWave& w, int lane, int n,
+                                             const uint32_t (&x)[2][kCols]) {
+  const int nrows = rmax_rows<kCols>(a, w);
+  float mr[kCols];
+#pragma unroll
+  for (int r = 0; r < kCols; ++r)
+    mr[r] = fmaxf(lane < w.j ? __uint_as_float(x[0][r]) : -INFINITY, 64 + lane < w.j ? __uint_as_float(x[1][r]) : -INFINITY);
+  for (int j0 = 128; j0 < w.j; j0 += 128) {
+    float y[2][kCols];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int jj = j0 + 64 * q + lane;
+#pragma unroll
+      for (int r = 0; r < kCols; ++r) y[q][r] = jj < w.j ? rmax_row<kCols>(a, w, r, nrows)[jj] : -INFINITY;
+    }
+#pragma unroll
+    for (int r = 0; r < kCols; ++r) mr[r] = fmaxf(mr[r], fmaxf(y[0][r], y[1][r]));
+  }
+  float m_run = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < kCols; ++r) {
+    if (r < nrows) {
+      const float m = wave_max_f32(mr[r]);
+      if (n == r) m_run = m * a.c1;
+    }
+  }
+  return m_run;
+}
+
 template <int LV, bool kQuantP, bool kSame, bool kPacked>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dec_values_kernel(DecodeArgs a) {
@@ -452,22 +525,17 @@ void dec_values_kernel(DecodeArgs a) {
   const RowOffs<kPacked> voff = row_offsets<kPacked>(vsrc, lane);
 
   const float* srow = a.s + w.row * a.s_stride + 64 * half;
-  // S of chunk c (keys 64 half + 8 c .. + 7 of tile t) in a ring of four chunks
-  float sv[4][8];
-  // (unconditional loads: lanes without a row read a row of this KV head and drop it)
+  // S of chunk c (keys 64 half + 8 c .. + 7 of tile t) in a ring of four chunks, kept as
+  // loaded (unconditional loads: lanes without a row read a row of this KV head, and their
+  // scores and lane maxima are made -inf where they are used, so that no select right after
+  // a load makes the wave wait for it)
+  u32x4 sv[4][2];
   auto load_s = [&](int t, int c, int slot) {
     const float* sp = srow + t * kKeyTile + 8 * c;
-    const u32x4 x0 = ld16(sp), x1 = ld16(sp + 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sv[slot][i] = w.live ? __uint_as_float(x0[i]) : -INFINITY;
-      sv[slot][4 + i] = w.live ? __uint_as_float(x1[i]) : -INFINITY;
-    }
+    sv[slot][0] = ld16(sp);
+    sv[slot][1] = ld16(sp + 4);
   };
-  auto load_g = [&](int t) {
-    const float2 x = *reinterpret_cast<const float2*>(a.gmx + (w.row * a.ntiles + t) * 2);
-    return w.live ? x : make_float2(-INFINITY, -INFINITY);
-  };
+  auto load_g = [&](int t) { return *reinterpret_cast<const float2*>(a.gmx + (w.row * a.ntiles + t) * 2); };
   // the first tile's lane maxima, V half tile and S chunks are in flight (in the order they
   // are used) while the maximum below is read
   RowsRaw<kPacked> vr;
@@ -493,7 +561,7 @@ void dec_values_kernel(DecodeArgs a) {
   }
   for (int t = w.t_lo; t < w.t_hi; ++t) {
     const int tn = min(t + 1, w.t_hi - 1);  // the next tile (past the last: a repeat, unused)
-    const float2 g = gnext;
+    const float2 g = w.live ? gnext : make_float2(-INFINITY, -INFINITY);
     gnext = load_g(tn);
     // the prefill kernel's tile recurrence: g.x, g.y are the lane maxima of the two halves
     const float mx = half ? g.y : g.x;
@@ -530,7 +598,10 @@ void dec_values_kernel(DecodeArgs a) {
       for (int mb = 0; mb < 4; ++mb) va[mb] = vt_fragment(region, lane, mb, c & 3);
       float pc[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[slot][j], a.c1, nm));
+      for (int j = 0; j < 8; ++j) {
+        const float sj = w.live ? __uint_as_float(sv[slot][j >> 2][j & 3]) : -INFINITY;
+        pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sj, a.c1, nm));
+      }
       // the S slot takes chunk c + 4 (of this tile or the next)
       load_s(c < 4 ? t : tn, (c + 4) & 7, slot);
       if (!(kQuantP && kSame)) {
@@ -619,30 +690,44 @@ void dec_values_compact_kernel(DecodeArgs a) {
     clive[i] = wc.live;
     sc[i] = a.s + wc.row * a.s_stride + 64 * ch + 8 * cc;
   }
-  auto load_sc = [&](int t, float (&x)[kUnits][8]) {
+  // S chunks and lane maxima are kept as loaded and made -inf for lanes without a row where
+  // they are used (in the tile loop): a select right after the loads would make the wave
+  // wait for them early
+  auto load_sc = [&](int t, u32x4 (&x)[kUnits][2]) {
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
-      const u32x4 x0 = ld16(sc[u] + t * kKeyTile), x1 = ld16(sc[u] + t * kKeyTile + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[u][i] = clive[u] ? __uint_as_float(x0[i]) : -INFINITY;
-        x[u][4 + i] = clive[u] ? __uint_as_float(x1[i]) : -INFINITY;
-      }
+      x[u][0] = ld16(sc[u] + t * kKeyTile);
+      x[u][1] = ld16(sc[u] + t * kKeyTile + 4);
     }
   };
-  auto load_g = [&](int t) {
-    const float2 x = *reinterpret_cast<const float2*>(a.gmx + (w.row * a.ntiles + t) * 2);
-    return w.live ? x : make_float2(-INFINITY, -INFINITY);
-  };
-  RowsRaw<kPacked> vr;
-  float2 gnext = make_float2(-INFINITY, -INFINITY);
-  float snext[kUnits][8];
-  if (w.t_lo < w.t_hi) {
-    gnext = load_g(w.t_lo);
-    load_rows<kPacked>(vsrc, voff, a.Lk, w.t_lo, 0, vr);
-    load_sc(w.t_lo, snext);
+  auto load_g = [&](int t) { return *reinterpret_cast<const float2*>(a.gmx + (w.row * a.ntiles + t) * 2); };
+  if (w.t_lo >= w.t_hi) {
+    // an empty split (past a causal row block's last key): a zero partial, which the combine
+    // weighs 0 (the split maximum does not matter then)
+    if (w.live) {
+      float* po = a.part_o + (static_cast<int64_t>(w.j) * a.rows_total + w.row) * kDim;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<float4*>(po + 32 * mb + 8 * j + 4 * half) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (half == 0) {
+        float* lm = a.part_lm + (static_cast<int64_t>(w.j) * a.rows_total + w.row) * 2;
+        lm[0] = 0.0f;
+        lm[1] = -INFINITY;
+      }
+    }
+    return;
   }
-  float m_run = running_max_before<kCols>(a, w, lane, n);
+  // the split maxima before this split first, then the first tile's lane maxima, V half tile
+  // and S chunks, all in flight together (unconditional, so that the waits count them exactly)
+  uint32_t rmx[2][kCols];
+  rmax_issue<kCols>(a, w, lane, rmx);
+  RowsRaw<kPacked> vr;
+  u32x4 snext[kUnits][2];
+  float2 gnext = load_g(w.t_lo);
+  load_rows<kPacked>(vsrc, voff, a.Lk, w.t_lo, 0, vr);
+  load_sc(w.t_lo, snext);
+  float m_run = rmax_finish<kCols>(a, w, lane, n, rmx);
   float l_run = 0.0f;
   floatx16 acc[4];
 #pragma unroll
@@ -654,13 +739,13 @@ void dec_values_compact_kernel(DecodeArgs a) {
   }
   for (int t = w.t_lo; t < w.t_hi; ++t) {
     const int tn = min(t + 1, w.t_hi - 1);  // the next tile (past the last: a repeat, unused)
-    const float2 g = gnext;
+    const float2 g = w.live ? gnext : make_float2(-INFINITY, -INFINITY);
     gnext = load_g(tn);
     float sx[kUnits][8];
 #pragma unroll
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sx[u][j] = snext[u][j];
+      for (int j = 0; j < 8; ++j) sx[u][j] = clive[u] ? __uint_as_float(snext[u][j >> 2][j & 3]) : -INFINITY;
     load_sc(tn, snext);
     // the full pass's tile recurrence, per column n
     const float mx_row = fmaxf(g.x, g.y);
