@@ -362,17 +362,31 @@ def linear_bench(tokens: int, steps: int, warmup: int) -> dict:
 
 
 def stream_reference() -> dict:
-    """This device's practical HBM rate for plain streams (torch's copy and sum over 1 GiB of
-    fp32, beyond the 256 MiB last-level cache): the measured reference point beside the
-    8 TB/s specification for the HBM-bound decode kernels."""
+    """This device's practical rates for plain streams, the measured reference points beside
+    the 8 TB/s specification for the HBM-bound decode kernels: torch's copy and sum over
+    1 GiB of fp32 (beyond the 256 MiB last-level cache), and the library's read probe
+    (faq_stream_probe: coalesced 16-byte loads, four in flight per thread) over 1 GiB and
+    over 128 MiB (about a 32k-key decode step's K and V, which the last-level cache holds
+    from one read to the next)."""
     import torch
+
+    from faquant_amd import _lib
 
     dev = torch.device("cuda:0")
     n = (1 << 30) // 4
     x = torch.randn(n, device=dev)
     y = torch.empty_like(x)
+    lib = _lib.load()
+    stream = _lib.stream_ptr(dev)
+    blocks = 4 * _ops_cus(dev)
+    out = torch.empty(blocks, device=dev)
+
+    def probe(nbytes):
+        return lambda: _lib.check(lib.faq_stream_probe(x.data_ptr(), nbytes, out.data_ptr(), blocks, stream))
+
     res = {}
-    for name, fn, nbytes in (("copy", lambda: y.copy_(x), 8 * n), ("sum", lambda: x.sum(), 4 * n)):
+    for name, fn, nbytes in (("copy", lambda: y.copy_(x), 8 * n), ("sum", lambda: x.sum(), 4 * n),
+                             ("read_probe_1GiB", probe(4 * n), 4 * n), ("read_probe_128MiB", probe(1 << 27), 1 << 27)):
         for _ in range(5):
             fn()
         torch.cuda.synchronize()
@@ -384,7 +398,14 @@ def stream_reference() -> dict:
         torch.cuda.synchronize()
         ms = a.elapsed_time(b) / 20
         res[name] = {"bytes": nbytes, "us": round(ms * 1e3, 1), "gbps": round(nbytes / ms / 1e6, 1)}
-    return {"stream_reference": "1 GiB fp32 through torch copy_ (read + write) and sum (read)", **res}
+    return {"stream_reference": "1 GiB fp32 through torch copy_ (read + write) and sum (read); faq_stream_probe "
+                                "reads of 1 GiB and 128 MiB", **res}
+
+
+def _ops_cus(dev) -> int:
+    from faquant_amd import _ops
+
+    return _ops._device_cus(dev)
 
 
 def main():

@@ -808,4 +808,13 @@ int faq_mfma_probe(float* out, int blocks, int iters, faq_stream_t stream) {
   return check_launch("faq_mfma_probe");
 }
 
+int faq_stream_probe(const void* x, int64_t bytes, float* out, int blocks, faq_stream_t stream) {
+  if (!x || !out) return fail(FAQ_EINVAL, "faq_stream_probe: null input or output");
+  if (!aligned16(x) || bytes < 16 || bytes % 16) return fail(FAQ_EINVAL, "faq_stream_probe: bytes must be a positive multiple of 16 at a 16-byte aligned address");
+  if (blocks < 1) return fail(FAQ_EINVAL, "faq_stream_probe: blocks must be positive");
+  hipLaunchKernelGGL(faq::stream_probe_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint4*>(x), bytes / 16, out);
+  return check_launch("faq_stream_probe");
+}
+
 }  // extern "C"

@@ -30,4 +30,25 @@ void mfma_probe_kernel(float* out, int iters) {
   out[static_cast<int64_t>(blockIdx.x) * blockDim.x + t] = s;
 }
 
+// Stream probe: the read rate a plain coalesced stream reaches on this device, the measured
+// reference point next to the 8 TB/s specification for the HBM-bound decode kernels.
+// 256-thread workgroups read `n16` 16-byte units in a grid-stride loop, four independent
+// 16-byte loads per thread in flight, and write one word per workgroup (so that the loads are
+// not removed).
+__global__ __launch_bounds__(256) void stream_probe_kernel(const uint4* __restrict__ x, int64_t n16, float* out) {
+  uint32_t acc = 0;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * 1024 + threadIdx.x;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * 1024;
+  for (; i + 768 < n16; i += step) {
+    const uint4 a = x[i], b = x[i + 256], c = x[i + 512], d = x[i + 768];
+    acc += (a.x ^ a.y ^ a.z ^ a.w) + (b.x ^ b.y ^ b.z ^ b.w) + (c.x ^ c.y ^ c.z ^ c.w) + (d.x ^ d.y ^ d.z ^ d.w);
+  }
+  for (; i < n16; i += 256) {
+    const uint4 a = x[i];
+    acc += a.x ^ a.y ^ a.z ^ a.w;
+  }
+  acc += __shfl_xor(acc, 1, 64);
+  if (threadIdx.x == 0) out[blockIdx.x] = static_cast<float>(acc);
+}
+
 }  // namespace faq

@@ -56,6 +56,9 @@
  *                         (simulated_flash_attention.py:801-806 via hif4.py:143-271)
  *   faq_mfma_probe        no reference counterpart: a measurement helper (the device's
  *                         sustained bf16 MFMA rate, the reference point of the benchmark)
+ *   faq_stream_probe      no reference counterpart: a measurement helper (the device's
+ *                         read rate for a plain stream, the reference point of the decode
+ *                         benchmark)
  */
 #ifndef FAQUANT_AMD_H
 #define FAQUANT_AMD_H
@@ -366,6 +369,16 @@ int faq_pquant_groups(const float* p, float* p_hat, int64_t groups, int levels, 
  * device's sustained dense bf16 MFMA rate.  out receives blocks * 512 fp32 values.
  */
 int faq_mfma_probe(float* out, int blocks, int iters, faq_stream_t stream);
+
+/*
+ * Measurement helper with no counterpart in the reference: `blocks` 256-thread workgroups
+ * read the `bytes` bytes at x (a positive multiple of 16, 16-byte aligned) with coalesced
+ * 16-byte loads in a grid-stride loop, four loads per thread in flight, and write one fp32
+ * word per workgroup to out.  Timed by the caller; the result is this device's read rate
+ * for a plain stream (from HBM, or from the last-level cache when x fits there and was
+ * read just before).
+ */
+int faq_stream_probe(const void* x, int64_t bytes, float* out, int blocks, faq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -40,7 +40,7 @@ def test_header_lists_the_entry_points():
         ["faq_last_error", "faq_version", "faq_hif4_qdq_rows", "faq_hif4_unpack_rows", "faq_hadamard_rows",
          "faq_act_qdq_rows", "faq_operand_prep", "faq_operand_prep_vt", "faq_attention_fwd",
          "faq_attention_fwd_split", "faq_attention_split_workspace", "faq_attention_mask_bounds",
-         "faq_mfma_probe", "faq_pquant_groups", "faq_hadamard_rows_native", "faq_attention_fwd_split_noalloc",
+         "faq_mfma_probe", "faq_stream_probe", "faq_pquant_groups", "faq_hadamard_rows_native", "faq_attention_fwd_split_noalloc",
          "faq_operand_prep_hif4_kv", "faq_attention_decode", "faq_attention_decode_workspace"]
     )
 
@@ -66,6 +66,9 @@ def test_validation_statuses_without_device_work(lib):
     assert "123, 12 or 13" in lib.faq_last_error().decode()
     assert lib.faq_mfma_probe(None, 1, 1, None) == _lib.EINVAL
     assert lib.faq_mfma_probe(p16, 0, 1, None) == _lib.EINVAL
+    assert lib.faq_stream_probe(None, 16, p16, 1, None) == _lib.EINVAL
+    assert lib.faq_stream_probe(p16, 24, p16, 1, None) == _lib.EINVAL
+    assert lib.faq_stream_probe(p16, 16, p16, 0, None) == _lib.EINVAL
     assert lib.faq_hadamard_rows(p16, p16, 1, 24, 3, 0, 0, None) == _lib.EINVAL
     assert "power of two" in lib.faq_last_error().decode()
     assert lib.faq_act_qdq_rows(p16, p16, 1, 96, 1, None, 64, 123, None) == _lib.EINVAL
