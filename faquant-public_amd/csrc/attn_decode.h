@@ -47,4 +47,11 @@ struct DecodeArgs {
 // Scores pass, then the values pass (partials per split; the caller combines them).
 void launch_decode(const DecodeArgs& a, int packed, int quant_p, int p_levels, int norm_same, hipStream_t st);
 
+// The one-pass form of the same (the same partials, bitwise): decode steps with P quantized,
+// the quantized-same normalizer, at most 8 live columns per row block, one key tile per
+// split and at most 64 key tiles.  epoch: nonzero, different for every call; spin_limit: rounds a split
+// waits for the maxima of the splits before it before computing them itself (< 0: always).
+bool decode_fused_fits(const DecodeArgs& a, int quant_p, int norm_same);
+void launch_decode_fused(const DecodeArgs& a, int packed, int p_levels, uint32_t epoch, int spin_limit, hipStream_t st);
+
 }  // namespace faq

@@ -51,6 +51,7 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<
 
 // The rows of a decode wave and its key tiles.
 struct DecWave {
+  int item;        // work item: (batch, KV head, row block) (wave-uniform)
   int b, kvh, j;   // batch, KV head, key split (wave-uniform)
   int pmin;        // first position of the row block (wave-uniform)
   int t_lo, t_hi;  // key tiles of the split (wave-uniform)
@@ -62,6 +63,7 @@ struct DecWave {
 __device__ __forceinline__ DecWave dec_wave(const DecodeArgs& a, int wave_id, int n) {
   DecWave w;
   const int item = wave_id / a.nsplit;
+  w.item = item;
   w.j = wave_id - item * a.nsplit;
   const int rb = item % a.n_rb;
   const int x = item / a.n_rb;
@@ -829,6 +831,368 @@ void dec_values_compact_kernel(DecodeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// One-pass decode for at most kCols = 4 or 8 live columns (the compact values pass's cases)
+// and one key tile per split: each wave computes its split's scores (kept in registers, in
+// the compact layout), publishes its split maxima, finds the running maximum before its
+// split from the maxima that the earlier splits of its row block published (a look-back
+// across waves), then runs the compact values pass on those scores.  K and V are read in
+// one launch and S never goes to memory; the arithmetic is the two passes', so the outputs
+// are the same bits.
+//
+// The published maxima live in a file-scope array of 64-bit words (value bits, and the
+// call's epoch in the high half: a word from another call never matches), slot
+// (item nsplit + split) kCols + column.  Waiting is bounded: after spin_limit rounds a wave
+// computes the maxima it still lacks itself, from K (spin_limit < 0: always), so a split
+// whose predecessors never run still finishes, with the same result.
+constexpr int kDecFlagSlots = 1 << 19;
+constexpr int kFusedMaxTps = 1;  // key tiles per split
+// The one pass is taken up to 64 key tiles (8192 keys): measured against the two passes
+// (Qwen3-8B heads, one tile per split), 8k 16.7 against 19.0 us (bf16) and 17.9 against
+// 19.9 (packed); 16k and 32k within +-0.5 us either way.
+constexpr int kFusedMaxTiles = 64;
+__device__ unsigned long long dec_flags[kDecFlagSlots];
+
+__device__ __forceinline__ void flag_publish(int64_t slot, uint32_t epoch, float v) {
+  const unsigned long long word = (static_cast<unsigned long long>(epoch) << 32) | __float_as_uint(v);
+  __hip_atomic_store(&dec_flags[slot], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long flag_read(int64_t slot) {
+  return __hip_atomic_load(&dec_flags[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The maximum of split w's scores (key tiles [t_lo, t_hi)) in lane (n, half) (column n, keys
+// 64 half + 0..63 of each tile), with the scores pass's loads, staging, MFMA chains and
+// masking: the look-back's own computation of a split maximum that did not arrive.
+template <bool kPacked>
+__device__ __forceinline__ float split_scores_max(const DecodeArgs& a, const DecWave& w, const bf16x8 (&qf)[8],
+                                                  const RowSrc& ksrc, const RowOffs<kPacked>& koff, uint8_t* region,
+                                                  int lane) {
+  const int n = lane & 31, half = lane >> 5;
+  const int off = a.Lk - a.Lq;
+  const int krow0 = 64 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+  float smax = -INFINITY;
+  RowsRaw<kPacked> raw;
+  load_rows<kPacked>(ksrc, koff, a.Lk, w.t_lo, 0, raw);
+  for (int t = w.t_lo; t < w.t_hi; ++t) {
+    const int key0 = t * kKeyTile;
+    floatx16 s[4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      wave_lds_order();
+      store_rows<kPacked>(raw, lane, region);
+      wave_lds_order();
+      load_rows<kPacked>(ksrc, koff, a.Lk, t + st, st ^ 1, raw, st == 0 || t + 1 < w.t_hi);
+#pragma unroll
+      for (int kb = 2 * st; kb < 2 * st + 2; ++kb) {
+        const int pi = krow0 + 16 * kb;
+        const uint8_t* kp = region + (((pi & 31) + 32 * (pi >> 6)) * kRowUnits + half) * 16;
+        s[kb] = floatx16{};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) s[kb] = mfma32(lds_read_at(kp, 32 * c), qf[c], s[kb]);
+      }
+    }
+    if (key0 + kKeyTile > a.Lk || (a.causal && key0 + kKeyTile - 1 > w.pmin + off)) {
+      const int lim = a.causal ? min(a.Lk - 1, w.pos + off) : a.Lk - 1;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (key0 + 64 * half + 16 * kb + i > lim) s[kb][i] = -INFINITY;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) smax = fmaxf(smax, s[kb][i]);
+  }
+  return smax;
+}
+
+// Running maximum before split w.j (c1-scaled, in lane n for column n) from the published
+// split maxima of splits 0 .. w.j - 1 of the row block: lane l waits for split j0 + l.
+template <bool kPacked, int kCols>
+__device__ __forceinline__ float lookback_max(const DecodeArgs& a, const DecWave& w, const bf16x8 (&qf)[8],
+                                              const RowSrc& ksrc, const RowOffs<kPacked>& koff, uint8_t* region,
+                                              int wave_id, int lane, uint32_t epoch, int spin_limit) {
+  const int n = lane & 31;
+  const int nrows = rmax_rows<kCols>(a, w);
+  const int64_t slot0 = static_cast<int64_t>(w.item) * a.nsplit * kCols;
+  float mr[kCols];
+#pragma unroll
+  for (int r = 0; r < kCols; ++r) mr[r] = -INFINITY;
+  for (int j0 = 0; j0 < w.j; j0 += 64) {
+    const int jj = j0 + lane;
+    const bool in = jj < w.j;
+    float x[kCols];
+    bool ok[kCols];
+#pragma unroll
+    for (int r = 0; r < kCols; ++r) {
+      x[r] = -INFINITY;
+      ok[r] = !in || r >= nrows;
+    }
+    if (spin_limit >= 0) {
+      for (int it = 0;; ++it) {
+        bool all = true;
+#pragma unroll
+        for (int r = 0; r < kCols; ++r) {
+          if (!ok[r]) {
+            const unsigned long long v = flag_read(slot0 + static_cast<int64_t>(jj) * kCols + r);
+            if (static_cast<uint32_t>(v >> 32) == epoch) {
+              x[r] = __uint_as_float(static_cast<uint32_t>(v));
+              ok[r] = true;
+            }
+          }
+          all = all && ok[r];
+        }
+        if (__ballot(!all) == 0 || it >= spin_limit) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    bool all = true;
+#pragma unroll
+    for (int r = 0; r < kCols; ++r) all = all && ok[r];
+    // splits whose maxima did not arrive: computed here, from K (wave-uniform loop)
+    uint64_t pending = __ballot(!all);
+    while (pending != 0) {
+      const int l = __builtin_ctzll(pending);
+      pending &= pending - 1;
+      const DecWave wp = dec_wave(a, wave_id - w.j + j0 + l, n);
+      const float mp = halves_max(split_scores_max<kPacked>(a, wp, qf, ksrc, koff, region, lane));
+#pragma unroll
+      for (int r = 0; r < kCols; ++r) {
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mp), r));
+        if (lane == l && r < nrows) x[r] = v;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kCols; ++r) mr[r] = fmaxf(mr[r], in && r < nrows ? x[r] : -INFINITY);
+  }
+  float m_run = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < kCols; ++r) {
+    if (r < nrows) {
+      const float m = wave_max_f32(mr[r]);
+      if (n == r) m_run = m * a.c1;
+    }
+  }
+  return m_run;
+}
+
+template <int LV, bool kPacked, int kCols>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void dec_fused_kernel(DecodeArgs a, uint32_t epoch, int spin_limit) {
+  static_assert(kCols == 4 || kCols == 8, "compact columns");
+  constexpr int kUnits = kCols / 4;
+  constexpr int kRegion = kStageBytes + kCols * 256;  // K or V half tile (and the scores' transfer), P^ chunks
+  __shared__ __attribute__((aligned(128))) uint8_t lds[kDecWaves * kRegion];
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31;
+  const int half = lane >> 5;
+  const int wave_id = dec_wave_id();
+  if (wave_id >= a.B * a.Hkv * a.n_rb * a.nsplit) return;
+  const DecWave w = dec_wave(a, wave_id, n);
+  uint8_t* const region = lds + (threadIdx.x >> 6) * kRegion;
+  uint8_t* const pslots = region + kStageBytes;
+  const RowSrc ksrc = k_source<kPacked>(a, w);
+  const int64_t slot = (static_cast<int64_t>(w.item) * a.nsplit + w.j) * kCols + n;
+  const bool publisher = w.live && half == 0 && n < kCols;
+
+  if (w.t_lo >= w.t_hi) {
+    // an empty split: its maxima are -inf, and its zero partial weighs 0 in the combine
+    if (publisher) flag_publish(slot, epoch, -INFINITY);
+    if (w.live) {
+      float* po = a.part_o + (static_cast<int64_t>(w.j) * a.rows_total + w.row) * kDim;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<float4*>(po + 32 * mb + 8 * j + 4 * half) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (half == 0) {
+        float* lm = a.part_lm + (static_cast<int64_t>(w.j) * a.rows_total + w.row) * 2;
+        lm[0] = 0.0f;
+        lm[1] = -INFINITY;
+      }
+    }
+    return;
+  }
+
+  bf16x8 qf[8];
+  {
+    // (columns without a row read row 0 of their head: their scores are not used)
+    const uint16_t* qp = a.q + w.b * a.q_sb + w.hq * a.q_sh + static_cast<int64_t>(w.live ? w.pos : 0) * a.q_sl + 8 * half;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) qf[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
+  }
+  // the split's one tile: S, masked, the lane maxima g (x: keys 0-63, y: 64-127 of column n)
+  const int t = w.t_lo;
+  const int key0 = t * kKeyTile;
+  floatx16 s[4];
+  {
+    const RowOffs<kPacked> koff = row_offsets<kPacked>(ksrc, lane);
+    const int krow0 = 64 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+    RowsRaw<kPacked> raw;
+    load_rows<kPacked>(ksrc, koff, a.Lk, t, 0, raw);
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      wave_lds_order();
+      store_rows<kPacked>(raw, lane, region);
+      wave_lds_order();
+      if (st == 0) load_rows<kPacked>(ksrc, koff, a.Lk, t, 1, raw);
+#pragma unroll
+      for (int kb = 2 * st; kb < 2 * st + 2; ++kb) {
+        const int pi = krow0 + 16 * kb;
+        const uint8_t* kp = region + (((pi & 31) + 32 * (pi >> 6)) * kRowUnits + half) * 16;
+        s[kb] = floatx16{};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) s[kb] = mfma32(lds_read_at(kp, 32 * c), qf[c], s[kb]);
+      }
+    }
+  }
+  const int off = a.Lk - a.Lq;
+  if (key0 + kKeyTile > a.Lk || (a.causal && key0 + kKeyTile - 1 > w.pmin + off)) {
+    const int lim = a.causal ? min(a.Lk - 1, w.pos + off) : a.Lk - 1;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (key0 + 64 * half + 16 * kb + i > lim) s[kb][i] = -INFINITY;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+  float2 g;
+  {
+    const uint32_t u = __float_as_uint(mx);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    g = make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  // the live columns' scores to the compact layout (unit: column cr + 4 u, key half ch,
+  // chunk cc) through the staged half tile's LDS, whose fragment reads were issued before
+  const int cr = lane >> 4, ch = (lane >> 3) & 1, cc = lane & 7;
+  float sx[kUnits][8];
+  {
+    float* sb = reinterpret_cast<float*>(region);
+    wave_lds_order();
+    if (n < kCols) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          *reinterpret_cast<float4*>(sb + n * kKeyTile + 64 * half + 16 * kb + 4 * u) =
+              make_float4(s[kb][4 * u], s[kb][4 * u + 1], s[kb][4 * u + 2], s[kb][4 * u + 3]);
+    }
+    wave_lds_order();
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      const bool live = dec_wave(a, wave_id, cr + 4 * u).live;
+      const float* sp = sb + (cr + 4 * u) * kKeyTile + 64 * ch + 8 * cc;
+      const float4 x0 = *reinterpret_cast<const float4*>(sp), x1 = *reinterpret_cast<const float4*>(sp + 4);
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sx[u][j] = live ? xs[j] : -INFINITY;
+    }
+  }
+  if (publisher) flag_publish(slot, epoch, fmaxf(g.x, g.y));
+  float m_run;
+  {
+    const RowOffs<kPacked> koff = row_offsets<kPacked>(ksrc, lane);
+    m_run = lookback_max<kPacked, kCols>(a, w, qf, ksrc, koff, region, wave_id, lane, epoch, spin_limit);
+  }
+  // (V loads after the look-back: its fallback needs the registers a V half tile would hold)
+  const RowSrc vsrc = v_source<kPacked>(a, w);
+  const RowOffs<kPacked> voff = row_offsets<kPacked>(vsrc, lane);
+  RowsRaw<kPacked> vr;
+  load_rows<kPacked>(vsrc, voff, a.Lk, t, 0, vr);
+
+  // the compact values pass on the tile
+  if (!w.live) g = make_float2(-INFINITY, -INFINITY);
+  const float m_new = fmaxf(m_run, fmaxf(g.x, g.y) * a.c1);
+  const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+  const float nm = -m_use;
+  // the two passes' first-tile rescale of the (zero) accumulator and l, kept so that a NaN
+  // maximum propagates the same way
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+  m_run = m_new;
+  floatx16 acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = floatx16{};
+  float l_run = 0.0f;
+  if (__ballot(alpha != 1.0f) != 0) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
+    l_run *= alpha;
+  }
+  wave_lds_order();
+#pragma unroll
+  for (int u = 0; u < kUnits; ++u) {
+    const int col = cr + 4 * u;
+    const float nmc = __shfl(nm, col, 64);
+    const float gx = __shfl(g.x, col, 64), gy = __shfl(g.y, col, 64);
+    const PQuant pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(ch ? gy : gx, a.c1, nmc)));
+    float pc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sx[u][j], a.c1, nmc));
+    pquant8<LV>(pc, pq);
+    *reinterpret_cast<bf16x8*>(pslots + (lane + 64 * u) * 16) = pack8<true>(pc);
+  }
+  wave_lds_order();
+  bf16x2_t ones2;
+  {
+    const uint32_t one2 = 0x3F803F80u;
+    __builtin_memcpy(&ones2, &one2, 4);
+  }
+  bf16x8 pb[8];
+  float rowsum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(pslots + (16 * (n & (kCols - 1)) + 8 * half + c) * 16);
+    pb[c] = n < kCols ? x : bf16x8{};
+    uint32_t wv[4];
+    __builtin_memcpy(wv, &pb[c], 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bf16x2_t pr;
+      __builtin_memcpy(&pr, &wv[i], 4);
+      rowsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, rowsum, false);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    if ((c & 3) == 0) {
+      wave_lds_order();
+      store_rows<kPacked>(vr, lane, region);
+      if ((t + 1) * kKeyTile > a.Lk) zero_tail_rows(a.Lk, t, c >> 2, lane, region);
+      wave_lds_order();
+      if (c == 0) load_rows<kPacked>(vsrc, voff, a.Lk, t, 1, vr);
+    }
+    bf16x8 va[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) va[mb] = vt_fragment(region, lane, mb, c & 3);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma32(va[mb], pb[c], acc[mb]);
+  }
+  l_run += halves_sum(rowsum);
+
+  if (w.live) {
+    float* po = a.part_o + (static_cast<int64_t>(w.j) * a.rows_total + w.row) * kDim;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<float4*>(po + 32 * mb + 8 * j + 4 * half) =
+            make_float4(acc[mb][4 * j], acc[mb][4 * j + 1], acc[mb][4 * j + 2], acc[mb][4 * j + 3]);
+    if (half == 0) {
+      float* lm = a.part_lm + (static_cast<int64_t>(w.j) * a.rows_total + w.row) * 2;
+      lm[0] = l_run;
+      lm[1] = m_run;
+    }
+  }
+}
+
 template <int LV, bool kQuantP, bool kSame>
 void launch_values(const DecodeArgs& a, int packed, dim3 grid, hipStream_t st) {
   if (packed) hipLaunchKernelGGL((dec_values_kernel<LV, kQuantP, kSame, true>), grid, dim3(256), 0, st, a);
@@ -853,6 +1217,30 @@ void launch_values_lv(const DecodeArgs& a, int packed, int quant_p, int same, di
 }
 
 }  // namespace
+
+bool decode_fused_fits(const DecodeArgs& a, int quant_p, int norm_same) {
+  return quant_p && norm_same && a.G * a.Lq <= 8 && a.tps <= kFusedMaxTps && a.ntiles <= kFusedMaxTiles &&
+         static_cast<int64_t>(a.B) * a.Hkv * a.n_rb * a.nsplit * (a.G * a.Lq <= 4 ? 4 : 8) <= kDecFlagSlots;
+}
+
+void launch_decode_fused(const DecodeArgs& a, int packed, int p_levels, uint32_t epoch, int spin_limit, hipStream_t st) {
+  const int64_t waves = static_cast<int64_t>(a.B) * a.Hkv * a.n_rb * a.nsplit;
+  const dim3 grid(static_cast<unsigned>((waves + kDecWaves - 1) / kDecWaves));
+  const bool four = a.G * a.Lq <= 4;
+  auto go = [&](auto lv) {
+    constexpr int LV = decltype(lv)::value;
+    if (packed) {
+      if (four) hipLaunchKernelGGL((dec_fused_kernel<LV, true, 4>), grid, dim3(256), 0, st, a, epoch, spin_limit);
+      else hipLaunchKernelGGL((dec_fused_kernel<LV, true, 8>), grid, dim3(256), 0, st, a, epoch, spin_limit);
+    } else {
+      if (four) hipLaunchKernelGGL((dec_fused_kernel<LV, false, 4>), grid, dim3(256), 0, st, a, epoch, spin_limit);
+      else hipLaunchKernelGGL((dec_fused_kernel<LV, false, 8>), grid, dim3(256), 0, st, a, epoch, spin_limit);
+    }
+  };
+  if (p_levels == 12) go(std::integral_constant<int, 12>{});
+  else if (p_levels == 13) go(std::integral_constant<int, 13>{});
+  else go(std::integral_constant<int, 123>{});
+}
 
 void launch_decode(const DecodeArgs& a, int packed, int quant_p, int p_levels, int norm_same, hipStream_t st) {
   const int64_t waves = static_cast<int64_t>(a.B) * a.Hkv * a.n_rb * a.nsplit;

@@ -3,7 +3,10 @@
 // caller's stream and reports errors through a thread-local message.
 #include <algorithm>
 #include <cstdarg>
+#include <atomic>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <string>
 
@@ -779,7 +782,24 @@ int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t 
   const int64_t waves = static_cast<int64_t>(B) * Hkv * a.n_rb * nsplit;
   if (waves > static_cast<int64_t>(INT32_MAX) - faq::kDecWaves) return fail(FAQ_EUNSUP, "%s: too many work items", who);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  faq::launch_decode(a, packed ? 1 : 0, quant_p, p_levels, norm_same, st);
+  // the one-pass form where it applies.  Test hooks: FAQ_DECODE_FUSED=0 keeps the two
+  // passes, =force requires the one pass (FAQ_EUNSUP where it does not apply);
+  // FAQ_DECODE_SPIN sets the look-back's wait bound (negative: every earlier split's
+  // maxima computed in the wave)
+  const char* fused_env = std::getenv("FAQ_DECODE_FUSED");
+  const bool fits = faq::decode_fused_fits(a, quant_p, norm_same);
+  if (fused_env && std::strcmp(fused_env, "force") == 0 && !fits)
+    return fail(FAQ_EUNSUP, "%s: the one-pass decode does not apply to this call", who);
+  if (!(fused_env && fused_env[0] == '0') && fits) {
+    const char* spin_env = std::getenv("FAQ_DECODE_SPIN");
+    const int spin = spin_env ? std::atoi(spin_env) : 4096;
+    static std::atomic<uint32_t> epochs{0};
+    uint32_t epoch = ++epochs;
+    if (epoch == 0) epoch = ++epochs;
+    faq::launch_decode_fused(a, packed ? 1 : 0, p_levels, epoch, spin, st);
+  } else {
+    faq::launch_decode(a, packed ? 1 : 0, quant_p, p_levels, norm_same, st);
+  }
   faq::SplitCombineArgs ca{a.part_o, a.part_lm, a.rows_total, nsplit, Hq, Lq, o, o_sb, o_sh, o_sl,
                            o_dtype == FAQ_F32, row_den};
   faq::launch_split_combine(ca, st);

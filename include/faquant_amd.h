@@ -4,8 +4,11 @@
  * Every entry point takes raw device pointers, sizes and element strides, writes into
  * caller-allocated outputs, enqueues its kernels on the given HIP stream and returns 0
  * or a negative status (FAQ_E*).  faq_last_error() returns a thread-local message for
- * the last failure on the calling thread.  No entry point allocates or keeps device
- * memory and none synchronizes the stream.  Pointers to float data must be 16-byte
+ * the last failure on the calling thread.  No entry point allocates device memory and
+ * none synchronizes the stream; the library's only device memory of its own is two
+ * file-scope arrays per GPU, loaded with the library (the scratch of
+ * faq_attention_fwd_split_noalloc, 8 MiB, and the split maxima that faq_attention_decode's
+ * one-pass form exchanges between waves, 4 MiB).  Pointers to float data must be 16-byte
  * aligned and rows must have a unit last-dimension stride.
  *
  * dtype codes: FAQ_F32 = 0, FAQ_BF16 = 1, FAQ_F16 = 2.
@@ -337,9 +340,15 @@ int faq_operand_prep_hif4_kv(const void* x, int in_dtype, int64_t sb, int64_t sh
  * give the same bits.  The query
  * heads sharing a KV head are computed together (one pass over each K/V tile for all of
  * them): a scores pass writes S and tile maxima to the workspace, a values pass runs the
- * recurrence per key range, and a combine sums the ranges.  `workspace` is device memory of
- * at least faq_attention_decode_workspace(B, Hq, Lq, Lk, nsplit) bytes, 16-byte aligned;
- * nsplit is 1..4096.  Replaces, for the decode steps of a KV cache
+ * recurrence per key range, and a combine sums the ranges.  Calls with P quantized, the
+ * quantized-same normalizer, at most 8 query rows per KV head (heads x positions), one key
+ * tile per range and at most 8192 keys run the scores and values of each range in one
+ * kernel instead (the same bits): each range publishes its maxima, stamped with a per-call
+ * epoch, to a file-scope array of the library and reads the earlier ranges' maxima from
+ * it, waiting a bounded time and otherwise computing them from K itself, so calls that
+ * overlap on one GPU stay correct.  `workspace` is device memory of at least
+ * faq_attention_decode_workspace(B, Hq, Lq, Lk, nsplit) bytes, 16-byte aligned; nsplit is
+ * 1..4096.  Replaces, for the decode steps of a KV cache
  * (src/faquant/simulated_flash_attention.py:243-289), the attention of
  * simulated_flash_attention.py:457-909.
  */

@@ -157,6 +157,61 @@ def test_decode_equals_split_path_bitwise(dev, case):
         assert_close_attention(dec_o.cpu().numpy(), ref, f"decode {case}")
 
 
+FUSED_CASES = [
+    # decode steps the one-pass kernel takes (P quantized, quantized-same, G x positions <= 8,
+    # one key tile per split, at most 64 tiles)
+    (1, 32, 8, 1, 5000, True, "quantized_same", True, "123", 40),   # G 4, ragged last tile
+    (1, 64, 8, 1, 8192, True, "quantized_same", True, "12", 64),    # G 8
+    (1, 8, 2, 2, 2000, True, "quantized_same", True, "13", 16),     # 8 columns over two positions
+    (3, 12, 4, 1, 129, True, "quantized_same", True, "123", 2),     # G 3, batch 3
+    (1, 2, 1, 1, 300, True, "quantized_same", True, "13", 16),      # empty splits past the last tile
+    (1, 40, 40, 1, 2000, False, "quantized_same", True, "123", 16), # MHA, non-causal
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"_{c[8]}_{c[9]}")
+def test_one_pass_decode_equals_two_passes_bitwise(dev, case, monkeypatch):
+    """The one-pass decode (look-back over the earlier splits' published maxima) gives the
+    two passes' output and row denominators bitwise, for bf16 and packed K/V, and so does
+    its fallback that computes every earlier split's maxima from K (wait bound < 0)."""
+    from faquant_amd import _ops
+
+    B, Hq, Hkv, Lq, Lk, causal, mode, qp, lv, nsplit = case
+    (q, k, v), (qh, kh, vh, vt), kw = _decode_inputs(case, dev)
+    kc = _ops.pack_operand(to_dev(k, dev, torch.bfloat16), levels=lv, out=_ops.PackedHiF4KV(B, Hkv, Lk, dev, lv))
+    vc = _ops.pack_operand(to_dev(v, dev, torch.bfloat16), levels=lv, out=_ops.PackedHiF4KV(B, Hkv, Lk, dev, lv))
+    print(f"[fused] {case}", flush=True)
+    for name, extra in (("bf16", dict(k=kh, v=vh)), ("packed", dict(packed=(kc, vc)))):
+        runs = {}
+        for path, env in (("two_pass", {"FAQ_DECODE_FUSED": "0"}), ("one_pass", {"FAQ_DECODE_FUSED": "force"}),
+                          ("fallback", {"FAQ_DECODE_FUSED": "force", "FAQ_DECODE_SPIN": "-1"})):
+            monkeypatch.delenv("FAQ_DECODE_FUSED", raising=False)
+            monkeypatch.delenv("FAQ_DECODE_SPIN", raising=False)
+            for key, val in env.items():
+                monkeypatch.setenv(key, val)
+            runs[path] = _run(lambda **a: _ops.attention_decode(qh, Lk, split=nsplit, **extra, **kw, **a), case, dev)
+        for path in ("one_pass", "fallback"):
+            assert torch.equal(runs[path][0], runs["two_pass"][0]), (name, path)
+            assert torch.equal(runs[path][1], runs["two_pass"][1]), (name, path)
+    # and repeated calls (new epochs over the same maxima slots) keep the bits
+    monkeypatch.setenv("FAQ_DECODE_FUSED", "force")
+    monkeypatch.delenv("FAQ_DECODE_SPIN", raising=False)
+    again = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, v=vh, split=nsplit, **kw, **a), case, dev)
+    first = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, v=vh, split=nsplit, **kw, **a), case, dev)
+    assert torch.equal(again[0], first[0]) and torch.equal(again[1], first[1])
+
+
+def test_one_pass_decode_is_refused_where_it_does_not_apply(dev, monkeypatch):
+    """The force hook reports calls outside the one pass's cases (two tiles per split)."""
+    from faquant_amd import _ops
+
+    case = (1, 32, 8, 1, 4096, True, "quantized_same", True, "123", 16)
+    (q, k, v), (qh, kh, vh, vt), kw = _decode_inputs(case, dev)
+    monkeypatch.setenv("FAQ_DECODE_FUSED", "force")
+    with pytest.raises(NotImplementedError, match="one-pass"):
+        _run(lambda **a: _ops.attention_decode(qh, 4096, k=kh, v=vh, split=16, **kw, **a), case, dev)
+
+
 def test_packed_nan_groups_match_bf16_rows(dev):
     """A NaN in K or V makes its 64-value HiF4 group NaN (E6M2 byte 0xFF in the packed
     rows): the packed decode gives NaN exactly where the bf16 rows do, and the same bits
