@@ -72,6 +72,28 @@ void launch_act(const faq::ActQdqArgs& a, int levels, int64_t threads, hipStream
   else hipLaunchKernelGGL((faq::act_qdq_rows_kernel<T, 123>), grid, dim3(256), 0, st, a);
 }
 
+template <typename T>
+void launch_act_row(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(a.rows));
+  if (levels == 12) hipLaunchKernelGGL((faq::act_row_kernel<T, 12>), grid, dim3(faq::kActRowThreads), lds, st, a);
+  else if (levels == 13) hipLaunchKernelGGL((faq::act_row_kernel<T, 13>), grid, dim3(faq::kActRowThreads), lds, st, a);
+  else hipLaunchKernelGGL((faq::act_row_kernel<T, 123>), grid, dim3(faq::kActRowThreads), lds, st, a);
+}
+
+// LDS bytes one workgroup of the current device may hold (cached per device; 64 KiB when
+// the query fails).
+size_t device_lds_per_block() {
+  static size_t cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) v = 65536;
+    cached[dev] = static_cast<size_t>(v);
+  }
+  return cached[dev];
+}
+
 template <typename Tin, typename Tround>
 void launch_prep(const faq::OperandPrepArgs& a, int levels, int64_t, hipStream_t st) {
   const int per_block = 16 * faq::kPrepRows;
@@ -454,6 +476,61 @@ int faq_act_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dty
   else if (dtype == FAQ_BF16) launch_act<__hip_bfloat16>(a, levels, threads, st);
   else launch_act<__half>(a, levels, threads, st);
   return check_launch("faq_act_qdq_rows");
+}
+
+int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const faq_act_opts* opts,
+                      int levels, faq_stream_t stream) {
+  const char* who = "faq_act_prep_rows";
+  if (!x || !y) return fail(FAQ_EINVAL, "%s: null input or output", who);
+  if (rows < 0) return fail(FAQ_EINVAL, "%s: negative size", who);
+  if (!valid_dtype(dtype)) return fail(FAQ_EINVAL, "%s: bad dtype", who);
+  if (levels != 0 && !valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
+  if (cols <= 0) return fail(FAQ_EINVAL, "HiF4 fake quantization does not support an empty axis");
+  if (cols % 64) return fail(FAQ_EUNSUP, "%s: row width must be a multiple of 64", who);
+  if (cols > faq::kActMaxCols) return fail(FAQ_EUNSUP, "%s: at most %d features per row", who, faq::kActMaxCols);
+  if (rows > 0x7FFFFFFF) return fail(FAQ_EUNSUP, "%s: too many rows", who);
+  if (!aligned16(x) || !aligned16(y)) return fail(FAQ_EINVAL, "%s: pointers must be 16-byte aligned", who);
+  faq_act_opts o{};
+  if (opts) o = *opts;
+  auto check_block = [&](int b) -> int {
+    if (b == 0) return FAQ_OK;
+    if (b < 2 || (b & (b - 1))) return fail(FAQ_EINVAL, "Hadamard dimension must be a power of two, got %d", b);
+    if (cols % b)
+      return fail(FAQ_EINVAL, "dimension %lld must be divisible by power-of-two block_size=%d", static_cast<long long>(cols), b);
+    return FAQ_OK;
+  };
+  if (o.rot_signs && !o.rot_perm) return fail(FAQ_EINVAL, "%s: a rotation needs both signs and permutation", who);
+  if (!o.rot_signs && (o.rot_perm || o.rot_block)) return fail(FAQ_EINVAL, "%s: a rotation needs both signs and permutation", who);
+  if (int st = check_block(o.rot_block)) return st;
+  if (int st = check_block(o.hadamard)) return st;
+  if (rows == 0) return FAQ_OK;
+  faq::ActRowArgs a{};
+  a.x = x;
+  a.y = y;
+  a.rows = rows;
+  a.cols = static_cast<int>(cols);
+  a.col_scale = o.col_scale;
+  a.rot_signs = o.rot_signs;
+  a.rot_perm = o.rot_perm;
+  a.rot_block = o.rot_block;
+  a.rot_div = sqrt_div(o.rot_block);
+  a.has_min = o.has_min != 0;
+  a.has_max = o.has_max != 0;
+  a.act_min = o.act_min;
+  a.act_max = o.act_max;
+  a.compand = o.compand;
+  a.n = o.hadamard;
+  a.div = sqrt_div(o.hadamard);
+  a.quant = levels != 0;
+  const size_t lds = faq::act_row_lds_bytes(a.cols, a.rot_signs != nullptr);
+  if (lds > device_lds_per_block())
+    return fail(FAQ_EUNSUP, "%s: a row of %lld features with a rotation needs %zu bytes of LDS, the device has %zu", who,
+                static_cast<long long>(cols), lds, device_lds_per_block());
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FAQ_F32) launch_act_row<float>(a, levels, lds, st);
+  else if (dtype == FAQ_BF16) launch_act_row<__hip_bfloat16>(a, levels, lds, st);
+  else launch_act_row<__half>(a, levels, lds, st);
+  return check_launch(who);
 }
 
 int faq_operand_prep(const void* x, int in_dtype, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,

@@ -510,6 +510,137 @@ __global__ __launch_bounds__(256) void act_qdq_rows_kernel(ActQdqArgs a) {
   if (have) Io<T>::store8(y + c0, v);
 }
 
+// ------------------------------------------------------------------ full activation path
+
+// The whole activation path of FakeQuantLinear.forward (quantization.py:199-276) for a row
+// that fits LDS: x * dtype(input_scale); the HiSQ input rotation (quantization.py:201-219:
+// fp32 x times the signs, gathered by the permutation, the per-block fp32 Hadamard of
+// rotation.py:117-135 when a block size is set, one cast back); the activation clamp (bounds
+// in the input dtype, NaN kept); x * companding scale; the online block Hadamard with one
+// cast back; the HiF4 QDQ; x / companding scale.  Every elementwise step rounds to the input
+// dtype as torch does.  One 256-thread workgroup per row, the row in LDS as fp32.
+constexpr int kActRowThreads = 256;
+constexpr int kActMaxCols = 16384;
+
+struct ActRowArgs {
+  const void* x;            // [rows, cols] contiguous, dtype T
+  void* y;                  // [rows, cols] contiguous, dtype T
+  int64_t rows;
+  int cols;                 // multiple of 64, at most kActMaxCols
+  const float* col_scale;   // [cols] input scale, or null
+  const int8_t* rot_signs;  // [cols] +1 / -1, or null: no rotation
+  const int32_t* rot_perm;  // [cols] gather order (index_select), values in [0, cols)
+  int rot_block;            // 0, or the rotation's block Hadamard size (power of two dividing cols)
+  SqrtDiv rot_div;
+  int has_min, has_max;
+  float act_min, act_max;   // clamp bounds (rounded to T in the kernel)
+  const float* compand;     // [cols] companding scale (values of T), or null
+  int n;                    // 0, or the online block Hadamard size
+  SqrtDiv div;
+  int quant;                // 1: HiF4 QDQ
+};
+
+// v / fp32(sqrt(n)), correctly rounded (div_sqrt_n for one value)
+__device__ __forceinline__ float div_sqrt_1(float v, const SqrtDiv& s) {
+  if (s.pow2) return v * s.r;
+  const float q = v * s.r;
+  const float e = __builtin_fmaf(-q, s.d, v);
+  const float y = __builtin_fmaf(e, s.r, q);
+  const float m = fabsf(v);
+  return (m >= 0x1p-105f && m <= 3.40282347e38f) ? y : v / s.d;
+}
+
+// Normalized Walsh-Hadamard transform of every b-block of the LDS row buf[0, cols): stages
+// of stride 1, 2, ..., b/2 writing (left + right, left - right), then the division by
+// fp32(sqrt(b)) (rotation.py:14-29).  Ends with the row written and visible to the block.
+__device__ __forceinline__ void lds_fwht(float* buf, int cols, int b, const SqrtDiv& dv, int tid) {
+  for (int s = 1; s < b; s <<= 1) {
+    __syncthreads();
+    for (int q = tid; q < cols / 2; q += kActRowThreads) {
+      const int i = (q / s) * 2 * s + (q % s);
+      const float l = buf[i], r = buf[i + s];
+      buf[i] = l + r;
+      buf[i + s] = l - r;
+    }
+  }
+  __syncthreads();
+  for (int j = tid; j < cols; j += kActRowThreads) buf[j] = div_sqrt_1(buf[j], dv);
+}
+
+// LDS: the row as fp32 in [0, cols), and with a rotation a second row for the gather,
+// act_row_lds_bytes() in all (dynamic shared memory).
+__host__ __device__ constexpr size_t act_row_lds_bytes(int cols, bool rotate) {
+  return static_cast<size_t>(rotate ? 2 : 1) * static_cast<size_t>(cols) * sizeof(float);
+}
+
+template <typename T, int LV>
+__global__ __launch_bounds__(kActRowThreads) void act_row_kernel(ActRowArgs a) {
+  extern __shared__ float act_row_lds[];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const T* x = static_cast<const T*>(a.x) + row * a.cols;
+  T* y = static_cast<T*>(a.y) + row * a.cols;
+  float* cur = act_row_lds;
+  for (int c0 = 8 * tid; c0 < a.cols; c0 += 8 * kActRowThreads) {
+    float v[8];
+    Io<T>::load8(x + c0, v);
+    if (a.col_scale) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(v[i] * Io<T>::round(a.col_scale[c0 + i]));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cur[c0 + i] = v[i];
+  }
+  // every later pass reads values that other lanes wrote
+  __syncthreads();
+  if (a.rot_signs) {
+    float* nxt = act_row_lds + a.cols;
+    for (int j = tid; j < a.cols; j += kActRowThreads) {
+      const int p = min(max(a.rot_perm[j], 0), a.cols - 1);  // (a valid permutation stays in range)
+      nxt[j] = cur[p] * static_cast<float>(a.rot_signs[p]);
+    }
+    cur = nxt;
+    if (a.rot_block) lds_fwht(cur, a.cols, a.rot_block, a.rot_div, tid);
+  }
+  // one cast back after the rotation, the clamp and the companding product, in place; each
+  // lane reads the entries it wrote last (the same j mapping)
+  const float lo = Io<T>::round(a.act_min), hi = Io<T>::round(a.act_max);
+  for (int j = tid; j < a.cols; j += kActRowThreads) {
+    float v = cur[j];
+    if (a.rot_signs) v = Io<T>::round(v);
+    if (!__builtin_isnan(v)) {
+      if (a.has_min) v = fmaxf(v, lo);
+      if (a.has_max) v = fminf(v, hi);
+    }
+    if (a.compand) v = Io<T>::round(v * a.compand[j]);
+    cur[j] = v;
+  }
+  if (a.n) {
+    lds_fwht(cur, a.cols, a.n, a.div, tid);
+    for (int j = tid; j < a.cols; j += kActRowThreads) cur[j] = Io<T>::round(cur[j]);
+  }
+  __syncthreads();
+  // QDQ: 8 values per lane, a 64-value group on 8 consecutive lanes; every lane takes part
+  // in every round (zeros past the row), as qdq8 exchanges values within its 8 lanes
+  const int rounds = (a.cols + 8 * kActRowThreads - 1) / (8 * kActRowThreads);
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int c0 = 8 * (tid + rd * kActRowThreads);
+    const bool have = c0 < a.cols;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = have ? cur[c0 + i] : 0.0f;
+    if (a.quant) qdq8<LV>(v);
+    if (have) {
+      if (a.compand) {
+        // the quantized tensor is in T before torch divides it
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(Io<T>::round(v[i]) / a.compand[c0 + i]);
+      }
+      Io<T>::store8(y + c0, v);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ operand prologue
 
 struct OperandPrepArgs {

@@ -59,6 +59,26 @@ class HiF4KV(ctypes.Structure):
 
 _kv_p = ctypes.POINTER(HiF4KV)
 
+
+class ActOpts(ctypes.Structure):
+    """``faq_act_opts``: the optional steps of the full Linear activation path."""
+
+    _fields_ = [
+        ("col_scale", _vp),
+        ("rot_signs", _vp),
+        ("rot_perm", _vp),
+        ("rot_block", _c_int),
+        ("has_min", _c_int),
+        ("has_max", _c_int),
+        ("act_min", _c_float),
+        ("act_max", _c_float),
+        ("compand", _vp),
+        ("hadamard", _c_int),
+    ]
+
+
+_act_opts_p = ctypes.POINTER(ActOpts)
+
 _SIGNATURES = {
     "faq_last_error": ([], ctypes.c_char_p),
     "faq_version": ([], ctypes.c_char_p),
@@ -69,6 +89,7 @@ _SIGNATURES = {
     "faq_hadamard_rows": ([_vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp], _c_int),
     "faq_hadamard_rows_native": ([_vp, _vp, _c_i64, _c_i64, _c_int, _vp], _c_int),
     "faq_act_qdq_rows": ([_vp, _vp, _c_i64, _c_i64, _c_int, _vp, _c_int, _c_int, _vp], _c_int),
+    "faq_act_prep_rows": ([_vp, _vp, _c_i64, _c_i64, _c_int, _act_opts_p, _c_int, _vp], _c_int),
     "faq_hif4_unpack_rows": ([_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _vp, _vp], _c_int),
     "faq_operand_prep": (
         [

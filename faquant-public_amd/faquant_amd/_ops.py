@@ -127,6 +127,69 @@ def hadamard_rows_native(x: torch.Tensor) -> torch.Tensor:
     return y.view(x.shape)
 
 
+def act_prep_rows(
+    x: torch.Tensor,
+    *,
+    levels: str | None,
+    col_scale: torch.Tensor | None = None,
+    rot_signs: torch.Tensor | None = None,
+    rot_perm: torch.Tensor | None = None,
+    rot_block: int | None = None,
+    act_min: float | None = None,
+    act_max: float | None = None,
+    compand: torch.Tensor | None = None,
+    hadamard: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The full activation path of a quantized Linear along the last axis of ``x``
+    (faq_act_prep_rows): x * dtype(col_scale); the HiSQ input rotation (fp32 x times
+    ``rot_signs``, gathered by ``rot_perm``, the per-block fp32 Hadamard of ``rot_block``
+    values when set, one cast back); the clamp to [act_min, act_max] in x's dtype; x times
+    ``compand`` (already in x's dtype); the online block Hadamard; HiF4 QDQ with
+    ``levels``; x / ``compand``.  Output in x's dtype."""
+    _lib.require_device(x, col_scale, rot_signs, rot_perm, compand)
+    lib = _lib.load()
+    if x.ndim == 0:
+        raise ValueError("HiF4 fake quantization requires at least one dimension")
+    cols = x.shape[-1]
+    xc = x.contiguous()
+    rows = xc.numel() // cols if cols else 0
+    y = torch.empty_like(xc) if out is None else out
+    keep = []
+
+    def vec(t, dtype, name):
+        if t is None:
+            return None
+        v = t.to(device=x.device, dtype=dtype).reshape(-1).contiguous()
+        if v.numel() != cols:
+            raise ValueError(f"{name} must hold {cols} values, got {v.numel()}")
+        keep.append(v)
+        return v.data_ptr()
+
+    if (rot_signs is None) != (rot_perm is None):
+        raise ValueError("the input rotation needs both signs and permutation")
+    opts = _lib.ActOpts(
+        col_scale=vec(col_scale, torch.float32, "input scale"),
+        rot_signs=vec(rot_signs, torch.int8, "rotation signs"),
+        rot_perm=vec(rot_perm, torch.int32, "rotation permutation"),
+        rot_block=int(rot_block or 0),
+        has_min=int(act_min is not None),
+        has_max=int(act_max is not None),
+        act_min=float(act_min) if act_min is not None else 0.0,
+        act_max=float(act_max) if act_max is not None else 0.0,
+        compand=vec(compand, torch.float32, "companding scale"),
+        hadamard=int(hadamard or 0),
+    )
+    _lib.check(
+        lib.faq_act_prep_rows(
+            xc.data_ptr(), y.data_ptr(), rows, cols, _lib.dtype_code(x.dtype), ctypes.byref(opts),
+            int(levels) if levels else 0, _lib.stream_ptr(x.device),
+        )
+    )
+    del keep
+    return y.view(x.shape)
+
+
 def act_qdq_rows(
     x: torch.Tensor,
     *,

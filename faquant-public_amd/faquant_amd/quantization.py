@@ -53,11 +53,15 @@ class FakeQuantLinear(torch.nn.Module):
 
     Drop-in for faquant.quantization.FakeQuantLinear (quantization.py:97-276) on the
     HiF4 path: the weight is quantized once at construction (levels
-    FAQUANT_HIF4_SCALE_LEVELS); each forward runs the activation prologue in one HIP
-    launch (``input_scale`` in the input dtype, the online block Hadamard in fp32 with one
-    cast back, the HiF4 QDQ with the ACT levels), then ``F.linear`` on the HiF4-exact
-    operands.  The input rotation (signs/permutation), activation clamp, companding and the
-    generalized (non-block) online Hadamard raise NotImplementedError.
+    FAQUANT_HIF4_SCALE_LEVELS); each forward runs the activation path in one HIP launch,
+    then ``F.linear`` on the HiF4-exact operands.  Without the HiSQ input rotation,
+    clamp or companding that launch is ``act_qdq_rows`` (``input_scale`` in the input
+    dtype, the online block Hadamard in fp32 with one cast back, the HiF4 QDQ with the ACT
+    levels); with any of them it is ``act_prep_rows``, which adds the rotation (signs,
+    permutation, block Hadamard; quantization.py:201-219), the clamp and the companding
+    product and quotient around the QDQ (quantization.py:220-276).  The companding scale
+    is computed with torch as the reference computes it (clamp to +-2.079, exp, cast to the
+    input dtype).  The generalized (non-block) online Hadamard raises NotImplementedError.
     """
 
     faquant_quantizes_input = True
@@ -91,12 +95,8 @@ class FakeQuantLinear(torch.nn.Module):
             )
         check_hif4_arguments(bits=bits, group_size=weight_group_size, symmetric=symmetric, clip_ratio=clip_ratio)
         check_hif4_arguments(bits=bits, group_size=activation_group_size, symmetric=symmetric, clip_ratio=clip_ratio)
-        if input_rotation_signs is not None or input_rotation_permutation is not None:
-            raise NotImplementedError("the HiSQ input rotation is not implemented on the MI355X")
-        if activation_min is not None or activation_max is not None:
-            raise NotImplementedError("activation clamping is not implemented on the MI355X")
-        if activation_compand_log_scale is not None:
-            raise NotImplementedError("activation companding is not implemented on the MI355X")
+        if (input_rotation_signs is None) != (input_rotation_permutation is None):
+            raise ValueError("the input rotation needs both signs and permutation")
         if online_hadamard and online_hadamard_block_size is None:
             raise NotImplementedError("the generalized (non-block) online Hadamard is not implemented on the MI355X")
         self.in_features = linear.in_features
@@ -110,9 +110,29 @@ class FakeQuantLinear(torch.nn.Module):
         self.online_hadamard_block_size = online_hadamard_block_size
         self.input_rotation_block_size = input_rotation_block_size
         self.register_buffer("input_scale", None if input_scale is None else input_scale.detach().float().clone())
-        for name in ("input_rotation_signs", "input_rotation_permutation", "activation_min", "activation_max",
-                     "activation_compand_log_scale"):
-            self.register_buffer(name, None)
+        self.register_buffer(
+            "input_rotation_signs",
+            None if input_rotation_signs is None else input_rotation_signs.detach().to(torch.int8).clone(),
+        )
+        self.register_buffer(
+            "input_rotation_permutation",
+            None if input_rotation_permutation is None else input_rotation_permutation.detach().long().clone(),
+        )
+        if self.input_rotation_permutation is not None:
+            perm = self.input_rotation_permutation.reshape(-1)
+            if perm.numel() != self.in_features or not torch.equal(
+                    torch.sort(perm.cpu()).values, torch.arange(self.in_features)):
+                raise ValueError("the input rotation permutation must be a permutation of the input features")
+        self.register_buffer(
+            "activation_min", None if activation_min is None else torch.as_tensor(activation_min).detach().float().clone()
+        )
+        self.register_buffer(
+            "activation_max", None if activation_max is None else torch.as_tensor(activation_max).detach().float().clone()
+        )
+        self.register_buffer(
+            "activation_compand_log_scale",
+            None if activation_compand_log_scale is None else activation_compand_log_scale.detach().float().clone(),
+        )
         weight = linear.weight.detach() if weight_override is None else weight_override.detach()
         if quantize_weight:
             from .hif4 import HIF4_SCALE_LEVELS
@@ -133,5 +153,23 @@ class FakeQuantLinear(torch.nn.Module):
         from .hif4 import HIF4_ACT_SCALE_LEVELS
 
         block = self.online_hadamard_block_size if self.online_hadamard else 0
-        xq = _ops.act_qdq_rows(x, levels=HIF4_ACT_SCALE_LEVELS, hadamard=int(block or 0), col_scale=self.input_scale)
+        extra = (self.input_rotation_signs is not None or self.activation_min is not None
+                 or self.activation_max is not None or self.activation_compand_log_scale is not None)
+        if not extra:
+            xq = _ops.act_qdq_rows(x, levels=HIF4_ACT_SCALE_LEVELS, hadamard=int(block or 0), col_scale=self.input_scale)
+        else:
+            compand = None
+            if self.activation_compand_log_scale is not None:
+                log_scale = self.activation_compand_log_scale
+                if log_scale.numel() != self.in_features:
+                    if self.in_features % log_scale.numel():
+                        raise RuntimeError("invalid activation companding shape")
+                    log_scale = log_scale.repeat_interleave(self.in_features // log_scale.numel())
+                compand = log_scale.clamp(-2.079, 2.079).exp().to(device=x.device, dtype=x.dtype)
+            xq = _ops.act_prep_rows(
+                x, levels=HIF4_ACT_SCALE_LEVELS, col_scale=self.input_scale, rot_signs=self.input_rotation_signs,
+                rot_perm=self.input_rotation_permutation, rot_block=self.input_rotation_block_size,
+                act_min=None if self.activation_min is None else float(self.activation_min),
+                act_max=None if self.activation_max is None else float(self.activation_max),
+                compand=compand, hadamard=int(block or 0))
         return torch.nn.functional.linear(_lib.forward_only(xq, x), self.weight, self.bias)

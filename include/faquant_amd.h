@@ -57,6 +57,9 @@
  *   faq_attention_decode_workspace  workspace size of faq_attention_decode
  *   faq_pquant_groups     the in-register P quantizer of faq_attention_fwd on given values
  *                         (simulated_flash_attention.py:801-806 via hif4.py:143-271)
+ *   faq_act_prep_rows     quantization.py:199-276 (the full FakeQuantLinear activation path:
+ *                         input scale, HiSQ rotation, clamp, companding, online Hadamard,
+ *                         HiF4 QDQ), hisq_rotation.py:50-71
  *   faq_mfma_probe        no reference counterpart: a measurement helper (the device's
  *                         sustained bf16 MFMA rate, the reference point of the benchmark)
  *   faq_stream_probe      no reference counterpart: a measurement helper (the device's
@@ -163,6 +166,37 @@ int faq_hif4_unpack_rows(const uint8_t* codes, const uint8_t* scale_byte, const 
  */
 int faq_act_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const float* col_scale,
                      int hadamard, int levels, faq_stream_t stream);
+
+/*
+ * Options of faq_act_prep_rows, each absent when NULL / 0.  Vectors hold one value per
+ * feature (cols).
+ */
+typedef struct faq_act_opts {
+  const float* col_scale;   /* input scale (multiplied in the input dtype) */
+  const int8_t* rot_signs;  /* HiSQ input rotation: signs (+1 / -1) ... */
+  const int32_t* rot_perm;  /* ... and the permutation (index_select order, a permutation of 0..cols-1) */
+  int rot_block;            /* the rotation's block Hadamard size, or 0 for none */
+  int has_min, has_max;     /* activation clamp bounds present */
+  float act_min, act_max;   /* the bounds (applied in the input dtype, NaN kept) */
+  const float* compand;     /* activation companding scale, already in the input dtype */
+  int hadamard;             /* online block Hadamard size, or 0 */
+} faq_act_opts;
+
+/*
+ * The whole activation path of a quantized Linear, as FakeQuantLinear.forward runs it
+ * (src/faquant/quantization.py:199-276): x * input_scale, the HiSQ input rotation (fp32 x
+ * times the signs, gathered by the permutation, the per-block fp32 Hadamard of
+ * rotation.py:117-135 when rot_block is set, one cast back; quantization.py:201-219 and
+ * hisq_rotation.py:50-71), the activation clamp, x * companding scale, the online block
+ * Hadamard with one cast back, the HiF4 QDQ with `levels` (0: none), and x / companding
+ * scale; each elementwise step rounds to the input dtype.  Rows of at most 16384 features
+ * (a multiple of 64), contiguous, fp32 / bf16 / fp16; one workgroup per row holding the row
+ * in LDS as fp32 (4 bytes a feature, 8 with a rotation; FAQ_EUNSUP beyond the device's LDS
+ * per workgroup).  opts may be NULL (then this is faq_act_qdq_rows without input scale or
+ * Hadamard).
+ */
+int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const faq_act_opts* opts,
+                      int levels, faq_stream_t stream);
 
 /*
  * V operand: x [B, H, L, 128] (strides sb, sh, sl), HiF4 QDQ with `levels` (0 = none),

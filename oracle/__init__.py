@@ -12,5 +12,7 @@ Modules:
                 code/metadata view of the same result.
   hadamard   -- normalized Sylvester-order fast Walsh-Hadamard transform.
   attention  -- tiled online-softmax attention simulator with Q/K/P/V quantization.
+  linear     -- the quantized Linear's activation path (input scale, HiSQ rotation,
+                clamp, companding, online Hadamard, HiF4 QDQ).
   inputs     -- seeded, version-stable synthetic inputs (PCG64) for tests and bench.
 """

@@ -22,8 +22,14 @@ Fixtures (numpy .npz, float32 unless noted):
                       configuration shapes listed in CASES.
   hadamard_native.npz hadamard_transform on bf16 and fp16 tensors (the butterflies run
                       in the tensor's dtype, each stage rounded), n = 8, 64, 128, 512.
+  linear_act.npz      the activation FakeQuantLinear.forward hands to F.linear (F.linear
+                      replaced by the identity while it runs): input scale, HiSQ rotation
+                      from derive_hisq_rotation with and without its block Hadamard,
+                      clamp, companding and the online block Hadamard, in bf16, fp16 and
+                      fp32.  Inputs and options are stored with the output.
 
-``python tests/golden/make_golden.py hadamard_native`` writes only that file.
+``python tests/golden/make_golden.py hadamard_native`` (or ``linear_act``) writes only that
+file.
 """
 
 from __future__ import annotations
@@ -213,17 +219,95 @@ def make_hadamard_native() -> dict[str, np.ndarray]:
     return out
 
 
+# name: (dtype, cols, rows, input_scale, rotation block (None: signs and permutation only;
+# 0: no rotation), clamp (min, max), companding log-scale length (0: none), online block)
+LINEAR_ACT_CASES = {
+    "bf16_rot1024": ("bfloat16", 1024, 16, False, 1024, (None, None), 0, 0),
+    "bf16_perm_clamp_comp_h64": ("bfloat16", 2048, 24, True, None, (-3.3, 2.7), 32, 64),
+    "fp32_all_h128": ("float32", 512, 12, True, 256, (None, 1.9), 512, 128),
+    "bf16_4096_all": ("bfloat16", 4096, 8, True, 1024, (-6.1, 5.2), 32, 4096),
+    "fp16_768_rot256_comp": ("float16", 768, 10, False, 256, (None, None), 12, 0),
+    "bf16_clamp_only": ("bfloat16", 640, 9, False, 0, (-0.7, 0.45), 0, 0),
+}
+
+
+def make_linear_act() -> dict[str, np.ndarray]:
+    """FakeQuantLinear.forward up to F.linear (quantization.py:199-276)."""
+    from faquant import quantization as ref_quant
+    from faquant.hif4 import HIF4_ACT_SCALE_LEVELS
+    from faquant.hisq_rotation import derive_hisq_rotation
+
+    out: dict[str, np.ndarray] = {"levels": np.array(HIF4_ACT_SCALE_LEVELS)}
+    seen = {}
+    real_f = ref_quant.F
+    ref_quant.F = SimpleNamespace(linear=lambda x, w, b: seen.setdefault("x", x.clone()))
+    try:
+        for k, (case, spec) in enumerate(LINEAR_ACT_CASES.items()):
+            dt_name, n, rows, with_scale, rblock, (lo, hi), comp_len, online = spec
+            dt = getattr(torch, dt_name)
+            g = inputs.rng(100 + k)
+            x = g.standard_normal((rows, n)) * g.uniform(0.05, 4.0, size=(rows, 1))
+            x[g.integers(0, rows, 6), g.integers(0, n, 6)] *= 40.0  # outliers
+            xt = torch.from_numpy(x.astype(np.float32)).to(dt)
+            kw = {}
+            if with_scale:
+                kw["input_scale"] = torch.from_numpy(g.uniform(0.25, 3.0, n).astype(np.float32))
+            if rblock != 0:
+                rot = derive_hisq_rotation(f"model.layers.{k}.mlp.down_proj", n, block_size=rblock or n)
+                kw["input_rotation_signs"] = rot.signs
+                kw["input_rotation_permutation"] = rot.permutation
+                kw["input_rotation_block_size"] = rblock
+            if lo is not None:
+                kw["activation_min"] = lo
+            if hi is not None:
+                kw["activation_max"] = hi
+            if comp_len:
+                kw["activation_compand_log_scale"] = torch.from_numpy(g.uniform(-3.0, 3.0, comp_len).astype(np.float32))
+            lin = torch.nn.Linear(n, n, bias=False).to(dt)
+            mod = ref_quant.FakeQuantLinear(
+                lin, quant_format="hif4", bits=4, weight_group_size=64, activation_group_size=64,
+                symmetric=True, clip_ratio=1.0, quantize_weight=False,
+                online_hadamard=bool(online), online_hadamard_block_size=online or None, **kw,
+            )
+            seen.clear()
+            mod(xt)
+            out[f"{case}__x"] = xt.float().numpy()
+            out[f"{case}__y"] = seen["x"].float().numpy()
+            out[f"{case}__dtype"] = np.array(dt_name)
+            for key, val in kw.items():
+                if isinstance(val, torch.Tensor):
+                    out[f"{case}__{key}"] = val.numpy()
+                else:  # a block size (0 for None) or a bound
+                    out[f"{case}__{key}"] = np.array(0 if val is None else val)
+            out[f"{case}__online"] = np.array(online)
+            if comp_len:
+                # the companding scale forward multiplies by, recomputed by the same expression
+                # on the same tensor: torch's CPU exp differs between vector units, so the
+                # fixture carries the values the reference used
+                ls = mod.activation_compand_log_scale
+                if ls.numel() != n:
+                    ls = ls.repeat_interleave(n // ls.numel())
+                out[f"{case}__compand_scale"] = ls.clamp(-2.079, 2.079).exp().to(dt).float().numpy()
+            print(f"linear_act {case}: {tuple(xt.shape)} {dt_name} {sorted(kw)} online={online}")
+    finally:
+        ref_quant.F = real_f
+    return out
+
+
 def main() -> None:
     torch.set_num_threads(os.cpu_count() or 1)
-    if sys.argv[1:] == ["hadamard_native"]:
-        np.savez_compressed(os.path.join(HERE, "hadamard_native.npz"), **make_hadamard_native())
-        print("hadamard_native.npz", os.path.getsize(os.path.join(HERE, "hadamard_native.npz")))
+    if sys.argv[1:] in (["hadamard_native"], ["linear_act"]):
+        name = sys.argv[1]
+        make = make_hadamard_native if name == "hadamard_native" else make_linear_act
+        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **make())
+        print(f"{name}.npz", os.path.getsize(os.path.join(HERE, f"{name}.npz")))
         return
     np.savez_compressed(os.path.join(HERE, "hif4_codec.npz"), **make_codec())
     np.savez_compressed(os.path.join(HERE, "hadamard.npz"), **make_hadamard())
     np.savez_compressed(os.path.join(HERE, "attention.npz"), **make_attention())
     np.savez_compressed(os.path.join(HERE, "hadamard_native.npz"), **make_hadamard_native())
-    for name in ("hif4_codec.npz", "hadamard.npz", "attention.npz", "hadamard_native.npz"):
+    np.savez_compressed(os.path.join(HERE, "linear_act.npz"), **make_linear_act())
+    for name in ("hif4_codec.npz", "hadamard.npz", "attention.npz", "hadamard_native.npz", "linear_act.npz"):
         print(name, os.path.getsize(os.path.join(HERE, name)))
 
 

@@ -1,15 +1,19 @@
 """HiF4 W4A4 Linear: the fused activation prologue and the Linear drop-ins.
 
-The activation path of FakeQuantLinear.forward (quantization.py:204-276) is
-x * dtype(input_scale) in the input dtype, the per-block fp32 Hadamard
-(rotation.py:117-135, true division by sqrt(n)) cast back to the input dtype, then
-fake_quantize (HiF4, ACT levels) in that dtype.  The oracle restates each step
-(pinned against the reference's codec and Hadamard goldens), so the fused kernel is
-compared with it bit for bit; the Linear drop-ins are compared with the reference's
-composition of those steps and F.linear.
+The activation path of FakeQuantLinear.forward (quantization.py:199-276) is
+x * dtype(input_scale) in the input dtype, the HiSQ input rotation, the clamp,
+the companding product, the per-block fp32 Hadamard (rotation.py:117-135, true
+division by sqrt(n)) cast back to the input dtype, fake_quantize (HiF4, ACT levels)
+in that dtype and the companding quotient.  The oracles restate each step (pinned
+against the reference's codec, Hadamard and FakeQuantLinear goldens), so the kernels
+are compared with them bit for bit, and with the reference-written activations
+directly; the Linear drop-ins are compared with the reference's composition of
+those steps and F.linear.
 """
 
 from __future__ import annotations
+
+import zlib
 
 import numpy as np
 import pytest
@@ -100,11 +104,158 @@ def test_fake_quant_linear_unsupported_options_raise(dev):
     common = dict(quant_format="hif4", bits=4, weight_group_size=64, activation_group_size=64, symmetric=True,
                   clip_ratio=1.0)
     with pytest.raises(NotImplementedError):
-        FakeQuantLinear(lin, **common, activation_min=-1.0)
-    with pytest.raises(NotImplementedError):
         FakeQuantLinear(lin, **common, online_hadamard=True)
     with pytest.raises(ValueError):
         FakeQuantLinear(lin, **{**common, "weight_group_size": 32})
+    with pytest.raises(ValueError, match="signs and permutation"):
+        FakeQuantLinear(lin, **common, input_rotation_signs=torch.ones(64, dtype=torch.int8))
+    with pytest.raises(ValueError, match="permutation of the input features"):
+        FakeQuantLinear(lin, **common, input_rotation_signs=torch.ones(64, dtype=torch.int8),
+                        input_rotation_permutation=torch.zeros(64, dtype=torch.long))
+
+
+# ---------------------------------------------------------------- the full activation path
+
+_TORCH_DT = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+
+
+def _prep_on_device(x, dtype, dev, levels, kw):
+    """oracle.linear keyword arguments -> _ops.act_prep_rows on the device."""
+    from faquant_amd import _ops
+
+    def t(a, dt=torch.float32):
+        return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dt)
+
+    return _ops.act_prep_rows(
+        to_dev(x, dev, _TORCH_DT[dtype]), levels=levels, col_scale=t(kw.get("input_scale")),
+        rot_signs=t(kw.get("rot_signs"), torch.int8), rot_perm=t(kw.get("rot_perm"), torch.int64),
+        rot_block=kw.get("rot_block"), act_min=kw.get("act_min"), act_max=kw.get("act_max"),
+        compand=t(kw.get("compand")), hadamard=kw.get("hadamard", 0),
+    )
+
+
+def _same(got, ref):
+    return np.array_equal(np.asarray(got, np.float32), np.asarray(ref, np.float32), equal_nan=True)
+
+
+def test_act_prep_rows_matches_reference_fixtures(dev):
+    """The reference's FakeQuantLinear wrote these activations (tests/golden/linear_act.npz)."""
+    from oracle import linear as OL
+    from tests.linear_cases import golden_cases
+
+    for name, c in sorted(golden_cases().items()):
+        print(f"[act_prep golden] {name}", flush=True)
+        got = _prep_on_device(c["x"], c["dtype"], dev, c["levels"], c["kw"]).float().cpu().numpy()
+        assert _same(got, c["y"]), name
+        assert _same(got, OL.fake_quant_linear_input(c["x"], c["dtype"], levels=c["levels"], **c["kw"]))
+
+
+def _random_prep_case(seed, cols, dtype, *, rot, rot_block, clamp, comp, hadamard, scale):
+    from tests.linear_cases import compand_scale
+
+    g = OI.rng(seed)
+    rows = 13
+    x = g.standard_normal((rows, cols)) * np.exp(g.standard_normal((rows, 1)))
+    x[g.integers(0, rows, 5), g.integers(0, cols, 5)] *= 30.0
+    x[2, 64:192] = 0.0
+    x = OQ.bf16_round(x) if dtype == "bfloat16" else (
+        x.astype(np.float16).astype(np.float32) if dtype == "float16" else x.astype(np.float32))
+    kw = {"hadamard": hadamard}
+    if scale:
+        kw["input_scale"] = g.uniform(0.3, 3.0, cols).astype(np.float32)
+    if rot:
+        kw["rot_signs"] = g.choice(np.array([-1, 1], np.int8), cols)
+        kw["rot_perm"] = g.permutation(cols)
+        kw["rot_block"] = rot_block
+    if clamp:
+        kw["act_min"], kw["act_max"] = -float(g.uniform(0.5, 4)), float(g.uniform(0.5, 4))
+    if comp:
+        kw["compand"] = compand_scale(g.uniform(-3, 3, cols // 64).astype(np.float32), cols, dtype)
+    return x, kw
+
+
+PREP_CONFIGS = {
+    # name: (cols, rot, rot_block, clamp, comp, hadamard, scale)
+    "rot_perm_only": (1024, True, None, False, False, 0, False),
+    "rot64_clamp": (1024, True, 64, True, False, 0, True),
+    "rot1024_all": (2048, True, 1024, True, True, 128, True),
+    "norot_clamp_comp_h512": (1536, False, None, True, True, 512, False),
+    "rot4096_h4096": (4096, True, 4096, False, True, 4096, True),
+    "qwen8b_down_12288": (12288, True, 1024, True, True, 0, False),
+    "max_16384_norot": (16384, False, None, True, False, 1024, True),
+}
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("levels", ["123", "12", "13"])
+@pytest.mark.parametrize("name", sorted(PREP_CONFIGS))
+def test_act_prep_rows_matches_oracle_bitwise(dev, name, levels, dtype):
+    from oracle import linear as OL
+
+    cols, rot, rot_block, clamp, comp, hadamard, scale = PREP_CONFIGS[name]
+    x, kw = _random_prep_case(zlib.crc32(f"{name}/{levels}/{dtype}".encode()) & 0xFFFF, cols, dtype, rot=rot, rot_block=rot_block,
+                              clamp=clamp, comp=comp, hadamard=hadamard, scale=scale)
+    print(f"[act_prep] {name} levels={levels} {dtype} cols={cols}", flush=True)
+    got = _prep_on_device(x, dtype, dev, levels, kw).float().cpu().numpy()
+    ref = OL.fake_quant_linear_input(x, dtype, levels=levels, **kw)
+    assert _same(got, ref)
+
+
+def test_act_prep_rows_nan_and_no_quantizer(dev):
+    from oracle import linear as OL
+
+    x, kw = _random_prep_case(77, 512, "bfloat16", rot=False, rot_block=None, clamp=True, comp=True,
+                              hadamard=0, scale=False)
+    x[1, 7] = np.nan  # the clamp keeps NaN; its quantization group turns NaN
+    for levels in ("123", None):
+        got = _prep_on_device(x, "bfloat16", dev, levels, kw).float().cpu().numpy()
+        assert _same(got, OL.fake_quant_linear_input(x, "bfloat16", levels=levels, **kw))
+        assert np.isnan(got[1, 7])
+    # leading dimensions, and rows that need two rounds of 8-value lanes per workgroup
+    x, kw = _random_prep_case(78, 4096, "bfloat16", rot=True, rot_block=256, clamp=False, comp=False,
+                              hadamard=0, scale=False)
+    got = _prep_on_device(x, "bfloat16", dev, "123", kw)
+    x3 = to_dev(x, dev, torch.bfloat16).reshape(13, 1, 4096)
+    from faquant_amd import _ops
+
+    got3 = _ops.act_prep_rows(x3, levels="123", rot_signs=torch.from_numpy(kw["rot_signs"]).to(dev),
+                              rot_perm=torch.from_numpy(kw["rot_perm"]).to(dev), rot_block=256)
+    assert got3.shape == (13, 1, 4096) and torch.equal(got3.reshape(13, 4096), got)
+
+
+def test_fake_quant_linear_full_path_equals_reference_composition(dev):
+    """FakeQuantLinear with every option of the activation path against the oracle's
+    activation and F.linear on the same HiF4 weight (quantization.py:199-276)."""
+    from oracle import linear as OL
+    from faquant_amd.hif4 import HIF4_ACT_SCALE_LEVELS
+    from faquant_amd.quantization import FakeQuantLinear
+
+    g = OI.rng(31)
+    n, m = 1024, 384
+    lin = torch.nn.Linear(n, m, bias=True).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(to_dev(g.standard_normal((m, n)) * 0.03, dev, torch.bfloat16))
+    signs = g.choice(np.array([-1, 1], np.int8), n)
+    perm = g.permutation(n)
+    scale = g.uniform(0.5, 2.0, n).astype(np.float32)
+    log_scale = g.uniform(-2.5, 2.5, n // 64).astype(np.float32)
+    mod = FakeQuantLinear(
+        lin, quant_format="hif4", bits=4, weight_group_size=64, activation_group_size=64, symmetric=True,
+        clip_ratio=1.0, online_hadamard=True, online_hadamard_block_size=128, input_scale=to_dev(scale, dev),
+        input_rotation_signs=torch.from_numpy(signs).to(dev), input_rotation_permutation=torch.from_numpy(perm).to(dev),
+        input_rotation_block_size=256, activation_min=-2.5, activation_max=3.25,
+        activation_compand_log_scale=to_dev(log_scale, dev),
+    )
+    x = OQ.bf16_round(g.standard_normal((3, 21, n)).astype(np.float32) * 1.7)
+    got = mod(to_dev(x, dev, torch.bfloat16))
+    # the companding scale as the module computes it, on the device (exp there)
+    comp = torch.from_numpy(log_scale).to(dev).repeat_interleave(64).clamp(-2.079, 2.079).exp().to(torch.bfloat16)
+    act = OL.fake_quant_linear_input(
+        x.reshape(-1, n), "bfloat16", levels=HIF4_ACT_SCALE_LEVELS, input_scale=scale, rot_signs=signs, rot_perm=perm,
+        rot_block=256, act_min=-2.5, act_max=3.25, compand=comp.float().cpu().numpy(), hadamard=128,
+    )
+    expected = torch.nn.functional.linear(to_dev(act, dev, torch.bfloat16), mod.weight, mod.bias)
+    assert torch.equal(got.reshape(-1, m), expected)
 
 
 def test_hif4_linear_equals_quantize_then_linear(dev):
