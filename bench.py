@@ -367,6 +367,61 @@ def linear_bench(tokens: int, steps: int, warmup: int) -> dict:
                       "frac": round(fl / ((tq + tg) * 1e-6) / (MFMA_BF16_PEAK_TFLOPS * 1e12), 3)}}
 
 
+# (name, in_features) of the Qwen3-8B Linear inputs: attention projections and the MLP
+QWEN8B_LINEAR_INPUTS = (("q/k/v/o_proj, gate/up_proj", 4096), ("down_proj", 12288))
+
+
+def linear_prep_bench(tokens: int, steps: int, warmup: int) -> dict:
+    """The quantized Linear's activation path over `tokens` bf16 rows at the Qwen3-8B input
+    widths: the fused prologue without extras (act_qdq_rows: HiF4 QDQ only) and the full path
+    with the HiSQ rotation (signs, permutation, block Hadamard of 1024), clamp and companding
+    (act_prep_rows), each against the 8 TB/s HBM peak on the activation bytes it must move
+    (read and write once)."""
+    import torch
+
+    from faquant_amd import _ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    rows = []
+    for name, k in QWEN8B_LINEAR_INPUTS:
+        x = torch.randn((tokens, k), device=dev, generator=gen).to(torch.bfloat16)
+        y = torch.empty_like(x)
+        signs = (torch.randint(0, 2, (k,), device=dev, generator=gen) * 2 - 1).to(torch.int8)
+        # the kernel's forms of the vectors (int32 permutation, fp32 companding scale holding
+        # bf16 values), as FakeQuantLinear caches them
+        perm = torch.randperm(k, device=dev, generator=gen).to(torch.int32)
+        comp = torch.rand((k,), device=dev, generator=gen).mul(2).sub(1).exp().to(torch.bfloat16).float()
+
+        def timed(fn):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(steps):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / steps
+
+        nbytes = 2 * 2 * tokens * k
+        entry = {"inputs": name, "in_features": k}
+        for label, fn in (
+            ("qdq_only", lambda: _ops.act_qdq_rows(x, levels="123", out=y)),
+            ("hisq_clamp_compand", lambda: _ops.act_prep_rows(x, levels="123", rot_signs=signs, rot_perm=perm,
+                                                              rot_block=1024, act_min=-8.0, act_max=8.0,
+                                                              compand=comp, out=y)),
+        ):
+            ms = timed(fn)
+            entry[label] = {"us": round(ms * 1e3, 1),
+                            "hbm_frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBPS * 1e9), 3)}
+        rows.append(entry)
+        del x, y
+    return {"metric": "quantized Linear activation path (Qwen3-8B input widths), 1 GPU", "tokens": tokens,
+            "steps": steps, "warmup": warmup, "dtype": "bf16", "layers": rows}
+
+
 def stream_reference() -> dict:
     """This device's practical rates for plain streams, the measured reference points beside
     the 8 TB/s specification for the HBM-bound decode kernels: torch's copy and sum over
@@ -429,6 +484,9 @@ def main():
                     help="time one decode step over CONTEXT cached keys of --config's heads instead")
     ap.add_argument("--linear", type=int, default=0, metavar="TOKENS",
                     help="time the HiF4 W4A4 Linear at the Wan2.2 DiT block shapes over TOKENS rows instead")
+    ap.add_argument("--linear-prep", type=int, default=0, metavar="TOKENS",
+                    help="time the quantized Linear's activation path (HiSQ rotation, clamp, companding) "
+                         "at the Qwen3-8B input widths over TOKENS rows instead")
     ap.add_argument("--stream-reference", action="store_true",
                     help="measure only the device's practical HBM stream rate (torch copy and sum over 1 GiB)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -445,6 +503,10 @@ def main():
 
     if args.linear:
         print(json.dumps(linear_bench(args.linear, args.steps, args.warmup)), flush=True)
+        return
+
+    if args.linear_prep:
+        print(json.dumps(linear_prep_bench(args.linear_prep, args.steps, args.warmup)), flush=True)
         return
 
     if args.stream_reference:

@@ -72,12 +72,22 @@ void launch_act(const faq::ActQdqArgs& a, int levels, int64_t threads, hipStream
   else hipLaunchKernelGGL((faq::act_qdq_rows_kernel<T, 123>), grid, dim3(256), 0, st, a);
 }
 
+template <typename T, int R, int NT>
+void launch_act_row_r(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(a.rows));
+  if (levels == 12) hipLaunchKernelGGL((faq::act_row_kernel<T, 12, R, NT>), grid, dim3(NT), lds, st, a);
+  else if (levels == 13) hipLaunchKernelGGL((faq::act_row_kernel<T, 13, R, NT>), grid, dim3(NT), lds, st, a);
+  else hipLaunchKernelGGL((faq::act_row_kernel<T, 123, R, NT>), grid, dim3(NT), lds, st, a);
+}
+
+// 8-value chunks per lane and threads per row: 256 threads with 1, 2 or 4 chunks each up to
+// 8192 features, 512 threads with 4 beyond.
 template <typename T>
 void launch_act_row(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(a.rows));
-  if (levels == 12) hipLaunchKernelGGL((faq::act_row_kernel<T, 12>), grid, dim3(faq::kActRowThreads), lds, st, a);
-  else if (levels == 13) hipLaunchKernelGGL((faq::act_row_kernel<T, 13>), grid, dim3(faq::kActRowThreads), lds, st, a);
-  else hipLaunchKernelGGL((faq::act_row_kernel<T, 123>), grid, dim3(faq::kActRowThreads), lds, st, a);
+  if (a.cols <= 2048) launch_act_row_r<T, 1, 256>(a, levels, lds, st);
+  else if (a.cols <= 4096) launch_act_row_r<T, 2, 256>(a, levels, lds, st);
+  else if (a.cols <= 8192) launch_act_row_r<T, 4, 256>(a, levels, lds, st);
+  else launch_act_row_r<T, 4, 512>(a, levels, lds, st);
 }
 
 // LDS bytes one workgroup of the current device may hold (cached per device; 64 KiB when
@@ -499,6 +509,8 @@ int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
       return fail(FAQ_EINVAL, "dimension %lld must be divisible by power-of-two block_size=%d", static_cast<long long>(cols), b);
     return FAQ_OK;
   };
+  if (!aligned16(o.col_scale) || !aligned16(o.rot_perm) || !aligned16(o.compand) || !aligned16(o.rot_signs))
+    return fail(FAQ_EINVAL, "%s: the input scale, sign, permutation and companding vectors must be 16-byte aligned", who);
   if (o.rot_signs && !o.rot_perm) return fail(FAQ_EINVAL, "%s: a rotation needs both signs and permutation", who);
   if (!o.rot_signs && (o.rot_perm || o.rot_block)) return fail(FAQ_EINVAL, "%s: a rotation needs both signs and permutation", who);
   if (int st = check_block(o.rot_block)) return st;
@@ -522,9 +534,10 @@ int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
   a.n = o.hadamard;
   a.div = sqrt_div(o.hadamard);
   a.quant = levels != 0;
-  const size_t lds = faq::act_row_lds_bytes(a.cols, a.rot_signs != nullptr);
+  const bool uses_lds = o.rot_signs || o.rot_block > 8 || o.hadamard > 8;
+  const size_t lds = uses_lds ? faq::act_row_lds_bytes(a.cols) : 0;
   if (lds > device_lds_per_block())
-    return fail(FAQ_EUNSUP, "%s: a row of %lld features with a rotation needs %zu bytes of LDS, the device has %zu", who,
+    return fail(FAQ_EUNSUP, "%s: a row of %lld features needs %zu bytes of LDS, the device has %zu", who,
                 static_cast<long long>(cols), lds, device_lds_per_block());
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == FAQ_F32) launch_act_row<float>(a, levels, lds, st);

@@ -519,7 +519,6 @@ __global__ __launch_bounds__(256) void act_qdq_rows_kernel(ActQdqArgs a) {
 // in the input dtype, NaN kept); x * companding scale; the online block Hadamard with one
 // cast back; the HiF4 QDQ; x / companding scale.  Every elementwise step rounds to the input
 // dtype as torch does.  One 256-thread workgroup per row, the row in LDS as fp32.
-constexpr int kActRowThreads = 256;
 constexpr int kActMaxCols = 16384;
 
 struct ActRowArgs {
@@ -540,103 +539,204 @@ struct ActRowArgs {
   int quant;                // 1: HiF4 QDQ
 };
 
-// v / fp32(sqrt(n)), correctly rounded (div_sqrt_n for one value)
-__device__ __forceinline__ float div_sqrt_1(float v, const SqrtDiv& s) {
-  if (s.pow2) return v * s.r;
-  const float q = v * s.r;
-  const float e = __builtin_fmaf(-q, s.d, v);
-  const float y = __builtin_fmaf(e, s.r, q);
-  const float m = fabsf(v);
-  return (m >= 0x1p-105f && m <= 3.40282347e38f) ? y : v / s.d;
+// Layout of act_row_kernel (NT threads): lane tid holds chunk c = tid + NT r (r < R) of the
+// row, the 8 values 8 c .. 8 c + 7, in registers (the coalesced load / store layout and the
+// QDQ layout: 8 consecutive lanes hold one 64-value group).  LDS holds one fp32 copy of the
+// row for the permutation gather and for the butterfly stages that cross lanes.
+// Value j sits at lds_pad(j) = j + j / 8: one spare word after every 8 values, so lanes that
+// write or read their 8-value chunks (8 words apart), and the first butterfly pass over LDS
+// (stride 8), touch distinct banks.
+__host__ __device__ constexpr size_t act_row_lds_bytes(int cols) {
+  return static_cast<size_t>(cols + cols / 8) * sizeof(float);
+}
+__device__ __forceinline__ int lds_pad(int j) { return j + (j >> 3); }
+
+// Butterflies (left + right, left - right) of the stages of stride 1 .. S (S = 1, 2 or 4)
+// on each lane's chunks (their pairs lie inside one chunk).
+template <int R, int S>
+__device__ __forceinline__ void fwht_in_chunks(float (&v)[R][8]) {
+#pragma unroll
+  for (int s = 1; s <= S; s <<= 1)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (!(i & s)) {
+          const float l = v[r][i], h = v[r][i + s];
+          v[r][i] = l + h;
+          v[r][i + s] = l - h;
+        }
 }
 
-// Normalized Walsh-Hadamard transform of every b-block of the LDS row buf[0, cols): stages
-// of stride 1, 2, ..., b/2 writing (left + right, left - right), then the division by
-// fp32(sqrt(b)) (rotation.py:14-29).  Ends with the row written and visible to the block.
-__device__ __forceinline__ void lds_fwht(float* buf, int cols, int b, const SqrtDiv& dv, int tid) {
-  for (int s = 1; s < b; s <<= 1) {
-    __syncthreads();
-    for (int q = tid; q < cols / 2; q += kActRowThreads) {
-      const int i = (q / s) * 2 * s + (q % s);
-      const float l = buf[i], r = buf[i + s];
-      buf[i] = l + r;
-      buf[i + s] = l - r;
-    }
+// One pass over the LDS row of the LR stages of stride s, 2 s, .. (LR = 1, 2 or 3; s a
+// multiple of 8, 2^LR s dividing the block): group g holds the 2^LR values j0 + m s.
+template <int LR, int NT>
+__device__ __forceinline__ void fwht_lds_pass(float* lds, int cols, int ls, int tid) {
+  constexpr int kRad = 1 << LR;
+  const int s = 1 << ls;
+  const int as = s + (s >> 3);  // j0 + m s sits at lds_pad(j0) + m (s + s / 8)
+  for (int g = tid; g < (cols >> LR); g += NT) {
+    const int a0 = lds_pad(((g >> ls) << (ls + LR)) | (g & (s - 1)));
+    float w[kRad];
+#pragma unroll
+    for (int m = 0; m < kRad; ++m) w[m] = lds[a0 + m * as];
+#pragma unroll
+    for (int t = 1; t < kRad; t <<= 1)
+#pragma unroll
+      for (int m = 0; m < kRad; ++m)
+        if (!(m & t)) {
+          const float l = w[m], h = w[m + t];
+          w[m] = l + h;
+          w[m + t] = l - h;
+        }
+#pragma unroll
+    for (int m = 0; m < kRad; ++m) lds[a0 + m * as] = w[m];
   }
-  __syncthreads();
-  for (int j = tid; j < cols; j += kActRowThreads) buf[j] = div_sqrt_1(buf[j], dv);
 }
 
-// LDS: the row as fp32 in [0, cols), and with a rotation a second row for the gather,
-// act_row_lds_bytes() in all (dynamic shared memory).
-__host__ __device__ constexpr size_t act_row_lds_bytes(int cols, bool rotate) {
-  return static_cast<size_t>(rotate ? 2 : 1) * static_cast<size_t>(cols) * sizeof(float);
+// Normalized Walsh-Hadamard transform of every b-block of the row (rotation.py:14-29): the
+// stages of stride 1, 2, ..., b / 2 in that order, each pair (i, i + s) becoming
+// (left + right, left - right), then the division by fp32(sqrt(b)).  Strides 1, 2, 4 run in
+// registers; larger strides in passes over LDS of up to three stages (s, 2 s, 4 s) on the
+// values j0 + m s read into registers: the same additions as one stage at a time.  Ends with
+// the transformed row in v.
+template <int R, int NT>
+__device__ __forceinline__ void fwht_row(float (&v)[R][8], float* lds, int cols, int b, const SqrtDiv& dv, int tid) {
+  if (b == 2) fwht_in_chunks<R, 1>(v);
+  else if (b == 4) fwht_in_chunks<R, 2>(v);
+  else fwht_in_chunks<R, 4>(v);
+  if (b > 8) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c0 = 8 * (tid + NT * r);
+      if (c0 < cols)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lds[lds_pad(c0) + i] = v[r][i];
+    }
+    const int lb = __builtin_ctz(b);
+    for (int ls = 3; ls < lb; ls += 3) {
+      __syncthreads();
+      const int lr = min(3, lb - ls);
+      if (lr == 3) fwht_lds_pass<3, NT>(lds, cols, ls, tid);
+      else if (lr == 2) fwht_lds_pass<2, NT>(lds, cols, ls, tid);
+      else fwht_lds_pass<1, NT>(lds, cols, ls, tid);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c0 = 8 * (tid + NT * r);
+      if (c0 < cols)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[r][i] = lds[lds_pad(c0) + i];
+    }
+    // the next user of the LDS row writes it again
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) div_sqrt_n(v[r], dv);
 }
 
-template <typename T, int LV>
-__global__ __launch_bounds__(kActRowThreads) void act_row_kernel(ActRowArgs a) {
+// One workgroup of NT threads per row of at most 8 NT R values.  R stays at most 4: with
+// 8 chunks per lane the compiler keeps the row in scratch memory instead of registers.
+template <typename T, int LV, int R, int NT>
+__global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
   extern __shared__ float act_row_lds[];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const T* x = static_cast<const T*>(a.x) + row * a.cols;
   T* y = static_cast<T*>(a.y) + row * a.cols;
-  float* cur = act_row_lds;
-  for (int c0 = 8 * tid; c0 < a.cols; c0 += 8 * kActRowThreads) {
-    float v[8];
-    Io<T>::load8(x + c0, v);
-    if (a.col_scale) {
+  float v[R][8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(v[i] * Io<T>::round(a.col_scale[c0 + i]));
+  for (int r = 0; r < R; ++r) {
+    const int c0 = 8 * (tid + NT * r);
+    if (c0 < a.cols) {
+      Io<T>::load8(x + c0, v[r]);
+      if (a.col_scale) {
+        float sc[8];
+        Io<float>::load8(a.col_scale + c0, sc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(v[r][i] * Io<T>::round(sc[i]));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[r][i] = 0.0f;
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) cur[c0 + i] = v[i];
   }
-  // every later pass reads values that other lanes wrote
-  __syncthreads();
   if (a.rot_signs) {
-    float* nxt = act_row_lds + a.cols;
-    for (int j = tid; j < a.cols; j += kActRowThreads) {
-      const int p = min(max(a.rot_perm[j], 0), a.cols - 1);  // (a valid permutation stays in range)
-      nxt[j] = cur[p] * static_cast<float>(a.rot_signs[p]);
+    // fp32 x times the signs in feature order (coalesced sign loads), then gathered by the
+    // permutation (index_select): value j is x[perm[j]] sign[perm[j]]
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c0 = 8 * (tid + NT * r);
+      if (c0 < a.cols) {
+        const uint2 sw = *reinterpret_cast<const uint2*>(a.rot_signs + c0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int8_t sg = static_cast<int8_t>(((i < 4 ? sw.x : sw.y) >> (8 * (i & 3))) & 0xFFu);
+          act_row_lds[lds_pad(c0) + i] = v[r][i] * static_cast<float>(sg);
+        }
+      }
     }
-    cur = nxt;
-    if (a.rot_block) lds_fwht(cur, a.cols, a.rot_block, a.rot_div, tid);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c0 = 8 * (tid + NT * r);
+      if (c0 < a.cols) {
+        const int4 pa = *reinterpret_cast<const int4*>(a.rot_perm + c0);
+        const int4 pb = *reinterpret_cast<const int4*>(a.rot_perm + c0 + 4);
+        const int pp[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[r][i] = act_row_lds[lds_pad(min(max(pp[i], 0), a.cols - 1))];  // (a valid permutation stays in range)
+      }
+    }
+    // every gather has read the row before the transform writes it
+    __syncthreads();
+    if (a.rot_block) fwht_row<R, NT>(v, act_row_lds, a.cols, a.rot_block, a.rot_div, tid);
   }
-  // one cast back after the rotation, the clamp and the companding product, in place; each
-  // lane reads the entries it wrote last (the same j mapping)
+  // one cast back after the rotation, the clamp (bounds in T, NaN kept), the companding
+  // product
   const float lo = Io<T>::round(a.act_min), hi = Io<T>::round(a.act_max);
-  for (int j = tid; j < a.cols; j += kActRowThreads) {
-    float v = cur[j];
-    if (a.rot_signs) v = Io<T>::round(v);
-    if (!__builtin_isnan(v)) {
-      if (a.has_min) v = fmaxf(v, lo);
-      if (a.has_max) v = fminf(v, hi);
+  float cs[R][8];  // the companding scale of the lane's values (1 without companding)
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c0 = 8 * (tid + NT * r);
+    if (a.compand && c0 < a.cols) {
+      Io<float>::load8(a.compand + c0, cs[r]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cs[r][i] = 1.0f;
     }
-    if (a.compand) v = Io<T>::round(v * a.compand[j]);
-    cur[j] = v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float t = v[r][i];
+      if (a.rot_signs) t = Io<T>::round(t);
+      if (!__builtin_isnan(t)) {
+        if (a.has_min) t = fmaxf(t, lo);
+        if (a.has_max) t = fminf(t, hi);
+      }
+      if (a.compand) t = Io<T>::round(t * cs[r][i]);
+      v[r][i] = t;
+    }
   }
   if (a.n) {
-    lds_fwht(cur, a.cols, a.n, a.div, tid);
-    for (int j = tid; j < a.cols; j += kActRowThreads) cur[j] = Io<T>::round(cur[j]);
+    fwht_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div, tid);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(v[r][i]);
   }
-  __syncthreads();
-  // QDQ: 8 values per lane, a 64-value group on 8 consecutive lanes; every lane takes part
-  // in every round (zeros past the row), as qdq8 exchanges values within its 8 lanes
-  const int rounds = (a.cols + 8 * kActRowThreads - 1) / (8 * kActRowThreads);
-  for (int rd = 0; rd < rounds; ++rd) {
-    const int c0 = 8 * (tid + rd * kActRowThreads);
-    const bool have = c0 < a.cols;
-    float v[8];
+  // QDQ: every lane takes part (zeros past the row), as qdq8 exchanges values within its 8
+  // lanes; then the companding quotient of the quantized values in T
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = have ? cur[c0 + i] : 0.0f;
-    if (a.quant) qdq8<LV>(v);
-    if (have) {
+  for (int r = 0; r < R; ++r) {
+    const int c0 = 8 * (tid + NT * r);
+    if (a.quant) qdq8<LV>(v[r]);
+    if (c0 < a.cols) {
       if (a.compand) {
-        // the quantized tensor is in T before torch divides it
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = Io<T>::round(Io<T>::round(v[i]) / a.compand[c0 + i]);
+        for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(Io<T>::round(v[r][i]) / cs[r][i]);
       }
-      Io<T>::store8(y + c0, v);
+      Io<T>::store8(y + c0, v[r]);
     }
   }
 }

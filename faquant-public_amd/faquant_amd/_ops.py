@@ -163,6 +163,8 @@ def act_prep_rows(
         v = t.to(device=x.device, dtype=dtype).reshape(-1).contiguous()
         if v.numel() != cols:
             raise ValueError(f"{name} must hold {cols} values, got {v.numel()}")
+        if v.data_ptr() % 16:  # the kernel reads these vectors 16 bytes at a time
+            v = v.clone()
         keep.append(v)
         return v.data_ptr()
 

@@ -148,6 +148,34 @@ class FakeQuantLinear(torch.nn.Module):
         else:
             self.bias = torch.nn.Parameter(linear.bias.detach().clone(), requires_grad=False)
 
+    def _prep_vectors(self, x: torch.Tensor):
+        """The per-feature vectors of the activation path in the kernel's forms (int32
+        permutation; the companding scale computed as the reference does: clamp to +-2.079,
+        exp, cast to x's dtype, then held as fp32) and the clamp bounds as floats, cached per
+        device and dtype and recomputed when a buffer is modified in place or replaced."""
+        tensors = (self.input_rotation_permutation, self.activation_compand_log_scale, self.activation_min,
+                   self.activation_max)
+        key = (x.device, x.dtype) + tuple(None if t is None else (id(t), t._version) for t in tensors)
+        cached = getattr(self, "_prep_cache", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        perm = None
+        if self.input_rotation_permutation is not None:
+            perm = self.input_rotation_permutation.to(device=x.device, dtype=torch.int32).contiguous()
+        compand = None
+        if self.activation_compand_log_scale is not None:
+            log_scale = self.activation_compand_log_scale
+            if log_scale.numel() != self.in_features:
+                if self.in_features % log_scale.numel():
+                    raise RuntimeError("invalid activation companding shape")
+                log_scale = log_scale.repeat_interleave(self.in_features // log_scale.numel())
+            compand = log_scale.clamp(-2.079, 2.079).exp().to(device=x.device, dtype=x.dtype).float().contiguous()
+        bounds = (None if self.activation_min is None else float(self.activation_min),
+                  None if self.activation_max is None else float(self.activation_max))
+        value = (perm, compand, bounds)
+        self._prep_cache = (key, value)
+        return value
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         from . import _ops
         from .hif4 import HIF4_ACT_SCALE_LEVELS
@@ -158,18 +186,9 @@ class FakeQuantLinear(torch.nn.Module):
         if not extra:
             xq = _ops.act_qdq_rows(x, levels=HIF4_ACT_SCALE_LEVELS, hadamard=int(block or 0), col_scale=self.input_scale)
         else:
-            compand = None
-            if self.activation_compand_log_scale is not None:
-                log_scale = self.activation_compand_log_scale
-                if log_scale.numel() != self.in_features:
-                    if self.in_features % log_scale.numel():
-                        raise RuntimeError("invalid activation companding shape")
-                    log_scale = log_scale.repeat_interleave(self.in_features // log_scale.numel())
-                compand = log_scale.clamp(-2.079, 2.079).exp().to(device=x.device, dtype=x.dtype)
+            perm, compand, bounds = self._prep_vectors(x)
             xq = _ops.act_prep_rows(
                 x, levels=HIF4_ACT_SCALE_LEVELS, col_scale=self.input_scale, rot_signs=self.input_rotation_signs,
-                rot_perm=self.input_rotation_permutation, rot_block=self.input_rotation_block_size,
-                act_min=None if self.activation_min is None else float(self.activation_min),
-                act_max=None if self.activation_max is None else float(self.activation_max),
+                rot_perm=perm, rot_block=self.input_rotation_block_size, act_min=bounds[0], act_max=bounds[1],
                 compand=compand, hadamard=int(block or 0))
         return torch.nn.functional.linear(_lib.forward_only(xq, x), self.weight, self.bias)

@@ -190,10 +190,11 @@ typedef struct faq_act_opts {
  * hisq_rotation.py:50-71), the activation clamp, x * companding scale, the online block
  * Hadamard with one cast back, the HiF4 QDQ with `levels` (0: none), and x / companding
  * scale; each elementwise step rounds to the input dtype.  Rows of at most 16384 features
- * (a multiple of 64), contiguous, fp32 / bf16 / fp16; one workgroup per row holding the row
- * in LDS as fp32 (4 bytes a feature, 8 with a rotation; FAQ_EUNSUP beyond the device's LDS
- * per workgroup).  opts may be NULL (then this is faq_act_qdq_rows without input scale or
- * Hadamard).
+ * (a multiple of 64), contiguous, fp32 / bf16 / fp16; one workgroup per row.  With the
+ * rotation or a Hadamard block above 8 the row passes through LDS as fp32 (4 bytes a feature;
+ * FAQ_EUNSUP beyond the device's LDS per workgroup).  x, y and the col_scale, rot_signs,
+ * rot_perm and compand vectors must be 16-byte aligned.  opts may be NULL (then this is faq_act_qdq_rows
+ * without input scale or Hadamard).
  */
 int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const faq_act_opts* opts,
                       int levels, faq_stream_t stream);

@@ -256,6 +256,18 @@ def test_fake_quant_linear_full_path_equals_reference_composition(dev):
     )
     expected = torch.nn.functional.linear(to_dev(act, dev, torch.bfloat16), mod.weight, mod.bias)
     assert torch.equal(got.reshape(-1, m), expected)
+    # the module caches the kernel's vector forms: an in-place change of a buffer is seen
+    with torch.no_grad():
+        mod.activation_max.fill_(1.5)
+        mod.activation_compand_log_scale.mul_(0.5)
+    comp = (torch.from_numpy(log_scale).to(dev) * 0.5).repeat_interleave(64).clamp(-2.079, 2.079).exp()
+    comp = comp.to(torch.bfloat16)
+    act = OL.fake_quant_linear_input(
+        x.reshape(-1, n), "bfloat16", levels=HIF4_ACT_SCALE_LEVELS, input_scale=scale, rot_signs=signs, rot_perm=perm,
+        rot_block=256, act_min=-2.5, act_max=1.5, compand=comp.float().cpu().numpy(), hadamard=128,
+    )
+    expected = torch.nn.functional.linear(to_dev(act, dev, torch.bfloat16), mod.weight, mod.bias)
+    assert torch.equal(mod(to_dev(x, dev, torch.bfloat16)).reshape(-1, m), expected)
 
 
 def test_hif4_linear_equals_quantize_then_linear(dev):
