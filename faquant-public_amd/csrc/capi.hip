@@ -463,8 +463,8 @@ int faq_hif4_unpack_rows(const uint8_t* codes, const uint8_t* scale_byte, const 
 
 int faq_act_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const float* col_scale,
                      int hadamard, int levels, faq_stream_t stream) {
-  if (!x || !y) return fail(FAQ_EINVAL, "faq_act_qdq_rows: null input or output");
   if (rows < 0) return fail(FAQ_EINVAL, "faq_act_qdq_rows: negative size");
+  if ((!x || !y) && rows > 0) return fail(FAQ_EINVAL, "faq_act_qdq_rows: null input or output");
   if (!valid_dtype(dtype)) return fail(FAQ_EINVAL, "faq_act_qdq_rows: bad dtype");
   if (levels != 0 && !valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
   if (hadamard != 0) {
@@ -491,8 +491,8 @@ int faq_act_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dty
 int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const faq_act_opts* opts,
                       int levels, faq_stream_t stream) {
   const char* who = "faq_act_prep_rows";
-  if (!x || !y) return fail(FAQ_EINVAL, "%s: null input or output", who);
   if (rows < 0) return fail(FAQ_EINVAL, "%s: negative size", who);
+  if ((!x || !y) && rows > 0) return fail(FAQ_EINVAL, "%s: null input or output", who);
   if (!valid_dtype(dtype)) return fail(FAQ_EINVAL, "%s: bad dtype", who);
   if (levels != 0 && !valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
   if (cols <= 0) return fail(FAQ_EINVAL, "HiF4 fake quantization does not support an empty axis");

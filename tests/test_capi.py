@@ -98,7 +98,15 @@ def test_validation_statuses_without_device_work(lib):
     ao = _lib.ActOpts()
     ao.rot_perm = p16
     assert lib.faq_act_prep_rows(p16, p16, 1, 128, 1, ctypes.byref(ao), 123, None) == _lib.EINVAL
+    ao = _lib.ActOpts()
+    ao.compand = p16 + 4  # the kernel reads the per-feature vectors 16 bytes at a time
+    assert lib.faq_act_prep_rows(p16, p16, 1, 128, 1, ctypes.byref(ao), 123, None) == _lib.EINVAL
+    assert "16-byte aligned" in lib.faq_last_error().decode()
     assert lib.faq_act_prep_rows(p16, p16, 0, 128, 1, None, 123, None) == _lib.OK
+    # an empty batch (torch gives its storage a null pointer) launches nothing
+    assert lib.faq_act_prep_rows(None, None, 0, 128, 1, None, 123, None) == _lib.OK
+    assert lib.faq_act_qdq_rows(None, None, 0, 128, 1, None, 0, 123, None) == _lib.OK
+    assert lib.faq_act_prep_rows(None, None, 1, 128, 1, None, 123, None) == _lib.EINVAL
     assert lib.faq_operand_prep(p16, 1, 128, 128, 128, 1, 1, 1, None, 0, None, 0, 0, 96, 1, None, p16, 128, 128, 128,
                                 123, None) == _lib.EUNSUP
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,

@@ -223,6 +223,37 @@ def test_act_prep_rows_nan_and_no_quantizer(dev):
     assert got3.shape == (13, 1, 4096) and torch.equal(got3.reshape(13, 4096), got)
 
 
+def test_act_prep_rows_edges(dev):
+    """One 64-feature row, a single row, many rows, fp16 infinities through the clamp,
+    misaligned option vectors (realigned on the host) and an empty batch."""
+    from oracle import linear as OL
+    from faquant_amd import _ops
+
+    for cols, rows, dtype in ((64, 1, "bfloat16"), (64, 5000, "float16"), (2048, 1, "float32")):
+        x, kw = _random_prep_case(cols + rows, cols, dtype, rot=True, rot_block=min(cols, 64), clamp=True, comp=True,
+                                  hadamard=32, scale=True)
+        x = np.resize(x, (rows, cols)).astype(np.float32)
+        if dtype == "float16":
+            x[0, :3] = [np.inf, -np.inf, 70000.0]  # clamped to the bounds (70000 is inf in fp16)
+        print(f"[act_prep edge] cols={cols} rows={rows} {dtype}", flush=True)
+        got = _prep_on_device(x, dtype, dev, "123", kw).float().cpu().numpy()
+        assert _same(got, OL.fake_quant_linear_input(x if dtype != "float16" else x.astype(np.float16).astype(np.float32),
+                                                     dtype, levels="123", **kw))
+    # option vectors at an offset that is not a multiple of 16 bytes
+    x, kw = _random_prep_case(9, 512, "bfloat16", rot=False, rot_block=None, clamp=False, comp=True,
+                              hadamard=0, scale=True)
+    scale = torch.zeros(513, device=dev)
+    scale[1:] = torch.from_numpy(kw["input_scale"]).to(dev)
+    comp = torch.zeros(514, device=dev)
+    comp[2:] = torch.from_numpy(kw["compand"]).to(dev)
+    got = _ops.act_prep_rows(to_dev(x, dev, torch.bfloat16), levels="123", col_scale=scale[1:], compand=comp[2:])
+    assert _same(got.float().cpu().numpy(), OL.fake_quant_linear_input(x, "bfloat16", levels="123", **kw))
+    empty = _ops.act_prep_rows(torch.empty((0, 512), device=dev, dtype=torch.bfloat16), levels="123",
+                               compand=comp[2:])
+    assert empty.shape == (0, 512)
+    assert _ops.act_qdq_rows(torch.empty((0, 3, 512), device=dev, dtype=torch.bfloat16), levels="123").shape == (0, 3, 512)
+
+
 def test_fake_quant_linear_full_path_equals_reference_composition(dev):
     """FakeQuantLinear with every option of the activation path against the oracle's
     activation and F.linear on the same HiF4 weight (quantization.py:199-276)."""
