@@ -370,7 +370,7 @@ const char* faq_version(void) { return "faquant_amd 0.1 gfx950"; }
 int faq_hif4_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, int levels, float* scale,
                       float* rec, int8_t* lv2, int8_t* lv3, uint8_t* codes, uint8_t* scale_byte, uint8_t* lv2_bits,
                       uint16_t* lv3_bits, faq_stream_t stream) {
-  if (!x || !y) return fail(FAQ_EINVAL, "faq_hif4_qdq_rows: null input or output");
+  if ((!x || !y) && rows > 0) return fail(FAQ_EINVAL, "faq_hif4_qdq_rows: null input or output");
   if (rows < 0 || cols <= 0) return fail(FAQ_EINVAL, "HiF4 fake quantization does not support an empty axis");
   if (!valid_dtype(dtype)) return fail(FAQ_EINVAL, "faq_hif4_qdq_rows: unsupported dtype %d", dtype);
   if (!valid_levels(levels)) return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", levels);
@@ -400,7 +400,8 @@ int faq_hif4_qdq_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
 
 int faq_hadamard_rows(const void* x, void* y, int64_t rows, int64_t cols, int block, int in_dtype, int out_dtype,
                       faq_stream_t stream) {
-  if (!x || !y) return fail(FAQ_EINVAL, "faq_hadamard_rows: null input or output");
+  if (rows < 0) return fail(FAQ_EINVAL, "faq_hadamard_rows: negative size");
+  if ((!x || !y) && rows > 0) return fail(FAQ_EINVAL, "faq_hadamard_rows: null input or output");
   if (block < 2 || block > 512 || (block & (block - 1)))
     return fail(FAQ_EINVAL, "Hadamard dimension must be a power of two, got %d", block);
   if (cols <= 0 || cols % block)
@@ -420,7 +421,8 @@ int faq_hadamard_rows(const void* x, void* y, int64_t rows, int64_t cols, int bl
 }
 
 int faq_hadamard_rows_native(const void* x, void* y, int64_t rows, int64_t cols, int dtype, faq_stream_t stream) {
-  if (!x || !y) return fail(FAQ_EINVAL, "faq_hadamard_rows_native: null input or output");
+  if (rows < 0) return fail(FAQ_EINVAL, "faq_hadamard_rows_native: negative size");
+  if ((!x || !y) && rows > 0) return fail(FAQ_EINVAL, "faq_hadamard_rows_native: null input or output");
   if (cols < 2 || cols > 512 || (cols & (cols - 1)))
     return fail(cols > 512 && !(cols & (cols - 1)) ? FAQ_EUNSUP : FAQ_EINVAL,
                 cols > 512 && !(cols & (cols - 1)) ? "faq_hadamard_rows_native: dimension %lld above 512"

@@ -107,6 +107,10 @@ def test_validation_statuses_without_device_work(lib):
     assert lib.faq_act_prep_rows(None, None, 0, 128, 1, None, 123, None) == _lib.OK
     assert lib.faq_act_qdq_rows(None, None, 0, 128, 1, None, 0, 123, None) == _lib.OK
     assert lib.faq_act_prep_rows(None, None, 1, 128, 1, None, 123, None) == _lib.EINVAL
+    assert lib.faq_hif4_qdq_rows(None, None, 0, 64, 1, 123, *([None] * 8), None) == _lib.OK
+    assert lib.faq_hadamard_rows(None, None, 0, 128, 64, 1, 1, None) == _lib.OK
+    assert lib.faq_hadamard_rows(p16, p16, -1, 128, 64, 1, 1, None) == _lib.EINVAL
+    assert lib.faq_hadamard_rows_native(None, None, 0, 128, 1, None) == _lib.OK
     assert lib.faq_operand_prep(p16, 1, 128, 128, 128, 1, 1, 1, None, 0, None, 0, 0, 96, 1, None, p16, 128, 128, 128,
                                 123, None) == _lib.EUNSUP
     rc = lib.faq_attention_fwd(p16, 0, 0, 0, p16, 0, 0, 0, p16, 0, 0, 128, 128, p16, 1, 0, 0, 0,

@@ -260,3 +260,19 @@ def test_transposed_value_operand(dev, src_dtype):
     got = vt.float().cpu().numpy()
     np.testing.assert_array_equal(got[..., :300].transpose(0, 1, 3, 2).view(np.uint32), ref.view(np.uint32))
     assert np.all(got[..., 300:] == 0)
+
+
+def test_empty_batches_return_empty(dev):
+    """Empty leading dimensions (torch gives the storage a null pointer) pass through the
+    quantizer, the Hadamard and the activation prologue as the reference's torch code does."""
+    import torch
+
+    from faquant_amd import _ops
+    from faquant_amd.hif4 import fake_quantize_hif4
+    from faquant_amd.rotation import hadamard_transform
+
+    for dt in (torch.float32, torch.bfloat16):
+        x = torch.empty((0, 3, 128), device=dev, dtype=dt)
+        assert fake_quantize_hif4(x, levels="123").shape == (0, 3, 128)
+        assert _ops.act_qdq_rows(x, levels="123", hadamard=64).shape == (0, 3, 128)
+    assert hadamard_transform(torch.empty((0, 64), device=dev)).shape == (0, 64)
