@@ -518,7 +518,8 @@ __global__ __launch_bounds__(256) void act_qdq_rows_kernel(ActQdqArgs a) {
 // rotation.py:117-135 when a block size is set, one cast back); the activation clamp (bounds
 // in the input dtype, NaN kept); x * companding scale; the online block Hadamard with one
 // cast back; the HiF4 QDQ; x / companding scale.  Every elementwise step rounds to the input
-// dtype as torch does.  One 256-thread workgroup per row, the row in LDS as fp32.
+// dtype as torch does.  One workgroup per row (256 or 512 threads), the row in registers;
+// LDS holds an fp32 copy for the permutation gather and the Hadamard strides above 4.
 constexpr int kActMaxCols = 16384;
 
 struct ActRowArgs {
