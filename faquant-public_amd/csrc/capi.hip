@@ -517,6 +517,19 @@ int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
   if (!o.rot_signs && (o.rot_perm || o.rot_block)) return fail(FAQ_EINVAL, "%s: a rotation needs both signs and permutation", who);
   if (int st = check_block(o.rot_block)) return st;
   if (int st = check_block(o.hadamard)) return st;
+  int online = o.hadamard, gen12 = 0;
+  if (o.hadamard_generalized) {
+    if (o.hadamard) return fail(FAQ_EINVAL, "%s: a block Hadamard and the generalized one are exclusive", who);
+    const int64_t b = cols % 12 ? 0 : cols / 12;
+    if (!(cols & (cols - 1))) {
+      online = static_cast<int>(cols);
+    } else if (b > 0 && !(b & (b - 1))) {
+      online = static_cast<int>(b);
+      gen12 = 1;
+    } else {
+      return fail(FAQ_EINVAL, "unsupported generalized Hadamard dimension: %lld", static_cast<long long>(cols));
+    }
+  }
   if (rows == 0) return FAQ_OK;
   faq::ActRowArgs a{};
   a.x = x;
@@ -533,10 +546,11 @@ int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
   a.act_min = o.act_min;
   a.act_max = o.act_max;
   a.compand = o.compand;
-  a.n = o.hadamard;
-  a.div = sqrt_div(o.hadamard);
+  a.n = online;
+  a.gen12 = gen12;
+  a.div = sqrt_div(gen12 ? static_cast<int>(cols) : online);
   a.quant = levels != 0;
-  const bool uses_lds = o.rot_signs || o.rot_block > 8 || o.hadamard > 8;
+  const bool uses_lds = o.rot_signs || o.rot_block > 8 || online > 8;
   const size_t lds = uses_lds ? faq::act_row_lds_bytes(a.cols) : 0;
   if (lds > device_lds_per_block())
     return fail(FAQ_EUNSUP, "%s: a row of %lld features needs %zu bytes of LDS, the device has %zu", who,

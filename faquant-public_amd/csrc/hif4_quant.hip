@@ -535,8 +535,9 @@ struct ActRowArgs {
   int has_min, has_max;
   float act_min, act_max;   // clamp bounds (rounded to T in the kernel)
   const float* compand;     // [cols] companding scale (values of T), or null
-  int n;                    // 0, or the online block Hadamard size
-  SqrtDiv div;
+  int n;                    // 0, or the online block Hadamard size (with gen12: cols / 12)
+  int gen12;                // 1: the generalized transform of a row of 12 n values
+  SqrtDiv div;              // division by fp32(sqrt(n)) (with gen12: of the row length)
   int quant;                // 1: HiF4 QDQ
 };
 
@@ -595,14 +596,14 @@ __device__ __forceinline__ void fwht_lds_pass(float* lds, int cols, int ls, int 
   }
 }
 
-// Normalized Walsh-Hadamard transform of every b-block of the row (rotation.py:14-29): the
-// stages of stride 1, 2, ..., b / 2 in that order, each pair (i, i + s) becoming
-// (left + right, left - right), then the division by fp32(sqrt(b)).  Strides 1, 2, 4 run in
-// registers; larger strides in passes over LDS of up to three stages (s, 2 s, 4 s) on the
-// values j0 + m s read into registers: the same additions as one stage at a time.  Ends with
-// the transformed row in v.
+// Unnormalized Walsh-Hadamard transform of every b-block of the row (rotation.py:14-29
+// without its division): the stages of stride 1, 2, ..., b / 2 in that order, each pair
+// (i, i + s) becoming (left + right, left - right).  Strides 1, 2, 4 run in registers; larger
+// strides in passes over LDS of up to three stages (s, 2 s, 4 s) on the values j0 + m s read
+// into registers: the same additions as one stage at a time.  Ends with the transformed row
+// in v.
 template <int R, int NT>
-__device__ __forceinline__ void fwht_row(float (&v)[R][8], float* lds, int cols, int b, const SqrtDiv& dv, int tid) {
+__device__ __forceinline__ void fwht_row_raw(float (&v)[R][8], float* lds, int cols, int b, int tid) {
   if (b == 2) fwht_in_chunks<R, 1>(v);
   else if (b == 4) fwht_in_chunks<R, 2>(v);
   else fwht_in_chunks<R, 4>(v);
@@ -633,8 +634,59 @@ __device__ __forceinline__ void fwht_row(float (&v)[R][8], float* lds, int cols,
     // the next user of the LDS row writes it again
     __syncthreads();
   }
+}
+
+// The normalized transform of every b-block: fwht_row_raw, then the division by
+// fp32(sqrt(b)) (b a power of two: the fma form equals the IEEE division on its range).
+template <int R, int NT>
+__device__ __forceinline__ void fwht_row(float (&v)[R][8], float* lds, int cols, int b, const SqrtDiv& dv, int tid) {
+  fwht_row_raw<R, NT>(v, lds, cols, b, tid);
 #pragma unroll
   for (int r = 0; r < R; ++r) div_sqrt_n(v[r], dv);
+}
+
+// The 12-point Hadamard matrix of rotation.py:32-50, row r as a mask of its -1 entries.
+__constant__ uint16_t kH12NegMask[12] = {0xFFE, 0x474, 0x8E8, 0x1D2, 0x3A4, 0x748,
+                                         0xE90, 0xD22, 0xA46, 0x48E, 0x91C, 0x23A};
+
+// generalized_hadamard_transform (rotation.py:53-69) of a row of n = 12 b values (b a power
+// of two): the reference pairs elements 2i, 2i + 1 and concatenates sums before differences,
+// which is the unnormalized FWHT of every b-block; then out[r b + c] = sum_h H12[r][h]
+// W[h b + c], accumulated in h order from 0 as the matmul does (each step one rounding), then
+// the IEEE division by fp32(sqrt(n)) (the fma form is not exact for these divisors).
+template <int R, int NT>
+__device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, int cols, int b, float d, int tid) {
+  fwht_row_raw<R, NT>(v, lds, cols, b, tid);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c0 = 8 * (tid + NT * r);
+    if (c0 < cols)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) lds[lds_pad(c0) + i] = v[r][i];
+  }
+  __syncthreads();
+  for (int c = tid; c < b; c += NT) {
+    float w[12];
+#pragma unroll
+    for (int h = 0; h < 12; ++h) w[h] = lds[lds_pad(h * b + c)];
+#pragma unroll
+    for (int r = 0; r < 12; ++r) {
+      const uint32_t m = kH12NegMask[r];
+      float acc = 0.0f;
+#pragma unroll
+      for (int h = 0; h < 12; ++h) acc = __builtin_fmaf((m >> h) & 1u ? -1.0f : 1.0f, w[h], acc);
+      lds[lds_pad(r * b + c)] = acc;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c0 = 8 * (tid + NT * r);
+    if (c0 < cols)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[r][i] = lds[lds_pad(c0) + i] / d;
+  }
+  __syncthreads();
 }
 
 // One workgroup of NT threads per row of at most 8 NT R values.  R stays at most 4: with
@@ -720,7 +772,8 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
     }
   }
   if (a.n) {
-    fwht_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div, tid);
+    if (a.gen12) generalized_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div.d, tid);
+    else fwht_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div, tid);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll

@@ -74,6 +74,7 @@ class ActOpts(ctypes.Structure):
         ("act_max", _c_float),
         ("compand", _vp),
         ("hadamard", _c_int),
+        ("hadamard_generalized", _c_int),
     ]
 
 

@@ -139,14 +139,17 @@ def act_prep_rows(
     act_max: float | None = None,
     compand: torch.Tensor | None = None,
     hadamard: int = 0,
+    hadamard_generalized: bool = False,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The full activation path of a quantized Linear along the last axis of ``x``
     (faq_act_prep_rows): x * dtype(col_scale); the HiSQ input rotation (fp32 x times
     ``rot_signs``, gathered by ``rot_perm``, the per-block fp32 Hadamard of ``rot_block``
     values when set, one cast back); the clamp to [act_min, act_max] in x's dtype; x times
-    ``compand`` (already in x's dtype); the online block Hadamard; HiF4 QDQ with
-    ``levels``; x / ``compand``.  Output in x's dtype."""
+    ``compand`` (already in x's dtype); the online block Hadamard of ``hadamard`` values, or
+    with ``hadamard_generalized`` the generalized transform of the whole row (rotation.py:
+    53-69: a power of two or 12 times one); HiF4 QDQ with ``levels``; x / ``compand``.
+    Output in x's dtype."""
     _lib.require_device(x, col_scale, rot_signs, rot_perm, compand)
     lib = _lib.load()
     if x.ndim == 0:
@@ -181,6 +184,7 @@ def act_prep_rows(
         act_max=float(act_max) if act_max is not None else 0.0,
         compand=vec(compand, torch.float32, "companding scale"),
         hadamard=int(hadamard or 0),
+        hadamard_generalized=int(bool(hadamard_generalized)),
     )
     _lib.check(
         lib.faq_act_prep_rows(

@@ -61,7 +61,8 @@ class FakeQuantLinear(torch.nn.Module):
     permutation, block Hadamard; quantization.py:201-219), the clamp and the companding
     product and quotient around the QDQ (quantization.py:220-276).  The companding scale
     is computed with torch as the reference computes it (clamp to +-2.079, exp, cast to the
-    input dtype).  The generalized (non-block) online Hadamard raises NotImplementedError.
+    input dtype).  Without a block size the online transform is the generalized one of the
+    whole row (rotation.py:53-69), also in ``act_prep_rows``.
     """
 
     faquant_quantizes_input = True
@@ -97,8 +98,6 @@ class FakeQuantLinear(torch.nn.Module):
         check_hif4_arguments(bits=bits, group_size=activation_group_size, symmetric=symmetric, clip_ratio=clip_ratio)
         if (input_rotation_signs is None) != (input_rotation_permutation is None):
             raise ValueError("the input rotation needs both signs and permutation")
-        if online_hadamard and online_hadamard_block_size is None:
-            raise NotImplementedError("the generalized (non-block) online Hadamard is not implemented on the MI355X")
         self.in_features = linear.in_features
         self.out_features = linear.out_features
         self.quant_format = quant_format
@@ -180,15 +179,16 @@ class FakeQuantLinear(torch.nn.Module):
         from . import _ops
         from .hif4 import HIF4_ACT_SCALE_LEVELS
 
-        block = self.online_hadamard_block_size if self.online_hadamard else 0
+        block = int(self.online_hadamard_block_size or 0) if self.online_hadamard else 0
+        generalized = bool(self.online_hadamard) and self.online_hadamard_block_size is None
         extra = (self.input_rotation_signs is not None or self.activation_min is not None
                  or self.activation_max is not None or self.activation_compand_log_scale is not None)
-        if not extra:
-            xq = _ops.act_qdq_rows(x, levels=HIF4_ACT_SCALE_LEVELS, hadamard=int(block or 0), col_scale=self.input_scale)
+        if not extra and not generalized and block <= 512:
+            xq = _ops.act_qdq_rows(x, levels=HIF4_ACT_SCALE_LEVELS, hadamard=block, col_scale=self.input_scale)
         else:
             perm, compand, bounds = self._prep_vectors(x)
             xq = _ops.act_prep_rows(
                 x, levels=HIF4_ACT_SCALE_LEVELS, col_scale=self.input_scale, rot_signs=self.input_rotation_signs,
                 rot_perm=perm, rot_block=self.input_rotation_block_size, act_min=bounds[0], act_max=bounds[1],
-                compand=compand, hadamard=int(block or 0))
+                compand=compand, hadamard=block, hadamard_generalized=generalized)
         return torch.nn.functional.linear(_lib.forward_only(xq, x), self.weight, self.bias)

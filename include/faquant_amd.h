@@ -180,6 +180,9 @@ typedef struct faq_act_opts {
   float act_min, act_max;   /* the bounds (applied in the input dtype, NaN kept) */
   const float* compand;     /* activation companding scale, already in the input dtype */
   int hadamard;             /* online block Hadamard size, or 0 */
+  int hadamard_generalized; /* 1: the online transform is generalized_hadamard_transform over
+                               the whole row (cols a power of two, or 12 times one;
+                               rotation.py:53-69); hadamard must then be 0 */
 } faq_act_opts;
 
 /*

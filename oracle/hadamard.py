@@ -2,6 +2,7 @@
 
 Follows ``src/faquant/rotation.py``:
   * ``hadamard_transform``                rotation.py:14-29
+  * ``generalized_hadamard_transform``    rotation.py:53-69 (12 * 2^k sizes)
   * ``chunked_block_hadamard_transform``  rotation.py:117-135
 and the two post-RoPE callers that wrap it in one fp32 excursion with a single
 cast back:
@@ -17,7 +18,9 @@ Parity pins (tests/test_oracle_hadamard.py): the dense Sylvester-matrix closed
 form in float64 (as tests/test_hisq_rotation.py:29-43 builds it), orthogonality
 and self-inverse (tests/test_rotation.py:10-18), chunked-equals-full, the exact
 64-point case, and golden vectors written by the reference (fp32, and bf16 / fp16
-tensors with their per-stage rounding).
+tensors with their per-stage rounding); the generalized transform by the Kronecker
+closed form H12 (x) H_b in float64, its orthogonality, and activations the reference's
+FakeQuantLinear wrote with it (tests/golden/linear_act.npz).
 """
 
 from __future__ import annotations
@@ -66,6 +69,51 @@ def block_hadamard_transform(x: np.ndarray, block_size: int) -> np.ndarray:
             f"dimension {x.shape[-1]} must be divisible by power-of-two block_size={block_size}"
         )
     return hadamard_transform(x.reshape(-1, block_size)).reshape(x.shape)
+
+
+# The 12-point Hadamard matrix of rotation.py:32-50, row r as a mask of its -1 entries
+# (bit h set: entry (r, h) is -1).
+H12_NEG_MASKS = (0xFFE, 0x474, 0x8E8, 0x1D2, 0x3A4, 0x748, 0xE90, 0xD22, 0xA46, 0x48E, 0x91C, 0x23A)
+
+
+def hadamard12() -> np.ndarray:
+    """The reference's 12-point Hadamard matrix (float32 entries +-1)."""
+    return np.array([[(-1.0 if (m >> h) & 1 else 1.0) for h in range(12)] for m in H12_NEG_MASKS], dtype=_F32)
+
+
+def generalized_hadamard_transform(x: np.ndarray) -> np.ndarray:
+    """``generalized_hadamard_transform`` (rotation.py:53-69) in float32 over the last axis.
+
+    A power-of-two size is ``hadamard_transform``.  For n = 12 b (b a power of two) the
+    reference's loop pairs elements 2i, 2i + 1 and concatenates sums before differences,
+    which is the unnormalized FWHT of every b-block with the stages in ``hadamard_transform``'s
+    order; then the 12 x 12 matrix mixes the blocks (out[r b + c] = sum_h H12[r, h] W[h b + c]),
+    summed in h order from 0 as the CPU matmul does (an fma chain: each step one rounding),
+    then a true division by fp32(sqrt(n)).
+    """
+    x = np.asarray(x, dtype=_F32)
+    n = x.shape[-1]
+    if _is_power_of_two(n):
+        return hadamard_transform(x)
+    if n % 12 or not _is_power_of_two(n // 12):
+        raise ValueError(f"unsupported generalized Hadamard dimension: {n}")
+    b = n // 12
+    w = x.reshape(-1, b).copy()
+    stride = 1
+    while stride < b:
+        v = w.reshape(-1, b // (2 * stride), 2, stride)
+        left = v[:, :, 0, :]
+        right = v[:, :, 1, :]
+        w = np.concatenate(((left + right)[:, :, None, :], (left - right)[:, :, None, :]), axis=2)
+        w = w.reshape(-1, b).astype(_F32)
+        stride *= 2
+    w = w.reshape(-1, 12, b)
+    h12 = hadamard12()
+    out = np.zeros_like(w)
+    for h in range(12):
+        out = (out + h12[None, :, h, None] * w[:, h : h + 1, :]).astype(_F32)
+    out = (out.reshape(x.shape) / _F32(math.sqrt(n))).astype(_F32)
+    return out
 
 
 def sylvester_matrix(n: int) -> np.ndarray:

@@ -9,8 +9,9 @@ Follows ``FakeQuantLinear.forward`` in src/faquant/quantization.py:199-276, befo
   3. ``x.clamp(min, max)``: the bounds are 0-d fp32 tensors, so torch clamps in x's
      dtype with the bounds rounded to it, and NaN stays NaN             (220-221)
   4. ``x * compand_scale`` with the scale already cast to x's dtype     (222-234)
-  5. the online block Hadamard in fp32 with one cast back, then the HiF4 fake quantizer
-     in x's dtype, or the quantizer alone                              (235-266)
+  5. the online block Hadamard in fp32 with one cast back (without a block size the
+     generalized transform of the whole row, rotation.py:53-69), then the HiF4 fake
+     quantizer in x's dtype, or the quantizer alone                    (235-266)
   6. ``x / compand_scale``                                             (267-268)
 Every elementwise torch op on a bf16 / fp16 tensor computes in fp32 and rounds to the
 dtype; on fp32 tensors the rounding is the identity.
@@ -54,6 +55,7 @@ def fake_quant_linear_input(
     act_max: float | None = None,
     compand: np.ndarray | None = None,
     hadamard: int = 0,
+    hadamard_generalized: bool = False,
 ) -> np.ndarray:
     """The activation F.linear receives, for x of values of ``dtype`` ("bfloat16",
     "float16" or "float32") given as float32.  ``compand`` is the companding scale already
@@ -82,6 +84,8 @@ def fake_quant_linear_input(
         v = rnd(v * c)
     if hadamard:
         v = rnd(OH.block_hadamard_transform(v, hadamard))
+    elif hadamard_generalized:
+        v = rnd(OH.generalized_hadamard_transform(v))
     if levels:
         v = OQ.fake_quantize_hif4(v, levels, dtype=dtype)
     if c is not None:

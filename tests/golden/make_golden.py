@@ -25,8 +25,9 @@ Fixtures (numpy .npz, float32 unless noted):
   linear_act.npz      the activation FakeQuantLinear.forward hands to F.linear (F.linear
                       replaced by the identity while it runs): input scale, HiSQ rotation
                       from derive_hisq_rotation with and without its block Hadamard,
-                      clamp, companding and the online block Hadamard, in bf16, fp16 and
-                      fp32.  Inputs and options are stored with the output.
+                      clamp, companding and the online block or generalized Hadamard, in
+                      bf16, fp16 and fp32.  Inputs and options are stored with the output;
+                      also generalized_hadamard_transform on fp32 rows (keys gen<n>__x/y).
 
 ``python tests/golden/make_golden.py hadamard_native`` (or ``linear_act``) writes only that
 file.
@@ -228,7 +229,14 @@ LINEAR_ACT_CASES = {
     "bf16_4096_all": ("bfloat16", 4096, 8, True, 1024, (-6.1, 5.2), 32, 4096),
     "fp16_768_rot256_comp": ("float16", 768, 10, False, 256, (None, None), 12, 0),
     "bf16_clamp_only": ("bfloat16", 640, 9, False, 0, (-0.7, 0.45), 0, 0),
+    # online Hadamard without a block size: generalized_hadamard_transform of the row
+    "bf16_generalized_768": ("bfloat16", 768, 11, True, 256, (None, None), 12, None),
+    "fp32_generalized_384_clamp": ("float32", 384, 7, False, 0, (-2.5, 2.5), 0, None),
+    "bf16_generalized_pow2_512": ("bfloat16", 512, 6, False, 0, (None, None), 8, None),
 }
+
+# sizes of the generalized transform's own vectors (fp32 rows, rotation.py:53-69)
+GENERALIZED_SIZES = (12, 24, 192, 768, 3072, 12288, 256)
 
 
 def make_linear_act() -> dict[str, np.ndarray]:
@@ -267,7 +275,7 @@ def make_linear_act() -> dict[str, np.ndarray]:
             mod = ref_quant.FakeQuantLinear(
                 lin, quant_format="hif4", bits=4, weight_group_size=64, activation_group_size=64,
                 symmetric=True, clip_ratio=1.0, quantize_weight=False,
-                online_hadamard=bool(online), online_hadamard_block_size=online or None, **kw,
+                online_hadamard=online is None or bool(online), online_hadamard_block_size=online or None, **kw,
             )
             seen.clear()
             mod(xt)
@@ -279,7 +287,7 @@ def make_linear_act() -> dict[str, np.ndarray]:
                     out[f"{case}__{key}"] = val.numpy()
                 else:  # a block size (0 for None) or a bound
                     out[f"{case}__{key}"] = np.array(0 if val is None else val)
-            out[f"{case}__online"] = np.array(online)
+            out[f"{case}__online"] = np.array(-1 if online is None else online)  # -1: generalized
             if comp_len:
                 # the companding scale forward multiplies by, recomputed by the same expression
                 # on the same tensor: torch's CPU exp differs between vector units, so the
@@ -291,6 +299,14 @@ def make_linear_act() -> dict[str, np.ndarray]:
             print(f"linear_act {case}: {tuple(xt.shape)} {dt_name} {sorted(kw)} online={online}")
     finally:
         ref_quant.F = real_f
+    from faquant.rotation import generalized_hadamard_transform
+
+    g = inputs.rng(140)
+    for n in GENERALIZED_SIZES:
+        rows = 5 if n <= 768 else 2
+        x = (g.standard_normal((rows, n)) * np.exp(g.standard_normal((rows, 1)) * 2)).astype(np.float32)
+        out[f"gen{n}__x"] = x
+        out[f"gen{n}__y"] = generalized_hadamard_transform(torch.from_numpy(x)).numpy()
     return out
 
 

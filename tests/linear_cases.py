@@ -26,7 +26,7 @@ def golden_cases() -> dict[str, dict]:
     """case -> {"x", "y", "dtype", "levels", "kw"}; "kw" are the oracle's keyword arguments
     (``oracle.linear.fake_quant_linear_input``)."""
     g = load_golden(GOLDEN)
-    names = sorted({k.split("__")[0] for k in g if "__" in k})
+    names = sorted({k.split("__")[0] for k in g if "__" in k and not k.startswith("gen")})
     out = {}
     for name in names:
         def get(key, default=None):
@@ -48,6 +48,16 @@ def golden_cases() -> dict[str, dict]:
         if get("activation_compand_log_scale") is not None:
             # the scale the reference multiplied by (exp's last bit depends on the CPU)
             kw["compand"] = get("compand_scale")
-        kw["hadamard"] = int(get("online"))
+        online = int(get("online"))
+        kw["hadamard"] = max(online, 0)
+        if online < 0:
+            kw["hadamard_generalized"] = True
         out[name] = {"x": x, "y": get("y"), "dtype": dtype, "levels": str(g["levels"]), "kw": kw}
     return out
+
+
+def generalized_vectors() -> dict[int, tuple]:
+    """n -> (x, y) of the reference's generalized_hadamard_transform on fp32 rows."""
+    g = load_golden(GOLDEN)
+    sizes = sorted({int(k[3:].split("__")[0]) for k in g if k.startswith("gen")})
+    return {n: (g[f"gen{n}__x"], g[f"gen{n}__y"]) for n in sizes}

@@ -28,7 +28,10 @@ def checker(tmp_path_factory):
     return exe
 
 
-@pytest.mark.parametrize("n", [2, 8, 32, 128, 512])
+# 2048 and 8192: the activation path's block Hadamard (blocks up to 16384).  The divisors of
+# the generalized transform, fp32(sqrt(12 * 2^k)), are not in this list: an exhaustive run
+# finds a few inputs where the fma form differs, so that transform divides.
+@pytest.mark.parametrize("n", [2, 8, 32, 128, 512, 2048, 8192])
 def test_fma_division_equals_ieee_division(checker, n):
     out = subprocess.run([checker, str(n)], capture_output=True, text=True, timeout=600)
     print(out.stdout.strip())

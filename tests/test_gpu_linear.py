@@ -103,8 +103,6 @@ def test_fake_quant_linear_unsupported_options_raise(dev):
     lin = torch.nn.Linear(64, 64).to(dev)
     common = dict(quant_format="hif4", bits=4, weight_group_size=64, activation_group_size=64, symmetric=True,
                   clip_ratio=1.0)
-    with pytest.raises(NotImplementedError):
-        FakeQuantLinear(lin, **common, online_hadamard=True)
     with pytest.raises(ValueError):
         FakeQuantLinear(lin, **{**common, "weight_group_size": 32})
     with pytest.raises(ValueError, match="signs and permutation"):
@@ -131,6 +129,7 @@ def _prep_on_device(x, dtype, dev, levels, kw):
         rot_signs=t(kw.get("rot_signs"), torch.int8), rot_perm=t(kw.get("rot_perm"), torch.int64),
         rot_block=kw.get("rot_block"), act_min=kw.get("act_min"), act_max=kw.get("act_max"),
         compand=t(kw.get("compand")), hadamard=kw.get("hadamard", 0),
+        hadamard_generalized=kw.get("hadamard_generalized", False),
     )
 
 
@@ -201,6 +200,24 @@ def test_act_prep_rows_matches_oracle_bitwise(dev, name, levels, dtype):
     assert _same(got, ref)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+@pytest.mark.parametrize("cols", [192, 768, 3072, 12288, 1024])
+def test_act_prep_rows_generalized_hadamard_matches_oracle(dev, cols, dtype):
+    """The online transform without a block size: generalized_hadamard_transform of the row
+    (12 * 2^k, or a power of two), alone and after the rotation, clamp and companding."""
+    from oracle import linear as OL
+
+    for extras in (False, True):
+        x, kw = _random_prep_case(cols + extras, cols, dtype, rot=extras, rot_block=64 if extras else None,
+                                  clamp=extras, comp=extras, hadamard=0, scale=extras)
+        kw["hadamard_generalized"] = True
+        print(f"[act_prep generalized] cols={cols} {dtype} extras={extras}", flush=True)
+        got = _prep_on_device(x, dtype, dev, "123", kw).float().cpu().numpy()
+        assert _same(got, OL.fake_quant_linear_input(x, dtype, levels="123", **kw))
+    with pytest.raises(ValueError, match="unsupported generalized Hadamard dimension"):  # 320 = 5 * 64
+        _prep_on_device(np.ones((2, 320), np.float32), dtype, dev, "123", {"hadamard_generalized": True})
+
+
 def test_act_prep_rows_nan_and_no_quantizer(dev):
     from oracle import linear as OL
 
@@ -252,6 +269,24 @@ def test_act_prep_rows_edges(dev):
                                compand=comp[2:])
     assert empty.shape == (0, 512)
     assert _ops.act_qdq_rows(torch.empty((0, 3, 512), device=dev, dtype=torch.bfloat16), levels="123").shape == (0, 3, 512)
+
+
+def test_fake_quant_linear_generalized_online_hadamard(dev):
+    """online_hadamard without a block size (Qwen3-8B down_proj has 12288 = 12 * 1024 input
+    features): the module's activation equals the oracle's generalized transform path."""
+    from oracle import linear as OL
+    from faquant_amd.hif4 import HIF4_ACT_SCALE_LEVELS
+    from faquant_amd.quantization import FakeQuantLinear
+
+    g = OI.rng(33)
+    for n in (768, 1024):
+        lin = torch.nn.Linear(n, 64, bias=False).to(dev, torch.bfloat16)
+        mod = FakeQuantLinear(lin, quant_format="hif4", bits=4, weight_group_size=64, activation_group_size=64,
+                              symmetric=True, clip_ratio=1.0, online_hadamard=True)
+        x = OQ.bf16_round(g.standard_normal((9, n)).astype(np.float32))
+        act = OL.fake_quant_linear_input(x, "bfloat16", levels=HIF4_ACT_SCALE_LEVELS, hadamard_generalized=True)
+        expected = torch.nn.functional.linear(to_dev(act, dev, torch.bfloat16), mod.weight, mod.bias)
+        assert torch.equal(mod(to_dev(x, dev, torch.bfloat16)), expected)
 
 
 def test_fake_quant_linear_full_path_equals_reference_composition(dev):

@@ -7,7 +7,7 @@ import pytest
 from oracle import hadamard as OH
 from oracle import hif4 as OQ
 from oracle import linear as OL
-from tests.linear_cases import golden_cases
+from tests.linear_cases import generalized_vectors, golden_cases
 
 CASES = golden_cases()
 
@@ -25,7 +25,8 @@ def test_fixtures_cover_every_step():
         keys |= {k for k, v in c["kw"].items() if v is not None and not (np.isscalar(v) and v == 0)}
         if c["kw"].get("rot_signs") is not None:
             keys.add("rot_block" if c["kw"]["rot_block"] else "rot_no_block")
-    assert {"input_scale", "rot_signs", "rot_block", "rot_no_block", "act_min", "act_max", "compand", "hadamard"} <= keys
+    assert {"input_scale", "rot_signs", "rot_block", "rot_no_block", "act_min", "act_max", "compand", "hadamard",
+            "hadamard_generalized"} <= keys
     assert {c["dtype"] for c in CASES.values()} == {"bfloat16", "float16", "float32"}
 
 
@@ -76,3 +77,26 @@ def test_companding_round_trip_without_quantizer():
     c = np.exp2(np.random.default_rng(3).integers(-3, 4, 128)).astype(np.float32)
     y = OL.fake_quant_linear_input(x, "bfloat16", levels=None, compand=c)
     np.testing.assert_array_equal(y, x)
+
+
+@pytest.mark.parametrize("n", sorted(generalized_vectors()))
+def test_generalized_hadamard_matches_reference(n):
+    x, y = generalized_vectors()[n]
+    np.testing.assert_array_equal(OH.generalized_hadamard_transform(x), y)
+
+
+def test_generalized_hadamard_closed_form():
+    """(H12 kron H_b) x / sqrt(12 b) in float64, orthogonal: H12 H12^T = 12 I."""
+    h12 = OH.hadamard12().astype(np.float64)
+    np.testing.assert_array_equal(h12 @ h12.T, 12 * np.eye(12))
+    g = np.random.default_rng(4)
+    for b in (1, 2, 16, 64):
+        n = 12 * b
+        x = g.standard_normal((3, n)).astype(np.float32)
+        dense = np.kron(h12, OH.sylvester_matrix(b)) / np.sqrt(n)
+        want = x.astype(np.float64) @ dense.T
+        got = OH.generalized_hadamard_transform(x)
+        np.testing.assert_allclose(got, want, rtol=0, atol=2e-6 * np.abs(want).max())
+        np.testing.assert_allclose(np.linalg.norm(got, axis=1), np.linalg.norm(x, axis=1), rtol=2e-6)
+    with pytest.raises(ValueError, match="unsupported generalized Hadamard dimension"):
+        OH.generalized_hadamard_transform(np.zeros((1, 36), np.float32))
