@@ -1,9 +1,12 @@
 """Normalized Walsh-Hadamard transforms on the MI355X: drop-in for faquant.rotation (hot-path subset).
 
-Reference: src/faquant/rotation.py:14-29 (``hadamard_transform``) and 117-135
-(``chunked_block_hadamard_transform``).  The HIP kernel runs the same fp32
-butterfly stages in the same order (strides 1, 2, ..., n/2) and divides by
-fp32(sqrt(n)) exactly as CPU torch does, so fp32 results are bit-identical.
+Reference: src/faquant/rotation.py:14-29 (``hadamard_transform``), 53-84
+(``generalized_hadamard_transform`` and its chunked form) and 117-135
+(``chunked_block_hadamard_transform``).  The HIP kernels run the same fp32
+butterfly stages in the same order (strides 1, 2, ..., n/2) and divide by
+fp32(sqrt(n)) exactly as CPU torch does, so fp32 results are bit-identical.  Blocks
+above 512 and the generalized transform run in the row kernel of the Linear activation
+path (rows of at most 16384 features, a multiple of 64).
 """
 
 from __future__ import annotations
@@ -26,6 +29,8 @@ def hadamard_transform(x: torch.Tensor) -> torch.Tensor:
     if not _is_power_of_two(size):
         raise ValueError(f"Hadamard dimension must be a power of two, got {size}")
     if x.dtype == torch.float32:
+        if size > 512:
+            return _row_path(x, hadamard=size)
         return _ops.hadamard_rows(x, size, torch.float32)
     if x.dtype in (torch.bfloat16, torch.float16):
         return _ops.hadamard_rows_native(x)
@@ -42,4 +47,41 @@ def chunked_block_hadamard_transform(x: torch.Tensor, *, block_size: int, chunk_
         raise ValueError(
             f"dimension {x.shape[-1]} must be divisible by power-of-two block_size={block_size}"
         )
+    if block_size > 512:
+        return _row_path(x, hadamard=block_size)
     return _ops.hadamard_rows(x, block_size, x.dtype)
+
+
+def _row_path(x: torch.Tensor, **kw) -> torch.Tensor:
+    """fp32 transform of each row with one cast back to x's dtype (the activation row
+    kernel without its quantizer)."""
+    cols = x.shape[-1]
+    if cols % 64 or cols > 16384:
+        raise NotImplementedError(
+            f"transforms of {cols} values run on rows of a multiple of 64 features, at most 16384"
+        )
+    return _ops.act_prep_rows(x, levels=None, **kw)
+
+
+def generalized_hadamard_transform(x: torch.Tensor) -> torch.Tensor:
+    """Normalized Hadamard transform for power-of-two or 12 * power-of-two axes
+    (rotation.py:53-69).  The reference computes in x's dtype; this build takes fp32 input
+    (exact), and other dtypes through ``chunked_generalized_hadamard_transform``."""
+    size = x.shape[-1]
+    if _is_power_of_two(size):
+        return hadamard_transform(x)
+    if size % 12 or not _is_power_of_two(size // 12):
+        raise ValueError(f"unsupported generalized Hadamard dimension: {size}")
+    if x.dtype != torch.float32:
+        raise NotImplementedError(f"generalized_hadamard_transform on the MI355X takes fp32 input, got {x.dtype}")
+    return _row_path(x, hadamard_generalized=True)
+
+
+def chunked_generalized_hadamard_transform(x: torch.Tensor, *, chunk_rows: int = 256) -> torch.Tensor:
+    """The generalized transform in fp32 with one cast back to x's dtype (rotation.py:72-84).
+    ``chunk_rows`` only bounded the reference's fp32 temporaries."""
+    del chunk_rows
+    size = x.shape[-1]
+    if not _is_power_of_two(size) and (size % 12 or not _is_power_of_two(size // 12)):
+        raise ValueError(f"unsupported generalized Hadamard dimension: {size}")
+    return _row_path(x, hadamard_generalized=True)

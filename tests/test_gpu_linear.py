@@ -368,3 +368,31 @@ def test_hif4_linear_equals_quantize_then_linear(dev):
         HiF4Linear(lin, weight_qdq=lambda w: w * 1.001, input_qdq=qdq, device=dev)
     with pytest.raises(ValueError, match="HiF4 weight of shape"):
         HiF4Linear(lin, weight_qdq=qdq, input_qdq=qdq, device=dev, weight=torch.zeros(3, 3))
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_rotation_dropins_on_the_row_kernel(dev, dtype):
+    """rotation.py drop-ins that run on the activation row kernel: block sizes above 512,
+    the generalized transform (fp32) and its chunked form (fp32 math, one cast back)."""
+    from oracle import hadamard as OH
+    from faquant_amd import rotation
+
+    g = OI.rng(44)
+    rnd = OQ.bf16_round if dtype == "bfloat16" else (lambda a: np.asarray(a, np.float32))
+    tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float32
+    for cols, block in ((2048, 1024), (12288, 4096), (16384, 16384)):
+        x = rnd(g.standard_normal((6, cols)).astype(np.float32) * 3)
+        got = rotation.chunked_block_hadamard_transform(to_dev(x, dev, tdt), block_size=block)
+        assert got.dtype == tdt and _same(got.float().cpu().numpy(), rnd(OH.block_hadamard_transform(x, block)))
+    for cols in (768, 12288, 2048):
+        x = rnd(g.standard_normal((5, cols)).astype(np.float32))
+        got = rotation.chunked_generalized_hadamard_transform(to_dev(x, dev, tdt))
+        assert _same(got.float().cpu().numpy(), rnd(OH.generalized_hadamard_transform(x)))
+        if dtype == "float32":
+            got = rotation.generalized_hadamard_transform(to_dev(x, dev))
+            assert _same(got.cpu().numpy(), OH.generalized_hadamard_transform(x))
+    if dtype == "float32":
+        x = g.standard_normal((3, 4096)).astype(np.float32)
+        assert _same(rotation.hadamard_transform(to_dev(x, dev)).cpu().numpy(), OH.hadamard_transform(x))
+    with pytest.raises(ValueError, match="unsupported generalized"):
+        rotation.generalized_hadamard_transform(torch.zeros((1, 320), device=dev))
