@@ -154,9 +154,10 @@ class FakeQuantLinear(torch.nn.Module):
         device and dtype and recomputed when a buffer is modified in place or replaced."""
         tensors = (self.input_rotation_permutation, self.activation_compand_log_scale, self.activation_min,
                    self.activation_max)
-        key = (x.device, x.dtype) + tuple(None if t is None else (id(t), t._version) for t in tensors)
+        key = (x.device, x.dtype) + tuple(None if t is None else t._version for t in tensors)
         cached = getattr(self, "_prep_cache", None)
-        if cached is not None and cached[0] == key:
+        # the cache holds the buffer objects themselves, so a replaced buffer never matches
+        if cached is not None and cached[0] == key and all(a is b for a, b in zip(cached[2], tensors)):
             return cached[1]
         perm = None
         if self.input_rotation_permutation is not None:
@@ -172,7 +173,7 @@ class FakeQuantLinear(torch.nn.Module):
         bounds = (None if self.activation_min is None else float(self.activation_min),
                   None if self.activation_max is None else float(self.activation_max))
         value = (perm, compand, bounds)
-        self._prep_cache = (key, value)
+        self._prep_cache = (key, value, tensors)
         return value
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

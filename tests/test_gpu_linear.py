@@ -334,6 +334,14 @@ def test_fake_quant_linear_full_path_equals_reference_composition(dev):
     )
     expected = torch.nn.functional.linear(to_dev(act, dev, torch.bfloat16), mod.weight, mod.bias)
     assert torch.equal(mod(to_dev(x, dev, torch.bfloat16)).reshape(-1, m), expected)
+    # and so is a replaced buffer
+    mod.activation_max = torch.tensor(2.0, device=dev)
+    act = OL.fake_quant_linear_input(
+        x.reshape(-1, n), "bfloat16", levels=HIF4_ACT_SCALE_LEVELS, input_scale=scale, rot_signs=signs, rot_perm=perm,
+        rot_block=256, act_min=-2.5, act_max=2.0, compand=comp.float().cpu().numpy(), hadamard=128,
+    )
+    expected = torch.nn.functional.linear(to_dev(act, dev, torch.bfloat16), mod.weight, mod.bias)
+    assert torch.equal(mod(to_dev(x, dev, torch.bfloat16)).reshape(-1, m), expected)
 
 
 def test_hif4_linear_equals_quantize_then_linear(dev):
