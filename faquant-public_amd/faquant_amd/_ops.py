@@ -19,6 +19,19 @@ HEAD_DIM = 128
 KEY_TILE = 128
 
 
+def _checked_out(out: torch.Tensor | None, like: torch.Tensor, shape=None, dtype=None, unit_last_only=False):
+    """``out`` if it can take the result (device, dtype, shape, and contiguous or, with
+    ``unit_last_only``, a unit last stride), else a ValueError; a new tensor when None."""
+    shape = tuple(like.shape) if shape is None else tuple(shape)
+    dtype = like.dtype if dtype is None else dtype
+    if out is None:
+        return torch.empty(shape, device=like.device, dtype=dtype)
+    if out.device != like.device or out.dtype != dtype or tuple(out.shape) != shape:
+        raise ValueError(f"out must be a {dtype} tensor of shape {shape} on {like.device}")
+    if not (out.stride(-1) == 1 if unit_last_only else out.is_contiguous()):
+        raise ValueError("out must be contiguous" if not unit_last_only else "out must have a unit last stride")
+    return out
+
 def _pad_keys(length: int) -> int:
     return max(KEY_TILE, (length + KEY_TILE - 1) // KEY_TILE * KEY_TILE)
 
@@ -46,7 +59,7 @@ def qdq_rows(
         raise ValueError("HiF4 fake quantization does not support an empty axis")
     xc = x.contiguous()
     rows = xc.numel() // cols
-    y = torch.empty_like(xc) if out is None else out
+    y = _checked_out(out, xc)
     groups = (cols + 63) // 64
     lead = tuple(x.shape[:-1])
     extra = {}
@@ -157,7 +170,7 @@ def act_prep_rows(
     cols = x.shape[-1]
     xc = x.contiguous()
     rows = xc.numel() // cols if cols else 0
-    y = torch.empty_like(xc) if out is None else out
+    y = _checked_out(out, xc)
     keep = []
 
     def vec(t, dtype, name):
@@ -214,7 +227,7 @@ def act_qdq_rows(
     cols = x.shape[-1]
     xc = x.contiguous()
     rows = xc.numel() // cols if cols else 0
-    y = torch.empty_like(xc) if out is None else out
+    y = _checked_out(out, xc)
     sc = None
     if col_scale is not None:
         sc = col_scale.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
@@ -272,7 +285,7 @@ def operand_prep(
     B, H, L, _ = x.shape
     sb, sh, sl = _bhld_strides(x)
     rdt = round_dtype or x.dtype
-    y = torch.empty((B, H, L, HEAD_DIM), device=x.device, dtype=torch.bfloat16) if out is None else out
+    y = _checked_out(out, x, (B, H, L, HEAD_DIM), torch.bfloat16, unit_last_only=True)
     rot = torch.empty((B, H, L, HEAD_DIM), device=x.device, dtype=rdt) if want_rotated else None
 
     def per_head(t):

@@ -404,3 +404,21 @@ def test_rotation_dropins_on_the_row_kernel(dev, dtype):
         assert _same(rotation.hadamard_transform(to_dev(x, dev)).cpu().numpy(), OH.hadamard_transform(x))
     with pytest.raises(ValueError, match="unsupported generalized"):
         rotation.generalized_hadamard_transform(torch.zeros((1, 320), device=dev))
+
+
+def test_output_tensors_are_checked(dev):
+    """A caller-provided output of the wrong shape, dtype or layout is refused before any
+    launch (the kernels write through its pointer)."""
+    from faquant_amd import _ops
+
+    x = torch.zeros((4, 256), device=dev, dtype=torch.bfloat16)
+    for bad in (torch.empty((4, 128), device=dev, dtype=torch.bfloat16),
+                torch.empty((4, 256), device=dev, dtype=torch.float32),
+                torch.empty((256, 4), device=dev, dtype=torch.bfloat16).t()):
+        with pytest.raises(ValueError, match="out must"):
+            _ops.act_qdq_rows(x, levels="123", out=bad)
+        with pytest.raises(ValueError, match="out must"):
+            _ops.act_prep_rows(x, levels="123", out=bad)
+    q = torch.zeros((1, 2, 8, 128), device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="out must"):
+        _ops.operand_prep(q, levels="123", out=torch.empty((1, 2, 4, 128), device=dev, dtype=torch.bfloat16))
