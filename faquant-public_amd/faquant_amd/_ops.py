@@ -615,6 +615,9 @@ def attention_fwd(
     Hkv = k.shape[1]
     if D != HEAD_DIM or k.shape[-1] != HEAD_DIM:
         raise NotImplementedError(f"the HIP attention kernel supports head_dim 128, got {D}")
+    _check_attention_tensors(q, out, row_den, B, Hq, Lq)
+    if k.shape[0] != B or k.shape[2] < int(key_length) or tuple(vt.shape[:3]) != (B, Hkv, HEAD_DIM):
+        raise ValueError("k must be [B, Hkv, >= key_length, 128] and vt [B, Hkv, 128, Lpad]")
     for t in (q, k, vt):
         if t.dtype != torch.bfloat16:
             raise TypeError("attention operands must be bf16")
@@ -649,6 +652,15 @@ def attention_fwd(
     )
     return out
 
+
+
+def _check_attention_tensors(q, out, row_den, B, Hq, Lq):
+    """The output and row denominators must cover every query row the kernels write."""
+    if tuple(out.shape) != (B, Hq, Lq, HEAD_DIM):
+        raise ValueError(f"attention output must be [B, Hq, Lq, 128] = {(B, Hq, Lq, HEAD_DIM)}, got {tuple(out.shape)}")
+    if row_den is not None and (row_den.dtype != torch.float32 or not row_den.is_contiguous()
+                                or tuple(row_den.shape) != (B, Hq, Lq)):
+        raise ValueError("row_den must be a contiguous fp32 [B, Hq, Lq] tensor")
 
 def decode_shaped(Hq: int, Hkv: int, Lq: int) -> bool:
     """Whether faq_attention_decode takes a call: all query rows of a KV head (G heads x Lq
@@ -703,6 +715,7 @@ def attention_decode(
     B, Hq, Lq, D = q.shape
     if D != HEAD_DIM or q.dtype != torch.bfloat16:
         raise NotImplementedError("the decode kernel takes bf16 queries with head_dim 128")
+    _check_attention_tensors(q, out, row_den, B, Hq, Lq)
     if out.dtype not in (torch.float32, torch.bfloat16) or out.stride(3) != 1:
         raise ValueError("attention output must be fp32 or bf16 with a unit stride along head_dim")
     Lk = int(key_length)

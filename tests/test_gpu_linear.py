@@ -422,3 +422,23 @@ def test_output_tensors_are_checked(dev):
     q = torch.zeros((1, 2, 8, 128), device=dev, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="out must"):
         _ops.operand_prep(q, levels="123", out=torch.empty((1, 2, 4, 128), device=dev, dtype=torch.bfloat16))
+
+
+def test_attention_wrappers_check_output_extent(dev):
+    """attention_fwd / attention_decode refuse an output or K that does not cover the rows
+    and keys they would touch."""
+    from faquant_amd import _ops
+
+    q = torch.zeros((1, 4, 8, 128), device=dev, dtype=torch.bfloat16)
+    k = torch.zeros((1, 2, 256, 128), device=dev, dtype=torch.bfloat16)
+    vt = torch.zeros((1, 2, 128, 256), device=dev, dtype=torch.bfloat16)
+    kw = dict(causal=True, scale=0.088, quant_p=True, p_levels="123", norm_same=True)
+    with pytest.raises(ValueError, match="attention output must be"):
+        _ops.attention_fwd(q, k, vt, 256, out=torch.empty((1, 4, 4, 128), device=dev), **kw)
+    with pytest.raises(ValueError, match="k must be"):
+        _ops.attention_fwd(q, k[:, :, :100], vt, 256, out=torch.empty((1, 4, 8, 128), device=dev), **kw)
+    with pytest.raises(ValueError, match="row_den"):
+        _ops.attention_fwd(q, k, vt, 256, out=torch.empty((1, 4, 8, 128), device=dev),
+                           row_den=torch.empty((1, 4, 4), device=dev), **kw)
+    with pytest.raises(ValueError, match="attention output must be"):
+        _ops.attention_decode(q[:, :, :1], 256, k=k, v=k, out=torch.empty((1, 4, 2, 128), device=dev), **kw)
