@@ -722,7 +722,8 @@ def attention_decode(
     if packed is None:
         if k is None or v is None or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
             raise TypeError("bf16 k and v are required without packed K/V")
-        if k.shape[-2] < Lk or v.shape[-2] < Lk or k.shape[-1] != HEAD_DIM or v.shape[-1] != HEAD_DIM:
+        if (k.shape[-2] < Lk or v.shape[-2] < Lk or k.shape[-1] != HEAD_DIM or v.shape[-1] != HEAD_DIM
+                or k.shape[0] != B or v.shape[0] != B or v.shape[1] != k.shape[1]):
             raise ValueError("k and v must be [B, Hkv, >= key_length, 128]")
         Hkv = k.shape[1]
         kargs = (k.data_ptr(), *_bhld_strides(k), v.data_ptr(), *_bhld_strides(v))
@@ -730,7 +731,8 @@ def attention_decode(
     else:
         kc, vc = packed
         Hkv = kc.codes.shape[1]
-        if kc.length < Lk or vc.length < Lk or vc.codes.shape[1] != Hkv:
+        if (kc.length < Lk or vc.length < Lk or vc.codes.shape[1] != Hkv or kc.codes.shape[0] != B
+                or vc.codes.shape[0] != B):
             raise ValueError("the packed K/V caches must hold key_length rows of the same heads")
         kargs = (0, 0, 0, 0, 0, 0, 0, 0)
         kp, vp = kc.descriptor(), vc.descriptor()
