@@ -72,22 +72,29 @@ void launch_act(const faq::ActQdqArgs& a, int levels, int64_t threads, hipStream
   else hipLaunchKernelGGL((faq::act_qdq_rows_kernel<T, 123>), grid, dim3(256), 0, st, a);
 }
 
-template <typename T, int R, int NT>
-void launch_act_row_r(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
+template <typename T, int R, int NT, bool G>
+void launch_act_row_g(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.rows));
-  if (levels == 12) hipLaunchKernelGGL((faq::act_row_kernel<T, 12, R, NT>), grid, dim3(NT), lds, st, a);
-  else if (levels == 13) hipLaunchKernelGGL((faq::act_row_kernel<T, 13, R, NT>), grid, dim3(NT), lds, st, a);
-  else hipLaunchKernelGGL((faq::act_row_kernel<T, 123, R, NT>), grid, dim3(NT), lds, st, a);
+  if (levels == 12) hipLaunchKernelGGL((faq::act_row_kernel<T, 12, R, NT, G>), grid, dim3(NT), lds, st, a);
+  else if (levels == 13) hipLaunchKernelGGL((faq::act_row_kernel<T, 13, R, NT, G>), grid, dim3(NT), lds, st, a);
+  else hipLaunchKernelGGL((faq::act_row_kernel<T, 123, R, NT, G>), grid, dim3(NT), lds, st, a);
 }
 
-// 8-value chunks per lane and threads per row: 256 threads with 1, 2 or 4 chunks each up to
-// 8192 features, 512 threads with 4 beyond.
+template <typename T, int R, int NT>
+void launch_act_row_r(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
+  if (a.gen12) launch_act_row_g<T, R, NT, true>(a, levels, lds, st);
+  else launch_act_row_g<T, R, NT, false>(a, levels, lds, st);
+}
+
+// 8-value chunks per lane and threads per row: 256 threads with 1 or 2 chunks each up to
+// 4096 features, then 512 and 1024 threads with 2 (more waves per row keep more loads in
+// flight: at 12288 features 1024 threads take 0.94 of the time of 512 with 4 chunks).
 template <typename T>
 void launch_act_row(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
   if (a.cols <= 2048) launch_act_row_r<T, 1, 256>(a, levels, lds, st);
   else if (a.cols <= 4096) launch_act_row_r<T, 2, 256>(a, levels, lds, st);
-  else if (a.cols <= 8192) launch_act_row_r<T, 4, 256>(a, levels, lds, st);
-  else launch_act_row_r<T, 4, 512>(a, levels, lds, st);
+  else if (a.cols <= 8192) launch_act_row_r<T, 2, 512>(a, levels, lds, st);
+  else launch_act_row_r<T, 2, 1024>(a, levels, lds, st);
 }
 
 // LDS bytes one workgroup of the current device may hold (cached per device; 64 KiB when

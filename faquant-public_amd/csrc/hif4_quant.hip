@@ -645,9 +645,10 @@ __device__ __forceinline__ void fwht_row(float (&v)[R][8], float* lds, int cols,
   for (int r = 0; r < R; ++r) div_sqrt_n(v[r], dv);
 }
 
-// The 12-point Hadamard matrix of rotation.py:32-50, row r as a mask of its -1 entries.
-__constant__ uint16_t kH12NegMask[12] = {0xFFE, 0x474, 0x8E8, 0x1D2, 0x3A4, 0x748,
-                                         0xE90, 0xD22, 0xA46, 0x48E, 0x91C, 0x23A};
+// The 12-point Hadamard matrix of rotation.py:32-50, row r as a mask of its -1 entries
+// (compile-time: each term of the mix is an add or a subtract).
+constexpr uint16_t kH12NegMask[12] = {0xFFE, 0x474, 0x8E8, 0x1D2, 0x3A4, 0x748,
+                                      0xE90, 0xD22, 0xA46, 0x48E, 0x91C, 0x23A};
 
 // generalized_hadamard_transform (rotation.py:53-69) of a row of n = 12 b values (b a power
 // of two): the reference pairs elements 2i, 2i + 1 and concatenates sums before differences,
@@ -671,10 +672,9 @@ __device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, in
     for (int h = 0; h < 12; ++h) w[h] = lds[lds_pad(h * b + c)];
 #pragma unroll
     for (int r = 0; r < 12; ++r) {
-      const uint32_t m = kH12NegMask[r];
       float acc = 0.0f;
 #pragma unroll
-      for (int h = 0; h < 12; ++h) acc = __builtin_fmaf((m >> h) & 1u ? -1.0f : 1.0f, w[h], acc);
+      for (int h = 0; h < 12; ++h) acc = __builtin_fmaf((kH12NegMask[r] >> h) & 1u ? -1.0f : 1.0f, w[h], acc);
       lds[lds_pad(r * b + c)] = acc;
     }
   }
@@ -691,7 +691,7 @@ __device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, in
 
 // One workgroup of NT threads per row of at most 8 NT R values.  R stays at most 4: with
 // 8 chunks per lane the compiler keeps the row in scratch memory instead of registers.
-template <typename T, int LV, int R, int NT>
+template <typename T, int LV, int R, int NT, bool kGen12>
 __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
   extern __shared__ float act_row_lds[];
   const int tid = threadIdx.x;
@@ -749,16 +749,11 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
   // one cast back after the rotation, the clamp (bounds in T, NaN kept), the companding
   // product
   const float lo = Io<T>::round(a.act_min), hi = Io<T>::round(a.act_max);
-  float cs[R][8];  // the companding scale of the lane's values (1 without companding)
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int c0 = 8 * (tid + NT * r);
-    if (a.compand && c0 < a.cols) {
-      Io<float>::load8(a.compand + c0, cs[r]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) cs[r][i] = 1.0f;
-    }
+    float cs[8];
+    if (a.compand && c0 < a.cols) Io<float>::load8(a.compand + c0, cs);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float t = v[r][i];
@@ -767,12 +762,13 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
         if (a.has_min) t = fmaxf(t, lo);
         if (a.has_max) t = fminf(t, hi);
       }
-      if (a.compand) t = Io<T>::round(t * cs[r][i]);
+      if (a.compand && c0 < a.cols) t = Io<T>::round(t * cs[i]);
       v[r][i] = t;
     }
   }
   if (a.n) {
-    if (a.gen12) generalized_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div.d, tid);
+    // the generalized form is its own instance: its 12-point mix costs registers
+    if constexpr (kGen12) generalized_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div.d, tid);
     else fwht_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div, tid);
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -787,8 +783,10 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
     if (a.quant) qdq8<LV>(v[r]);
     if (c0 < a.cols) {
       if (a.compand) {
+        float cs[8];
+        Io<float>::load8(a.compand + c0, cs);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(Io<T>::round(v[r][i]) / cs[r][i]);
+        for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(Io<T>::round(v[r][i]) / cs[i]);
       }
       Io<T>::store8(y + c0, v[r]);
     }
