@@ -10,6 +10,12 @@
 //                          src/faquant/wan22_attention.py:186-192, 219-221)
 //   operand_prep_vt_kernel V QDQ written transposed ([d][key], keys padded with zeros to
 //                          a multiple of 128) for the attention kernel's PV operand.
+//   act_qdq_rows_kernel    the quantized Linear's input prologue: input scale, block
+//                          Hadamard up to 512, HiF4 QDQ (reference: quantization.py:199-276)
+//   act_row_kernel         the whole Linear activation path, one workgroup per row: HiSQ
+//                          rotation, clamp, companding, block or generalized Hadamard, QDQ
+//                          (reference: quantization.py:199-276, hisq_rotation.py:50-71,
+//                          rotation.py:53-69, 117-135)
 //
 // Layout: one lane owns 8 consecutive values of a row (one 16-byte bf16 vector); a
 // 64-value HiF4 group spans 8 adjacent lanes and its maxima reduce with xor shuffles
