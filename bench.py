@@ -373,10 +373,10 @@ QWEN8B_LINEAR_INPUTS = (("q/k/v/o_proj, gate/up_proj", 4096), ("down_proj", 1228
 
 def linear_prep_bench(tokens: int, steps: int, warmup: int) -> dict:
     """The quantized Linear's activation path over `tokens` bf16 rows at the Qwen3-8B input
-    widths: the fused prologue without extras (act_qdq_rows: HiF4 QDQ only) and the full path
-    with the HiSQ rotation (signs, permutation, block Hadamard of 1024), clamp and companding
-    (act_prep_rows), each against the 8 TB/s HBM peak on the activation bytes it must move
-    (read and write once)."""
+    widths: the fused prologue without extras (act_qdq_rows: HiF4 QDQ only), the full path
+    with the HiSQ rotation (signs, permutation, block Hadamard of 1024), clamp and companding,
+    and the generalized online Hadamard of the whole row (act_prep_rows), each against the
+    8 TB/s HBM peak on the activation bytes it must move (read and write once)."""
     import torch
 
     from faquant_amd import _ops
@@ -412,6 +412,8 @@ def linear_prep_bench(tokens: int, steps: int, warmup: int) -> dict:
             ("hisq_clamp_compand", lambda: _ops.act_prep_rows(x, levels="123", rot_signs=signs, rot_perm=perm,
                                                               rot_block=1024, act_min=-8.0, act_max=8.0,
                                                               compand=comp, out=y)),
+            # the online Hadamard without a block size: the whole row (12 x 1024 at 12288)
+            ("online_generalized", lambda: _ops.act_prep_rows(x, levels="123", hadamard_generalized=True, out=y)),
         ):
             ms = timed(fn)
             entry[label] = {"us": round(ms * 1e3, 1),
