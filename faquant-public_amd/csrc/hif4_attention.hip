@@ -640,6 +640,13 @@ void attn_fwd_kernel(AttnArgs a) {
       // stage the DMA of the next step overwrites
       wait_all_memory();
       __syncthreads();
+      // The two waves of a SIMD leave the barrier together, and with equal priorities the
+      // older one wins every issue conflict: it finishes its P chunks far ahead and then waits
+      // at the next barrier while the younger one runs alone at the single-wave issue rate.
+      // Priorities that fall as a wave advances through the tile (3 for QK, the maximum and
+      // chunks 0-1, down to 0 for chunks 6-7) let the wave that is behind win instead, so the
+      // two converge and reach the barrier together.
+      __builtin_amdgcn_s_setprio(3);
       if (t + 1 < g.t_hi) {
         load_tile(b, g.kvh, t + 1, (step + 1) & 1);
       } else if (next_item < n_items && ng.t_lo < ng.t_hi) {
@@ -778,6 +785,10 @@ void attn_fwd_kernel(AttnArgs a) {
         bf16x8 pprev, plprev;
 #pragma unroll
         for (int c = 0; c <= 8; ++c) {
+          if (c < 2) __builtin_amdgcn_s_setprio(3);
+          else if (c < 4) __builtin_amdgcn_s_setprio(2);
+          else if (c < 6) __builtin_amdgcn_s_setprio(1);
+          else __builtin_amdgcn_s_setprio(0);
           bf16x8 va[4];
           if (c >= 1) {
 #pragma unroll
