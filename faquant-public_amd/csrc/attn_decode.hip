@@ -581,7 +581,7 @@ void dec_values_kernel(DecodeArgs a) {
       l_run *= alpha;
     }
     PQuant pq;
-    if (kQuantP) pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
+    if (kQuantP) pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(p_arg<!(kQuantP && kSame)>(mx, a.c1, nm)));
     float rowsum = 0.0f;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
@@ -602,7 +602,7 @@ void dec_values_kernel(DecodeArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float sj = w.live ? __uint_as_float(sv[slot][j >> 2][j & 3]) : -INFINITY;
-        pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sj, a.c1, nm));
+        pc[j] = __builtin_amdgcn_exp2f(p_arg<!(kQuantP && kSame)>(sj, a.c1, nm));
       }
       // the S slot takes chunk c + 4 (of this tile or the next)
       load_s(c < 4 ? t : tn, (c + 4) & 7, slot);
@@ -770,10 +770,10 @@ void dec_values_compact_kernel(DecodeArgs a) {
       const int col = cr + 4 * u;
       const float nmc = __shfl(nm, col, 64);
       const float gx = __shfl(g.x, col, 64), gy = __shfl(g.y, col, 64);
-      const PQuant pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(ch ? gy : gx, a.c1, nmc)));
+      const PQuant pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(p_arg<false>(ch ? gy : gx, a.c1, nmc)));
       float pc[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sx[u][j], a.c1, nmc));
+      for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(p_arg<false>(sx[u][j], a.c1, nmc));
       pquant8<LV>(pc, pq);
       *reinterpret_cast<bf16x8*>(pslots + (lane + 64 * u) * 16) = pack8<true>(pc);
     }
@@ -1132,10 +1132,10 @@ void dec_fused_kernel(DecodeArgs a, uint32_t epoch, int spin_limit) {
     const int col = cr + 4 * u;
     const float nmc = __shfl(nm, col, 64);
     const float gx = __shfl(g.x, col, 64), gy = __shfl(g.y, col, 64);
-    const PQuant pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(ch ? gy : gx, a.c1, nmc)));
+    const PQuant pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(p_arg<false>(ch ? gy : gx, a.c1, nmc)));
     float pc[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sx[u][j], a.c1, nmc));
+    for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(p_arg<false>(sx[u][j], a.c1, nmc));
     pquant8<LV>(pc, pq);
     *reinterpret_cast<bf16x8*>(pslots + (lane + 64 * u) * 16) = pack8<true>(pc);
   }

@@ -212,6 +212,20 @@ __device__ __forceinline__ bf16x8 pack8(const float* v) {
   return r;
 }
 
+// Exponent argument of P = exp2(s c1 - m), m = the running maximum of RN(s c1) (log2 units).
+// kExact: RN(RN(s c1) - m), the reference's order (scores scaled, then the maximum
+// subtracted: sfa:727, 797), which gives the row-maximum key exactly 0 and P = 1.  Otherwise
+// one fma, s c1 - m rounded once: the row-maximum key then gets the product's rounding
+// residual r = mx c1 - RN(mx c1), |r| <= ulp(m) / 2, and P = 2^r (exactly 1 for |m| < 1,
+// within 2^-24 |m| ln 2 of 1 otherwise).  The quantized_same form takes the fma: there the
+// normalizer sums the same P^ as the numerator, so a single key's output is V^ whatever P
+// is, and a P^ code changes only if that key lies on a rounding boundary; the second
+// instruction per score would cost about 5% of the kernel.
+template <bool kExact>
+__device__ __forceinline__ float p_arg(float s, float c1, float nm) {
+  return kExact ? (s * c1) + nm : __builtin_fmaf(s, c1, nm);
+}
+
 __device__ __forceinline__ float floor2(float x) { return __uint_as_float(__float_as_uint(x) & 0xFF800000u); }
 
 // max of two non-negative floats as an integer max of their bit patterns
@@ -427,6 +441,7 @@ void attn_fwd_kernel(AttnArgs a) {
   constexpr bool kDense = kMask == 3 || kMask == 4;
   constexpr bool kSoftcap = kMask == 2 || kMask == 4;
   constexpr bool kRanges = kMask == 1 || kMask == 2;
+  constexpr bool kExactArg = !(kQuantP && kSame);  // see p_arg
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
 
   const int tid = threadIdx.x;
@@ -625,10 +640,12 @@ void attn_fwd_kernel(AttnArgs a) {
     // tiles before its split (sfa:788-806: P of tile t depends on the maximum after tile t)
     float m_run = (a.m_start && row_live) ? a.m_start[static_cast<int64_t>(split) * a.rows_total + row] : -INFINITY;
     float l_run = 0.0f;
-    // probe (kDiag): the other normalizer source (sum of P when l sums P^, and the reverse),
-    // rescaled like l, and per-element sums over this lane's keys: #(P^ = 0 < P),
-    // sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869)
-    float sh_run = 0.0f, dg_zero = 0.0f, dg_err = 0.0f, dg_ref = 0.0f;
+    // probe (kDiag): sum P^ and sum P, rescaled like l, and per-element sums over this
+    // lane's keys: #(P^ = 0 < P), sum (P^ - P)^2, sum P^2 (sfa:36-185, 835-869).  They are
+    // taken on the P of the exact exponent argument (p_arg<true>) in both normalizer modes,
+    // so the summary does not depend on the mode, as the reference's P does not; the output
+    // path keeps the mode's own form, so the outputs equal the plain kernel's.
+    float dq_run = 0.0f, dp_run = 0.0f, dg_zero = 0.0f, dg_err = 0.0f, dg_ref = 0.0f;
 
     // next item of this workgroup (its first tile is fetched during this item's last one)
     const int next_item = item_of(k_round + 1);
@@ -769,16 +786,23 @@ void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mb][i] *= alpha;
           l_run *= alpha;
-          if (kDiag) sh_run *= alpha;
+          if (kDiag) {
+            dq_run *= alpha;
+            dp_run *= alpha;
+          }
         }
         // ---- P, its HiF4 QDQ and the row sum, one 8-key chunk at a time; chunk c of this lane
         // is keys 64 half + 8c .. 8c+7, the B operand of PV k-chunk c.
         PQuant pq;
         if (kQuantP) {
           // group maximum = P of the lane's largest score (same fma and exp2)
-          pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(__builtin_fmaf(mx, a.c1, nm)));
+          pq = pquant_setup<LV>(__builtin_amdgcn_exp2f(p_arg<kExactArg>(mx, a.c1, nm)));
         }
-        float rowsum = 0.0f, shadow = 0.0f;
+        // the probe's quantizer on the exact-argument P (the same as pq when the output path
+        // takes that argument)
+        PQuant pqx{};
+        if (kDiag) pqx = kExactArg ? pq : pquant_setup<LV>(__builtin_amdgcn_exp2f(p_arg<true>(mx, a.c1, nm)));
+        float rowsum = 0.0f, dq_sum = 0.0f, dp_sum = 0.0f;
         // Software pipeline over the eight 8-key chunks: iteration c computes chunk c's P^
         // (VALU) while the MFMAs of chunk c - 1 issue one at a time between those VALU
         // instructions.
@@ -798,7 +822,7 @@ void attn_fwd_kernel(AttnArgs a) {
           if (c < 8) {
             float pc[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
+            for (int j = 0; j < 8; ++j) pc[j] = __builtin_amdgcn_exp2f(p_arg<kExactArg>(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
             if (!(kQuantP && kSame)) {
               // the normalizer sums P (unquantized mode, or no P quantization)
 #pragma unroll
@@ -808,31 +832,37 @@ void attn_fwd_kernel(AttnArgs a) {
               float pu[8];
               if (kDiag) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                  pu[j] = pc[j];
-                  if (kSame) shadow += pc[j];
-                }
+                for (int j = 0; j < 8; ++j) pu[j] = pc[j];
               }
               pquant8<LV>(pc, pq);
               pcur = pack8<true>(pc);
-              if (kSame || kDiag) {
+              if (kSame) {
                 uint32_t wv[4];
                 __builtin_memcpy(wv, &pcur, 16);
-                float& qsum = kSame ? rowsum : shadow;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                   bf16x2_t pr;
                   __builtin_memcpy(&pr, &wv[i], 4);
-                  qsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, qsum, false);
+                  rowsum = __builtin_amdgcn_fdot2_f32_bf16(pr, ones2, rowsum, false);
                 }
               }
               if (kDiag) {
+                // P and P^ of the exact exponent argument
+                float pe[8], qe[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                  const float d = pc[j] - pu[j];
+                  pe[j] = kExactArg ? pu[j] : __builtin_amdgcn_exp2f(p_arg<true>(s[c >> 1][8 * (c & 1) + j], a.c1, nm));
+                  qe[j] = kExactArg ? pc[j] : pe[j];
+                }
+                if (!kExactArg) pquant8<LV>(qe, pqx);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                  const float d = qe[j] - pe[j];
+                  dq_sum += qe[j];
+                  dp_sum += pe[j];
                   dg_err = __builtin_fmaf(d, d, dg_err);
-                  dg_ref = __builtin_fmaf(pu[j], pu[j], dg_ref);
-                  dg_zero += (pc[j] == 0.0f && pu[j] > 0.0f) ? 1.0f : 0.0f;
+                  dg_ref = __builtin_fmaf(pe[j], pe[j], dg_ref);
+                  dg_zero += (qe[j] == 0.0f && pe[j] > 0.0f) ? 1.0f : 0.0f;
                 }
                 if (a.p_dump && row_live) {
                   // this chunk's keys key0 + 64 half + 8c .. + 7 (within the padded row)
@@ -882,7 +912,10 @@ void attn_fwd_kernel(AttnArgs a) {
           plprev = plcur;
         }
         l_run += halves_sum(rowsum);
-        if (kDiag) sh_run += halves_sum(shadow);
+        if (kDiag) {
+          dq_run += halves_sum(dq_sum);
+          dp_run += halves_sum(dp_sum);
+        }
       } while (false);
     }
 
@@ -918,8 +951,8 @@ void attn_fwd_kernel(AttnArgs a) {
         const float zero = halves_sum(dg_zero), err = halves_sum(dg_err), ref = halves_sum(dg_ref);
         if (half == 0 && a.diag) {
           float* dg = a.diag + row * 5;
-          dg[0] = kSame ? l : sh_run;
-          dg[1] = kSame ? sh_run : l;
+          dg[0] = dq_run;
+          dg[1] = dp_run;
           dg[2] = zero;
           dg[3] = err;
           dg[4] = ref;

@@ -1,14 +1,22 @@
 """GPU parity of the HiF4 QK/PV attention kernel against the oracle and the reference goldens.
 
-Tolerance (fp32 math): the kernel's P-hat codes equal the reference quantizer's on the
+Tolerances (fp32 math).  The kernel's P-hat codes equal the reference quantizer's on the
 kernel's own P bit for bit (tests/test_gpu_pquant.py), but that P comes from a hardware
 exp2 on log2-scaled scores summed in MFMA order, the oracle's from numpy exp on BLAS-order
-sums, so P differs by a few ulp and a few P codes flip where P lies on a rounding boundary
-(the flip rate is measured in test_gpu_pquant.py).  The bar is a relative Frobenius error
-<= 1e-3 and a max abs error <= 1e-2 of the output's max magnitude (the reference measured
-its own Triton kernel at 4-7e-4 relative error against its simulator,
-docs/WAN22.md:172-175).  Identities (constant V under P-Reordering, fused == unfused
-prologue) are checked to a few ulps or bitwise.
+sums, so P differs by a few ulp, and where a P lies on a code boundary its code flips: one
+flip moves an output row by one HiF4 step of one key's weight.  Each test therefore carries
+its own bar, about ten times the error it reaches (measured on MI355X, the figure beside
+each constant):
+- TIGHT: paths with no code flips in the tested rows (the shape cases, levels, config 1,
+  flags off, decode, chunked prefill): relative Frobenius 1e-5, max 1e-4 of the output's
+  largest magnitude (reached: 2e-7 / 2e-6);
+- FLIPS: inputs drawn with large scores (x2-x3 queries, masks, softcaps, mixed levels,
+  random configurations, goldens), where flips are seen: 1e-3 / 1e-2 (reached: 1.4e-4 /
+  5e-3 in the unquantized-normalizer random cases; the reference measured its own Triton
+  kernel at 4-7e-4 relative error against its simulator, docs/WAN22.md:172-175).
+The full-size bars are per configuration (tests/test_gpu_full_size.py).  Identities
+(constant V under P-Reordering, fused == unfused prologue) are checked to a few ulps or
+bitwise, and rows that see a single key bitwise (tests/test_gpu_single_key.py).
 """
 
 from __future__ import annotations
@@ -27,15 +35,17 @@ from tests.golden.cases import CASES, build_inputs, golden_output
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-FRO_TOL = 1e-3
+FRO_TOL = 1e-3  # the FLIPS bar (module docstring)
 MAX_TOL = 1e-2
+TIGHT = dict(fro_tol=1e-5, max_tol=1e-4)
 
 
 def to_dev(a, dev, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev).to(dtype)
 
 
-def assert_close_attention(got: np.ndarray, ref: np.ndarray, what: str = ""):
+def assert_close_attention(got: np.ndarray, ref: np.ndarray, what: str = "", *, fro_tol: float = FRO_TOL,
+                           max_tol: float = MAX_TOL):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape
@@ -44,8 +54,8 @@ def assert_close_attention(got: np.ndarray, ref: np.ndarray, what: str = ""):
     fro = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
     mx = np.abs(got - ref).max() / scale
     print(f"[parity] {what} fro_rel={fro:.3e} max_rel={mx:.3e}", flush=True)
-    assert fro <= FRO_TOL, (what, fro)
-    assert mx <= MAX_TOL, (what, mx)
+    assert fro <= fro_tol, (what, fro, fro_tol)
+    assert mx <= max_tol, (what, mx, max_tol)
 
 
 def module(*, qk=True, pv=True, mode="quantized_same", causal=True, query_chunk=256, key_chunk=128):
@@ -149,7 +159,7 @@ def test_kernel_matches_oracle_fp32_out(dev, shape, mode):
     v = OQ.bf16_round(g.standard_normal((B, Hkv, Lk, 128), dtype=np.float32))
     got = _kernel(dev, q, k, v, causal=causal, mode=mode)
     ref = _oracle(q, k, v, causal=causal, mode=mode)
-    assert_close_attention(got, ref, f"{shape} {mode}")
+    assert_close_attention(got, ref, f"{shape} {mode}", **TIGHT)
     if causal and Lq > Lk:
         assert np.count_nonzero(got[:, : Lq - Lk]) == 0
 
@@ -157,7 +167,8 @@ def test_kernel_matches_oracle_fp32_out(dev, shape, mode):
 @pytest.mark.parametrize("levels", ["12", "13"])
 def test_p_levels_variants(dev, levels):
     q, k, v = OI.qwen(5, 4, 1, 256, student_t_keys=True)
-    assert_close_attention(_kernel(dev, q, k, v, levels=levels), _oracle(q, k, v, levels=levels), f"levels {levels}")
+    assert_close_attention(_kernel(dev, q, k, v, levels=levels), _oracle(q, k, v, levels=levels), f"levels {levels}",
+                           **TIGHT)
 
 
 @pytest.mark.parametrize("qk,pv", [(True, False), (False, True), (False, False)])
@@ -165,7 +176,7 @@ def test_quantization_flags(dev, qk, pv):
     q, k, v = OI.qwen(6, 4, 1, 256)
     mode = "unquantized"
     assert_close_attention(_kernel(dev, q, k, v, qk=qk, pv=pv, mode=mode),
-                           _oracle(q, k, v, qk=qk, pv=pv, mode=mode), f"qk={qk} pv={pv}")
+                           _oracle(q, k, v, qk=qk, pv=pv, mode=mode), f"qk={qk} pv={pv}", **TIGHT)
 
 
 def test_constant_values_are_reproduced_under_p_reordering(dev):
@@ -207,7 +218,7 @@ def test_config1_full(dev):
     for mode in ("quantized_same", "unquantized"):
         out, _ = simulated_flash_attention_forward(module(mode=mode), to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), None)
         assert out.dtype == torch.float32
-        assert_close_attention(out.cpu().numpy(), _oracle(q, k, v, mode=mode), f"config1 {mode}")
+        assert_close_attention(out.cpu().numpy(), _oracle(q, k, v, mode=mode), f"config1 {mode}", **TIGHT)
 
 
 def test_wan_hif4_attention_drop_in(dev):

@@ -15,7 +15,7 @@ import pytest
 
 from oracle import hif4 as OQ
 from oracle import inputs as OI
-from tests.test_gpu_attention import _oracle, assert_close_attention, module, to_dev
+from tests.test_gpu_attention import TIGHT, _oracle, assert_close_attention, module, to_dev
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -79,7 +79,7 @@ def test_decode_steps_equal_prefill_rows_and_match_oracle(dev):
     q, k, v = _qkv(34, 8, 2, 1000, 1000)
     qt, kt, vt = (to_dev(a, dev, torch.float32) for a in (q, k, v))
     full, _ = simulated_flash_attention_forward(module(), qt, kt, vt, None)
-    assert_close_attention(full.float().cpu().numpy(), _oracle(q, k, v), "prefill 1000 keys")
+    assert_close_attention(full.float().cpu().numpy(), _oracle(q, k, v), "prefill 1000 keys", **TIGHT)
     mod = module()
     simulated_flash_attention_forward(mod, qt[:, :, :997], kt[:, :, :997], vt[:, :, :997], None)
     for length in (998, 999, 1000):
@@ -186,4 +186,5 @@ def test_split_key_path_equals_one_pass(dev, case):
     # l is a sum over up to ~10^5 keys (fp32 P in unquantized mode) taken in another order
     np.testing.assert_allclose(dens[1], dens[0], rtol=3e-6)
     ref = _oracle(q, k, v, causal=causal, levels=lv, mode=mode, qk=True, pv=qp)
-    assert_close_attention(outs[1], ref, f"split {case}")
+    # the split path's row blocks see random keys x3: codes flip (reached 1.4e-5 / 1.3e-4)
+    assert_close_attention(outs[1], ref, f"split {case}", fro_tol=2e-4, max_tol=2e-3)

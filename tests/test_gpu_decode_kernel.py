@@ -22,7 +22,7 @@ import pytest
 
 from oracle import hif4 as OQ
 from oracle import inputs as OI
-from tests.test_gpu_attention import _oracle, assert_close_attention, module, to_dev
+from tests.test_gpu_attention import TIGHT, _oracle, assert_close_attention, module, to_dev
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -154,7 +154,7 @@ def test_decode_equals_split_path_bitwise(dev, case):
         assert torch.equal(pk_l, dec_l)
     if case[4] == 5000 or Lq > 1:
         ref = _oracle(q, k, v, causal=causal, levels=lv, mode=mode, qk=True, pv=qp)
-        assert_close_attention(dec_o.cpu().numpy(), ref, f"decode {case}")
+        assert_close_attention(dec_o.cpu().numpy(), ref, f"decode {case}", **TIGHT)
 
 
 FUSED_CASES = [
@@ -254,7 +254,7 @@ def test_drop_in_runs_decode_steps_on_the_decode_kernel(dev):
     _ops.attention_decode(qh, 5000, k=kh, v=vh, split=n, out=out.transpose(1, 2), **kw)
     assert torch.equal(got, out)
     ref = _oracle(q, k, v, causal=True, levels="123", dtype="bfloat16")
-    assert_close_attention(got.float().cpu().numpy(), ref, "drop-in decode step")
+    assert_close_attention(got.float().cpu().numpy(), ref, "drop-in decode step", **TIGHT)
 
 
 @pytest.mark.parametrize("core", [False, True], ids=["sdpa", "qwen_core"])
@@ -298,4 +298,4 @@ def test_packed_cache_decode_steps_match_bf16_cache(dev, core):
     assert np.array_equal(_packed_values(kc), kb)
     if not core:
         ref = _oracle(q[:, :, -1:], k, v, causal=True, levels="123", dtype="bfloat16")  # bf16 output
-        assert_close_attention(a.float().cpu().numpy(), ref, "packed decode step")
+        assert_close_attention(a.float().cpu().numpy(), ref, "packed decode step", **TIGHT)

@@ -2,8 +2,10 @@
 
 The reference quantizes the attention output after its cast to the query dtype, along
 the hidden axis Hq * 128 in groups of 64 (each group is half of one head's row).  The
-fused epilogue must equal that composition bitwise: attention, cast, then the row
-quantizer (itself pinned bit-exact against the reference's codec goldens).
+fused epilogue must equal that composition bitwise: the kernel's own plain output (cast to
+the output dtype), then the oracle's fake_quantize_hif4 (the reference's hif4.py:377-390,
+pinned by its known-answer vector and goldens) over [B, L, Hq * 128], and also the HIP row
+quantizer on the same values.
 """
 
 from __future__ import annotations
@@ -45,9 +47,14 @@ def test_fused_output_qdq_equals_attention_then_row_quantizer(dev, out_dtype, le
     _ops.attention_fwd(qh, kh, vt, lk, out=plain.transpose(1, 2), **kw)
     fused = torch.empty_like(plain)
     _ops.attention_fwd(qh, kh, vt, lk, out=fused.transpose(1, 2), out_levels=levels, **kw)
-    expected = _ops.qdq_rows(plain.reshape(1, lq, hq * 128), levels).view(plain.shape)
+    rows = plain.reshape(1, lq, hq * 128)
+    dt = "bfloat16" if out_dtype == torch.bfloat16 else "float32"
+    oracle = OQ.fake_quantize_hif4(rows.float().cpu().numpy(), levels, dtype=dt).reshape(plain.shape)
     print(f"[epilogue] {shape} {levels} {out_dtype}", flush=True)
-    assert torch.equal(fused, expected)
+    got = fused.float().cpu().numpy()
+    assert np.array_equal(got, oracle)
+    # and the HIP row quantizer on the same values
+    assert torch.equal(fused, _ops.qdq_rows(rows, levels).view(plain.shape))
     assert not torch.equal(fused, plain)
 
 

@@ -36,6 +36,18 @@ CASES = {
     "wan720p": (((-32, 0), (37888, 37920), (0, 32)), (0, 17, -1)),
 }
 
+# Per-configuration bars, about ten times the error reached on MI355X (relative Frobenius /
+# max of the largest magnitude; reached in brackets).  Wan 720p scales heads by up to 4, so
+# its scores are large and a P-hat code flip (P from exp2 vs numpy exp, a few ulp apart)
+# shows in the sampled rows; the other configurations have no flip in them.
+TOLERANCE = {
+    "qwen8b_8k": (1e-5, 1e-5),    # [1.3e-7 / 2.9e-7]
+    "qwen8b_32k": (1e-5, 1e-5),   # [1.4e-7 / 2.5e-7]
+    "qwen32b_16k": (1e-5, 3e-5),  # [7.7e-7 / 2.5e-6]
+    "wan480p": (1e-5, 1e-5),      # [1.5e-7 / 2.4e-7]
+    "wan720p": (5e-4, 2e-3),      # [5.2e-5 / 1.9e-4]
+}
+
 
 @pytest.mark.parametrize("name", list(CASES))
 def test_full_size_sampled_rows_match_oracle(dev, name):
@@ -75,5 +87,6 @@ def test_full_size_sampled_rows_match_oracle(dev, name):
             qs = rot(q[:, h : h + 1, p0:p1].float().cpu().numpy())
             ref = OA.simulated_flash_attention(qs, kr[:, :, :kend], vr[:, :, :kend], mconf)
             got = out[:, p0:p1, h : h + 1].cpu().numpy()
-            assert_close_attention(got, ref, f"{name} rows {p0}:{p1} head {h}")
+            fro_tol, max_tol = TOLERANCE[name]
+            assert_close_attention(got, ref, f"{name} rows {p0}:{p1} head {h}", fro_tol=fro_tol, max_tol=max_tol)
     print(f"[full] {name} checked in {time.time() - t0:.1f}s", flush=True)

@@ -442,3 +442,31 @@ def test_attention_wrappers_check_output_extent(dev):
                            row_den=torch.empty((1, 4, 4), device=dev), **kw)
     with pytest.raises(ValueError, match="attention output must be"):
         _ops.attention_decode(q[:, :, :1], 256, k=k, v=k, out=torch.empty((1, 4, 2, 128), device=dev), **kw)
+
+
+def test_companding_scale_is_within_one_ulp_of_the_exact_exponential(dev):
+    """The companding scale (quantization.py:228-234) is torch's exp of the clamped log
+    scale on the buffer's device, then cast to the activation dtype, as in the reference,
+    which also takes exp wherever its buffer lives: its last bit is the device's exp.  Pin it
+    to exp itself: for fp32 activations within one fp32 ulp of the correctly rounded
+    exponential (float64 exp rounded once), and for bf16 activations within one bf16 ulp of it
+    (bitwise away from bf16 rounding ties)."""
+    from faquant_amd.quantization import FakeQuantLinear
+
+    g = OI.rng(61)
+    n = 4096
+    log_scale = g.uniform(-2.5, 2.5, n).astype(np.float32)
+    exact = np.exp(np.clip(log_scale, np.float32(-2.079), np.float32(2.079)).astype(np.float64))
+    lin = torch.nn.Linear(n, 64, bias=False).to(dev, torch.bfloat16)
+    mod = FakeQuantLinear(lin, quant_format="hif4", bits=4, weight_group_size=64, activation_group_size=64,
+                          symmetric=True, clip_ratio=1.0, activation_compand_log_scale=to_dev(log_scale, dev))
+    for dtype, round_exact in ((torch.float32, lambda a: a.astype(np.float32)),
+                               (torch.bfloat16, lambda a: OQ.bf16_round(a.astype(np.float32)))):
+        _, compand, _ = mod._prep_vectors(torch.zeros(1, n, device=dev, dtype=dtype))
+        got = compand.cpu().numpy()
+        want = round_exact(exact)
+        step = np.spacing(want) if dtype == torch.float32 else np.spacing(want) * 65536.0
+        off = np.abs(got.astype(np.float64) - want.astype(np.float64)) / step
+        print(f"[compand] {dtype}: {int((off > 0).sum())} of {n} differ from the exact value, max {off.max():.2f} ulp",
+              flush=True)
+        assert off.max() <= 1.0

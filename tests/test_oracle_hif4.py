@@ -180,3 +180,31 @@ def test_dispatcher_errors():
         hif4.fake_quantize(x, quant_format="hif4", group_size=64, symmetric=False)
     with pytest.raises(ValueError, match="clipping"):
         hif4.fake_quantize(x, quant_format="hif4", group_size=64, clip_ratio=0.9)
+
+
+def test_int_format_known_answers():
+    """Closed-form values of the int branch (quantization.py:74-94): scales that are powers
+    of two keep every step exact, so the expected outputs follow from the rule alone --
+    round half to even (torch.round), the signed range [-2^(b-1), 2^(b-1) - 1], the clip
+    ratio applied to the maximum before the scale, the asymmetric zero point and range, the
+    eps floor of the scale, and bits >= 16 as the identity."""
+    q = lambda x, **kw: hif4.fake_quantize(np.array([x], np.float32), **kw)[0]  # noqa: E731
+    # symmetric int4, max 7: scale 1, ties to even, -7 in range
+    np.testing.assert_array_equal(q([0.5, 1.5, 2.5, -7.0], bits=4, group_size=4), [0.0, 2.0, 2.0, -7.0])
+    # clip ratio 0.5 of max 14: scale 1, 14 clamps to 7 and -10 to -8 (qmin = -8)
+    np.testing.assert_array_equal(q([14.0, -10.0, 1.5, 0.25], bits=4, group_size=4, clip_ratio=0.5),
+                                  [7.0, -8.0, 2.0, 0.0])
+    # symmetric int8 with max 127 * 2^-3: scale 2^-3
+    np.testing.assert_array_equal(q([127 / 8, -1.0, 0.0625, 0.1875], bits=8, group_size=4),
+                                  [127 / 8, -1.0, 0.0, 0.25])
+    # asymmetric int2 over [-1, 2]: scale 1, zero point 1, codes 0..3
+    np.testing.assert_array_equal(q([-1.0, 0.0, 1.0, 2.0], bits=2, group_size=4, symmetric=False), [-1.0, 0.0, 1.0, 2.0])
+    # asymmetric int2, all non-negative (the range is widened to include 0): scale 1, zero 0
+    np.testing.assert_array_equal(q([3.0, 0.5, 1.5, 3.0], bits=2, group_size=4, symmetric=False), [3.0, 0.0, 2.0, 3.0])
+    # an all-zero group: the scale floors at fp32 eps and the group stays zero
+    np.testing.assert_array_equal(q([0.0, 0.0, 0.0, 0.0], bits=4, group_size=4), [0.0, 0.0, 0.0, 0.0])
+    # groups are independent; group_size -1 is the whole row
+    np.testing.assert_array_equal(q([7.0, 1.0, 0.5, 3.5], bits=4, group_size=2), [7.0, 1.0, 0.5, 3.5])
+    np.testing.assert_array_equal(q([7.0, 1.0, 0.5, 3.5], bits=4, group_size=-1), [7.0, 1.0, 0.0, 4.0])
+    # bits >= 16: unchanged
+    np.testing.assert_array_equal(q([0.1, -0.3, 7.7, 1e-9], bits=16, group_size=4), np.float32([0.1, -0.3, 7.7, 1e-9]))
