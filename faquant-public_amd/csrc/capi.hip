@@ -900,7 +900,14 @@ int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t 
   // FAQ_DECODE_SPIN sets the look-back's wait bound (negative: every earlier split's
   // maxima computed in the wave)
   const char* fused_env = std::getenv("FAQ_DECODE_FUSED");
-  const bool fits = faq::decode_fused_fits(a, quant_p, norm_same);
+  // The one pass tells its published maxima from an earlier call's by an epoch passed at
+  // launch.  A launch recorded into a HIP graph keeps its epoch on every replay, so a replay
+  // could accept the maxima a previous replay left; calls on a capturing stream (or where
+  // the capture state cannot be read) take the two passes, which carry no state between
+  // calls.
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  const bool capturing = hipStreamIsCapturing(st, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone;
+  const bool fits = faq::decode_fused_fits(a, quant_p, norm_same) && !capturing;
   if (fused_env && std::strcmp(fused_env, "force") == 0 && !fits)
     return fail(FAQ_EUNSUP, "%s: the one-pass decode does not apply to this call", who);
   if (!(fused_env && fused_env[0] == '0') && fits) {

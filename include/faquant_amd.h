@@ -384,7 +384,11 @@ int faq_operand_prep_hif4_kv(const void* x, int in_dtype, int64_t sb, int64_t sh
  * kernel instead (the same bits): each range publishes its maxima, stamped with a per-call
  * epoch, to a file-scope array of the library and reads the earlier ranges' maxima from
  * it, waiting a bounded time and otherwise computing them from K itself, so calls that
- * overlap on one GPU stay correct.  `workspace` is device memory of at least
+ * overlap on one GPU stay correct; they share the array, though, and a range whose
+ * predecessors' maxima another call overwrote waits out the whole bound (4096 rounds)
+ * before computing them, so overlapping decode calls can run much slower.  A call on a
+ * stream that is capturing a HIP graph runs the two passes: a recorded launch would keep
+ * its epoch on every replay.  `workspace` is device memory of at least
  * faq_attention_decode_workspace(B, Hq, Lq, Lk, nsplit) bytes, 16-byte aligned; nsplit is
  * 1..4096.  Replaces, for the decode steps of a KV cache
  * (src/faquant/simulated_flash_attention.py:243-289), the attention of

@@ -193,12 +193,57 @@ def test_one_pass_decode_equals_two_passes_bitwise(dev, case, monkeypatch):
         for path in ("one_pass", "fallback"):
             assert torch.equal(runs[path][0], runs["two_pass"][0]), (name, path)
             assert torch.equal(runs[path][1], runs["two_pass"][1]), (name, path)
-    # and repeated calls (new epochs over the same maxima slots) keep the bits
-    monkeypatch.setenv("FAQ_DECODE_FUSED", "force")
+    # and a call right after another one over the same maxima slots (a new epoch) ignores the
+    # maxima the first left: keys scaled by 2 (HiF4 values stay exact) change every split
+    # maximum, and the second call must still equal its own two-pass result
     monkeypatch.delenv("FAQ_DECODE_SPIN", raising=False)
-    again = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, v=vh, split=nsplit, **kw, **a), case, dev)
-    first = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, v=vh, split=nsplit, **kw, **a), case, dev)
-    assert torch.equal(again[0], first[0]) and torch.equal(again[1], first[1])
+    kh2 = kh * 2
+    monkeypatch.setenv("FAQ_DECODE_FUSED", "0")
+    want = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh2, v=vh, split=nsplit, **kw, **a), case, dev)
+    monkeypatch.setenv("FAQ_DECODE_FUSED", "force")
+    _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh, v=vh, split=nsplit, **kw, **a), case, dev)
+    second = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kh2, v=vh, split=nsplit, **kw, **a), case, dev)
+    assert not torch.equal(second[1], runs["two_pass"][1])  # the maxima did change
+    assert torch.equal(second[0], want[0]) and torch.equal(second[1], want[1])
+
+
+def test_decode_captured_in_a_graph_replays_with_new_keys(dev, monkeypatch):
+    """A decode step recorded into a HIP graph (torch.cuda.graph) and replayed over new K
+    contents gives each replay's two-pass result bitwise: on a capturing stream the entry
+    takes the two passes, which keep no state between calls (a recorded one-pass launch would
+    keep its epoch and could accept an earlier replay's published maxima).  Each replay is
+    followed by eager work and a synchronization before it is checked."""
+    from faquant_amd import _ops
+
+    case = (1, 32, 8, 1, 5000, True, "quantized_same", True, "123", 40)  # a one-pass case when eager
+    B, Hq, Hkv, Lq, Lk, causal, mode, qp, lv, nsplit = case
+    (q, k, v), (qh, kh, vh, vt), kw = _decode_inputs(case, dev)
+    monkeypatch.delenv("FAQ_DECODE_FUSED", raising=False)
+    monkeypatch.delenv("FAQ_DECODE_SPIN", raising=False)
+    kbuf = kh.clone()
+    out = torch.empty((B, Lq, Hq, 128), device=dev, dtype=torch.float32)
+    den = torch.empty((B, Hq, Lq), device=dev, dtype=torch.float32)
+    call = lambda: _ops.attention_decode(qh, Lk, k=kbuf, v=vh, split=nsplit, out=out.transpose(1, 2),  # noqa: E731
+                                         row_den=den, **kw)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep, factor in enumerate((1.0, 2.0, 0.5, 4.0, 1.0)):
+        kbuf.copy_(kh * factor)
+        graph.replay()
+        torch.cuda.synchronize()
+        got_o, got_l = out.clone(), den.clone()
+        monkeypatch.setenv("FAQ_DECODE_FUSED", "0")
+        want = _run(lambda **a: _ops.attention_decode(qh, Lk, k=kbuf, v=vh, split=nsplit, **kw, **a), case, dev)
+        monkeypatch.delenv("FAQ_DECODE_FUSED")
+        torch.cuda.synchronize()
+        print(f"[graph] replay {rep} keys x{factor}", flush=True)
+        assert torch.equal(got_o, want[0]) and torch.equal(got_l, want[1]), rep
 
 
 def test_one_pass_decode_is_refused_where_it_does_not_apply(dev, monkeypatch):
