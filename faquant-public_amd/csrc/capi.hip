@@ -86,15 +86,15 @@ void launch_act_row_r(const faq::ActRowArgs& a, int levels, size_t lds, hipStrea
   else launch_act_row_g<T, R, NT, false>(a, levels, lds, st);
 }
 
-// 8-value chunks per lane and threads per row: 256 threads with 1 or 2 chunks each up to
-// 4096 features, then 512 and 1024 threads with 2 (more waves per row keep more loads in
-// flight: at 12288 features 1024 threads take 0.94 of the time of 512 with 4 chunks).
+// 8-value chunks per lane and threads per workgroup: 256 threads with 1 or 2 chunks each up
+// to 4096 features, then 512 and 1024 threads with 2, and 1024 threads with 4 up to 32768.
 template <typename T>
 void launch_act_row(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
   if (a.cols <= 2048) launch_act_row_r<T, 1, 256>(a, levels, lds, st);
   else if (a.cols <= 4096) launch_act_row_r<T, 2, 256>(a, levels, lds, st);
   else if (a.cols <= 8192) launch_act_row_r<T, 2, 512>(a, levels, lds, st);
-  else launch_act_row_r<T, 2, 1024>(a, levels, lds, st);
+  else if (a.cols <= 16384) launch_act_row_r<T, 2, 1024>(a, levels, lds, st);
+  else launch_act_row_r<T, 4, 1024>(a, levels, lds, st);
 }
 
 // LDS bytes one workgroup of the current device may hold (cached per device; 64 KiB when
@@ -518,8 +518,10 @@ int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
       return fail(FAQ_EINVAL, "dimension %lld must be divisible by power-of-two block_size=%d", static_cast<long long>(cols), b);
     return FAQ_OK;
   };
-  if (!aligned16(o.col_scale) || !aligned16(o.rot_perm) || !aligned16(o.compand) || !aligned16(o.rot_signs))
+  if (!aligned16(o.col_scale) || !aligned16(o.rot_perm) || !aligned16(o.compand) || !aligned16(o.rot_signs) ||
+      !aligned16(o.compand_rcp))
     return fail(FAQ_EINVAL, "%s: the input scale, sign, permutation and companding vectors must be 16-byte aligned", who);
+  if (o.compand_rcp && !o.compand) return fail(FAQ_EINVAL, "%s: a companding reciprocal needs the companding scale", who);
   if (o.rot_signs && !o.rot_perm) return fail(FAQ_EINVAL, "%s: a rotation needs both signs and permutation", who);
   if (!o.rot_signs && (o.rot_perm || o.rot_block)) return fail(FAQ_EINVAL, "%s: a rotation needs both signs and permutation", who);
   if (int st = check_block(o.rot_block)) return st;
@@ -553,6 +555,7 @@ int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
   a.act_min = o.act_min;
   a.act_max = o.act_max;
   a.compand = o.compand;
+  a.compand_rcp = o.compand_rcp;
   a.n = online;
   a.gen12 = gen12;
   a.div = sqrt_div(gen12 ? static_cast<int>(cols) : online);
@@ -566,6 +569,21 @@ int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
   if (dtype == FAQ_F32) launch_act_row<float>(a, levels, lds, st);
   else if (dtype == FAQ_BF16) launch_act_row<__hip_bfloat16>(a, levels, lds, st);
   else launch_act_row<__half>(a, levels, lds, st);
+  return check_launch(who);
+}
+
+int faq_act_compand_rcp(const float* compand, float* rcp, int64_t n, int dtype, faq_stream_t stream) {
+  const char* who = "faq_act_compand_rcp";
+  if (n < 0) return fail(FAQ_EINVAL, "%s: negative size", who);
+  if ((!compand || !rcp) && n > 0) return fail(FAQ_EINVAL, "%s: null input or output", who);
+  if (!valid_dtype(dtype)) return fail(FAQ_EINVAL, "%s: bad dtype", who);
+  if (n == 0) return FAQ_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  if (dtype == FAQ_F32) hipLaunchKernelGGL(faq::compand_rcp_kernel<float>, grid, dim3(256), 0, st, compand, rcp, n);
+  else if (dtype == FAQ_BF16)
+    hipLaunchKernelGGL(faq::compand_rcp_kernel<__hip_bfloat16>, grid, dim3(256), 0, st, compand, rcp, n);
+  else hipLaunchKernelGGL(faq::compand_rcp_kernel<__half>, grid, dim3(256), 0, st, compand, rcp, n);
   return check_launch(who);
 }
 

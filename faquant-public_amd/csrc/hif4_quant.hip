@@ -42,6 +42,17 @@ struct Io<float> {
     *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
     *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
   }
+  // 8 values as loaded, unpacked later (a load kept in flight across other work)
+  struct Raw {
+    float4 a, b;
+  };
+  static __device__ __forceinline__ Raw load_raw8(const float* p) {
+    return Raw{*reinterpret_cast<const float4*>(p), *reinterpret_cast<const float4*>(p + 4)};
+  }
+  static __device__ __forceinline__ void unpack8(const Raw& w, float* v) {
+    v[0] = w.a.x; v[1] = w.a.y; v[2] = w.a.z; v[3] = w.a.w;
+    v[4] = w.b.x; v[5] = w.b.y; v[6] = w.b.z; v[7] = w.b.w;
+  }
 };
 
 template <>
@@ -69,21 +80,51 @@ struct Io<__hip_bfloat16> {
     for (int i = 0; i < 4; ++i) w[i] = pack2_bf16_hw(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
   }
+  using Raw = uint4;
+  static __device__ __forceinline__ Raw load_raw8(const T* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ void unpack8(const Raw& a, float* v) {
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
 };
+
+// fp32 -> fp16, round to nearest even, of a value already rounded to fp32.  The empty asm
+// keeps the compiler from fusing the multiply or add that produced v into the conversion as
+// one mixed-precision fma (v_fma_mixlo_f16 a, b, 0): that rounds the exact a * b once to fp16
+// instead of rounding to fp32 first, as torch does, and its +0 addend turns a -0 product
+// into +0.
+__device__ __forceinline__ __half f16_rn(float v) {
+  asm volatile("" : "+v"(v));
+  return __float2half_rn(v);
+}
 
 template <>
 struct Io<__half> {
   using T = __half;
   static __device__ __forceinline__ float load(const T* p) { return __half2float(*p); }
-  static __device__ __forceinline__ void store(T* p, float v) { *p = __float2half_rn(v); }
-  static __device__ __forceinline__ float round(float v) { return __half2float(__float2half_rn(v)); }
+  static __device__ __forceinline__ void store(T* p, float v) { *p = f16_rn(v); }
+  static __device__ __forceinline__ float round(float v) { return __half2float(f16_rn(v)); }
   static __device__ __forceinline__ void load8(const T* p, float* v) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = __half2float(p[i]);
   }
   static __device__ __forceinline__ void store8(T* p, const float* v) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = __float2half_rn(v[i]);
+    for (int i = 0; i < 8; ++i) p[i] = f16_rn(v[i]);
+  }
+  using Raw = uint4;
+  static __device__ __forceinline__ Raw load_raw8(const T* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ void unpack8(const Raw& a, float* v) {
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[i] & 0xFFFFu)));
+      v[2 * i + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[i] >> 16)));
+    }
   }
 };
 
@@ -526,7 +567,7 @@ __global__ __launch_bounds__(256) void act_qdq_rows_kernel(ActQdqArgs a) {
 // cast back; the HiF4 QDQ; x / companding scale.  Every elementwise step rounds to the input
 // dtype as torch does.  One workgroup per row (256 or 512 threads), the row in registers;
 // LDS holds an fp32 copy for the permutation gather and the Hadamard strides above 4.
-constexpr int kActMaxCols = 16384;
+constexpr int kActMaxCols = 32768;
 
 struct ActRowArgs {
   const void* x;            // [rows, cols] contiguous, dtype T
@@ -541,16 +582,18 @@ struct ActRowArgs {
   int has_min, has_max;
   float act_min, act_max;   // clamp bounds (rounded to T in the kernel)
   const float* compand;     // [cols] companding scale (values of T), or null
+  const float* compand_rcp; // [cols] fp32(1 / compand) where the product form is exact, else 0; or null
   int n;                    // 0, or the online block Hadamard size (with gen12: cols / 12)
   int gen12;                // 1: the generalized transform of a row of 12 n values
   SqrtDiv div;              // division by fp32(sqrt(n)) (with gen12: of the row length)
   int quant;                // 1: HiF4 QDQ
 };
 
-// Layout of act_row_kernel (NT threads): lane tid holds chunk c = tid + NT r (r < R) of the
-// row, the 8 values 8 c .. 8 c + 7, in registers (the coalesced load / store layout and the
-// QDQ layout: 8 consecutive lanes hold one 64-value group).  LDS holds one fp32 copy of the
-// row for the permutation gather and for the butterfly stages that cross lanes.
+// Layout of act_row_kernel (NT threads, R chunks per lane): lane tid holds chunk
+// c = tid + NT r (r < R) of the row, the 8 values 8 c .. 8 c + 7, in registers (the
+// coalesced load / store layout and the QDQ layout: 8 consecutive lanes hold one 64-value
+// group).  LDS holds one fp32 copy of the row for the permutation gather and for the
+// butterfly stages that cross lanes.
 // Value j sits at lds_pad(j) = j + j / 8: one spare word after every 8 values, so lanes that
 // write or read their 8-value chunks (8 words apart), and the first butterfly pass over LDS
 // (stride 8), touch distinct banks.
@@ -558,6 +601,12 @@ __host__ __device__ constexpr size_t act_row_lds_bytes(int cols) {
   return static_cast<size_t>(cols + cols / 8) * sizeof(float);
 }
 __device__ __forceinline__ int lds_pad(int j) { return j + (j >> 3); }
+
+// First value of chunk r of lane `tid`.
+template <int R, int NT>
+__device__ __forceinline__ int act_c0(int tid, int r) {
+  return 8 * (tid + NT * r);
+}
 
 // Butterflies (left + right, left - right) of the stages of stride 1 .. S (S = 1, 2 or 4)
 // on each lane's chunks (their pairs lie inside one chunk).
@@ -576,7 +625,11 @@ __device__ __forceinline__ void fwht_in_chunks(float (&v)[R][8]) {
         }
 }
 
-// One pass over the LDS row of the LR stages of stride s, 2 s, .. (LR = 1, 2 or 3; s a
+// Butterfly stages per pass over the LDS row (radix 16: a 1024-block's strides 8 .. 512 in
+// two passes instead of three with radix 8; 12-18% less time at 4096 and 12288 features).
+constexpr int kActRadix = 4;
+
+// One pass over the LDS row of the LR stages of stride s, 2 s, .. (LR = 1 .. 4; s a
 // multiple of 8, 2^LR s dividing the block): group g holds the 2^LR values j0 + m s.
 template <int LR, int NT>
 __device__ __forceinline__ void fwht_lds_pass(float* lds, int cols, int ls, int tid) {
@@ -602,41 +655,52 @@ __device__ __forceinline__ void fwht_lds_pass(float* lds, int cols, int ls, int 
   }
 }
 
+template <int R, int NT>
+__device__ __forceinline__ void row_to_lds(const float (&v)[R][8], float* lds, int cols, int tid) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c0 = act_c0<R, NT>(tid, r);
+    if (c0 < cols)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) lds[lds_pad(c0) + i] = v[r][i];
+  }
+}
+
+template <int R, int NT>
+__device__ __forceinline__ void row_from_lds(float (&v)[R][8], const float* lds, int cols, int tid) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c0 = act_c0<R, NT>(tid, r);
+    if (c0 < cols)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[r][i] = lds[lds_pad(c0) + i];
+  }
+}
+
 // Unnormalized Walsh-Hadamard transform of every b-block of the row (rotation.py:14-29
 // without its division): the stages of stride 1, 2, ..., b / 2 in that order, each pair
 // (i, i + s) becoming (left + right, left - right).  Strides 1, 2, 4 run in registers; larger
-// strides in passes over LDS of up to three stages (s, 2 s, 4 s) on the values j0 + m s read
-// into registers: the same additions as one stage at a time.  Ends with the transformed row
-// in v.
+// strides in passes over LDS of up to kActRadix stages (s, 2 s, 4 s, ..) on the values
+// j0 + m s read into registers: the same additions as one stage at a time.  Ends with the
+// transformed row in v.
 template <int R, int NT>
 __device__ __forceinline__ void fwht_row_raw(float (&v)[R][8], float* lds, int cols, int b, int tid) {
   if (b == 2) fwht_in_chunks<R, 1>(v);
   else if (b == 4) fwht_in_chunks<R, 2>(v);
   else fwht_in_chunks<R, 4>(v);
   if (b > 8) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int c0 = 8 * (tid + NT * r);
-      if (c0 < cols)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) lds[lds_pad(c0) + i] = v[r][i];
-    }
+    row_to_lds<R, NT>(v, lds, cols, tid);
     const int lb = __builtin_ctz(b);
-    for (int ls = 3; ls < lb; ls += 3) {
+    for (int ls = 3; ls < lb; ls += kActRadix) {
       __syncthreads();
-      const int lr = min(3, lb - ls);
-      if (lr == 3) fwht_lds_pass<3, NT>(lds, cols, ls, tid);
+      const int lr = min(kActRadix, lb - ls);
+      if (lr == 4) fwht_lds_pass<4, NT>(lds, cols, ls, tid);
+      else if (lr == 3) fwht_lds_pass<3, NT>(lds, cols, ls, tid);
       else if (lr == 2) fwht_lds_pass<2, NT>(lds, cols, ls, tid);
       else fwht_lds_pass<1, NT>(lds, cols, ls, tid);
     }
     __syncthreads();
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int c0 = 8 * (tid + NT * r);
-      if (c0 < cols)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[r][i] = lds[lds_pad(c0) + i];
-    }
+    row_from_lds<R, NT>(v, lds, cols, tid);
     // the next user of the LDS row writes it again
     __syncthreads();
   }
@@ -664,13 +728,7 @@ constexpr uint16_t kH12NegMask[12] = {0xFFE, 0x474, 0x8E8, 0x1D2, 0x3A4, 0x748,
 template <int R, int NT>
 __device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, int cols, int b, float d, int tid) {
   fwht_row_raw<R, NT>(v, lds, cols, b, tid);
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int c0 = 8 * (tid + NT * r);
-    if (c0 < cols)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) lds[lds_pad(c0) + i] = v[r][i];
-  }
+  row_to_lds<R, NT>(v, lds, cols, tid);
   __syncthreads();
   for (int c = tid; c < b; c += NT) {
     float w[12];
@@ -687,7 +745,7 @@ __device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, in
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int c0 = 8 * (tid + NT * r);
+    const int c0 = act_c0<R, NT>(tid, r);
     if (c0 < cols)
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[r][i] = lds[lds_pad(c0) + i] / d;
@@ -695,10 +753,34 @@ __device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, in
   __syncthreads();
 }
 
+// Whether the companding quotient T(x / c) of every T value x equals T(x * fp32(1 / c)):
+// bf16 scales that are normal numbers, fp16 scales below 8 in magnitude (the reference's
+// scales exp(clamp(log_scale, -2.079, 2.079)) lie in (0.125, 8)).  Proved over every pair of
+// 16-bit values on the CPU (tests/compand_div_check.c); fp32 always divides.
+template <typename T>
+__device__ __forceinline__ bool compand_product_exact(float c) {
+  const uint32_t u = __float_as_uint(c) & 0x7FFFFFFFu;
+  if constexpr (std::is_same<T, __hip_bfloat16>::value) return (u & 0x7F800000u) != 0;
+  else if constexpr (std::is_same<T, __half>::value) return u < 0x41000000u;
+  else return false;
+}
+
+// rcp[j] = fp32(1 / c[j]) where the product form of the companding quotient is exact for
+// dtype T, 0 elsewhere (the activation kernel divides those columns).
+template <typename T>
+__global__ __launch_bounds__(256) void compand_rcp_kernel(const float* c, float* rcp, int64_t n) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j < n) rcp[j] = compand_product_exact<T>(c[j]) ? 1.0f / c[j] : 0.0f;
+}
+
 // One workgroup of NT threads per row of at most 8 NT R values.  R stays at most 4: with
 // 8 chunks per lane the compiler keeps the row in scratch memory instead of registers.
+// With R <= 2 the kernel asks for 8 waves per SIMD (at most 64 VGPRs): two 1024-thread or
+// eight 256-thread workgroups per CU (at 67 VGPRs one fewer fits, and a 12288-feature row
+// with a 1024-block rotation took 126 instead of 103 us).
 template <typename T, int LV, int R, int NT, bool kGen12>
-__global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 8 : 1))) void act_row_kernel(
+    ActRowArgs a) {
   extern __shared__ float act_row_lds[];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
@@ -707,7 +789,7 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
   float v[R][8];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int c0 = 8 * (tid + NT * r);
+    const int c0 = act_c0<R, NT>(tid, r);
     if (c0 < a.cols) {
       Io<T>::load8(x + c0, v[r]);
       if (a.col_scale) {
@@ -726,7 +808,7 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
     // permutation (index_select): value j is x[perm[j]] sign[perm[j]]
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int c0 = 8 * (tid + NT * r);
+      const int c0 = act_c0<R, NT>(tid, r);
       if (c0 < a.cols) {
         const uint2 sw = *reinterpret_cast<const uint2*>(a.rot_signs + c0);
 #pragma unroll
@@ -739,7 +821,7 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int c0 = 8 * (tid + NT * r);
+      const int c0 = act_c0<R, NT>(tid, r);
       if (c0 < a.cols) {
         const int4 pa = *reinterpret_cast<const int4*>(a.rot_perm + c0);
         const int4 pb = *reinterpret_cast<const int4*>(a.rot_perm + c0 + 4);
@@ -757,7 +839,7 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
   const float lo = Io<T>::round(a.act_min), hi = Io<T>::round(a.act_max);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int c0 = 8 * (tid + NT * r);
+    const int c0 = act_c0<R, NT>(tid, r);
     float cs[8];
     if (a.compand && c0 < a.cols) Io<float>::load8(a.compand + c0, cs);
 #pragma unroll
@@ -782,20 +864,33 @@ __global__ __launch_bounds__(NT) void act_row_kernel(ActRowArgs a) {
       for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(v[r][i]);
   }
   // QDQ: every lane takes part (zeros past the row), as qdq8 exchanges values within its 8
-  // lanes; then the companding quotient of the quantized values in T
+  // lanes; then the companding quotient of the quantized values in T: a product with the
+  // column's reciprocal (compand_rcp) where every column of the lane's chunk has one and the
+  // wave agrees (a uniform branch), the IEEE division otherwise
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int c0 = 8 * (tid + NT * r);
+    const int c0 = act_c0<R, NT>(tid, r);
     if (a.quant) qdq8<LV>(v[r]);
-    if (c0 < a.cols) {
-      if (a.compand) {
+    if (a.compand) {
+      float rc[8];
+      bool ok = a.compand_rcp != nullptr;
+      if (ok && c0 < a.cols) {
+        Io<float>::load8(a.compand_rcp + c0, rc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ok = ok && rc[i] != 0.0f;
+      }
+      if (__all(ok)) {
+        if (c0 < a.cols)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(Io<T>::round(v[r][i]) * rc[i]);
+      } else if (c0 < a.cols) {
         float cs[8];
         Io<float>::load8(a.compand + c0, cs);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(Io<T>::round(v[r][i]) / cs[i]);
       }
-      Io<T>::store8(y + c0, v[r]);
     }
+    if (c0 < a.cols) Io<T>::store8(y + c0, v[r]);
   }
 }
 

@@ -75,6 +75,7 @@ class ActOpts(ctypes.Structure):
         ("compand", _vp),
         ("hadamard", _c_int),
         ("hadamard_generalized", _c_int),
+        ("compand_rcp", _vp),
     ]
 
 
@@ -91,6 +92,7 @@ _SIGNATURES = {
     "faq_hadamard_rows_native": ([_vp, _vp, _c_i64, _c_i64, _c_int, _vp], _c_int),
     "faq_act_qdq_rows": ([_vp, _vp, _c_i64, _c_i64, _c_int, _vp, _c_int, _c_int, _vp], _c_int),
     "faq_act_prep_rows": ([_vp, _vp, _c_i64, _c_i64, _c_int, _act_opts_p, _c_int, _vp], _c_int),
+    "faq_act_compand_rcp": ([_vp, _vp, _c_i64, _c_int, _vp], _c_int),
     "faq_hif4_unpack_rows": ([_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _vp, _vp], _c_int),
     "faq_operand_prep": (
         [

@@ -154,6 +154,7 @@ def act_prep_rows(
     hadamard: int = 0,
     hadamard_generalized: bool = False,
     out: torch.Tensor | None = None,
+    compand_rcp: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The full activation path of a quantized Linear along the last axis of ``x``
     (faq_act_prep_rows): x * dtype(col_scale); the HiSQ input rotation (fp32 x times
@@ -162,8 +163,9 @@ def act_prep_rows(
     ``compand`` (already in x's dtype); the online block Hadamard of ``hadamard`` values, or
     with ``hadamard_generalized`` the generalized transform of the whole row (rotation.py:
     53-69: a power of two or 12 times one); HiF4 QDQ with ``levels``; x / ``compand``.
-    Output in x's dtype."""
-    _lib.require_device(x, col_scale, rot_signs, rot_perm, compand)
+    Output in x's dtype.  ``compand_rcp`` is ``act_compand_rcp(compand, x.dtype)``, computed
+    here when not given (callers that keep the scale keep it too)."""
+    _lib.require_device(x, col_scale, rot_signs, rot_perm, compand, compand_rcp)
     lib = _lib.load()
     if x.ndim == 0:
         raise ValueError("HiF4 fake quantization requires at least one dimension")
@@ -186,6 +188,8 @@ def act_prep_rows(
 
     if (rot_signs is None) != (rot_perm is None):
         raise ValueError("the input rotation needs both signs and permutation")
+    if compand is not None and compand_rcp is None and rows > 0:
+        compand_rcp = act_compand_rcp(compand.to(device=x.device, dtype=torch.float32).reshape(-1), x.dtype)
     opts = _lib.ActOpts(
         col_scale=vec(col_scale, torch.float32, "input scale"),
         rot_signs=vec(rot_signs, torch.int8, "rotation signs"),
@@ -198,6 +202,7 @@ def act_prep_rows(
         compand=vec(compand, torch.float32, "companding scale"),
         hadamard=int(hadamard or 0),
         hadamard_generalized=int(bool(hadamard_generalized)),
+        compand_rcp=vec(compand_rcp, torch.float32, "companding reciprocal") if compand is not None else None,
     )
     _lib.check(
         lib.faq_act_prep_rows(
@@ -207,6 +212,19 @@ def act_prep_rows(
     )
     del keep
     return y.view(x.shape)
+
+
+def act_compand_rcp(compand: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """fp32 reciprocals of a companding scale (fp32 values of ``dtype``) where the activation
+    kernel's product form of x / scale is exact for ``dtype``, 0 elsewhere
+    (faq_act_compand_rcp)."""
+    _lib.require_device(compand)
+    lib = _lib.load()
+    c = compand.to(torch.float32).reshape(-1).contiguous()
+    rcp = torch.empty_like(c)
+    _lib.check(lib.faq_act_compand_rcp(c.data_ptr(), rcp.data_ptr(), c.numel(), _lib.dtype_code(dtype),
+                                       _lib.stream_ptr(c.device)))
+    return rcp
 
 
 def act_qdq_rows(

@@ -150,8 +150,9 @@ class FakeQuantLinear(torch.nn.Module):
     def _prep_vectors(self, x: torch.Tensor):
         """The per-feature vectors of the activation path in the kernel's forms (int32
         permutation; the companding scale computed as the reference does: clamp to +-2.079,
-        exp, cast to x's dtype, then held as fp32) and the clamp bounds as floats, cached per
-        device and dtype and recomputed when a buffer is modified in place or replaced."""
+        exp, cast to x's dtype, then held as fp32; its reciprocals for the kernel's product
+        form of the final division) and the clamp bounds as floats, cached per device and
+        dtype and recomputed when a buffer is modified in place or replaced."""
         tensors = (self.input_rotation_permutation, self.activation_compand_log_scale, self.activation_min,
                    self.activation_max)
         key = (x.device, x.dtype) + tuple(None if t is None else t._version for t in tensors)
@@ -162,7 +163,7 @@ class FakeQuantLinear(torch.nn.Module):
         perm = None
         if self.input_rotation_permutation is not None:
             perm = self.input_rotation_permutation.to(device=x.device, dtype=torch.int32).contiguous()
-        compand = None
+        compand = rcp = None
         if self.activation_compand_log_scale is not None:
             log_scale = self.activation_compand_log_scale
             if log_scale.numel() != self.in_features:
@@ -170,9 +171,12 @@ class FakeQuantLinear(torch.nn.Module):
                     raise RuntimeError("invalid activation companding shape")
                 log_scale = log_scale.repeat_interleave(self.in_features // log_scale.numel())
             compand = log_scale.clamp(-2.079, 2.079).exp().to(device=x.device, dtype=x.dtype).float().contiguous()
+            from . import _ops
+
+            rcp = _ops.act_compand_rcp(compand, x.dtype)
         bounds = (None if self.activation_min is None else float(self.activation_min),
                   None if self.activation_max is None else float(self.activation_max))
-        value = (perm, compand, bounds)
+        value = (perm, compand, bounds, rcp)
         self._prep_cache = (key, value, tensors)
         return value
 
@@ -187,9 +191,9 @@ class FakeQuantLinear(torch.nn.Module):
         if not extra and not generalized and block <= 512:
             xq = _ops.act_qdq_rows(x, levels=HIF4_ACT_SCALE_LEVELS, hadamard=block, col_scale=self.input_scale)
         else:
-            perm, compand, bounds = self._prep_vectors(x)
+            perm, compand, bounds, rcp = self._prep_vectors(x)
             xq = _ops.act_prep_rows(
                 x, levels=HIF4_ACT_SCALE_LEVELS, col_scale=self.input_scale, rot_signs=self.input_rotation_signs,
                 rot_perm=perm, rot_block=self.input_rotation_block_size, act_min=bounds[0], act_max=bounds[1],
-                compand=compand, hadamard=block, hadamard_generalized=generalized)
+                compand=compand, hadamard=block, hadamard_generalized=generalized, compand_rcp=rcp)
         return torch.nn.functional.linear(_lib.forward_only(xq, x), self.weight, self.bias)

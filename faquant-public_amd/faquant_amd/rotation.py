@@ -6,7 +6,7 @@ Reference: src/faquant/rotation.py:14-29 (``hadamard_transform``), 53-84
 butterfly stages in the same order (strides 1, 2, ..., n/2) and divide by
 fp32(sqrt(n)) exactly as CPU torch does, so fp32 results are bit-identical.  Blocks
 above 512 and the generalized transform run in the row kernel of the Linear activation
-path (rows of at most 16384 features, a multiple of 64).
+path (rows of at most 32768 features, a multiple of 64).
 """
 
 from __future__ import annotations
@@ -56,9 +56,9 @@ def _row_path(x: torch.Tensor, **kw) -> torch.Tensor:
     """fp32 transform of each row with one cast back to x's dtype (the activation row
     kernel without its quantizer)."""
     cols = x.shape[-1]
-    if cols % 64 or cols > 16384:
+    if cols % 64 or cols > 32768:
         raise NotImplementedError(
-            f"transforms of {cols} values run on rows of a multiple of 64 features, at most 16384"
+            f"transforms of {cols} values run on rows of a multiple of 64 features, at most 32768"
         )
     return _ops.act_prep_rows(x, levels=None, **kw)
 

@@ -183,6 +183,8 @@ typedef struct faq_act_opts {
   int hadamard_generalized; /* 1: the online transform is generalized_hadamard_transform over
                                the whole row (cols a power of two, or 12 times one;
                                rotation.py:53-69); hadamard must then be 0 */
+  const float* compand_rcp; /* optional, with compand: faq_act_compand_rcp of the companding
+                               scale; the final x / compand is then a product where exact */
 } faq_act_opts;
 
 /*
@@ -192,15 +194,26 @@ typedef struct faq_act_opts {
  * rotation.py:117-135 when rot_block is set, one cast back; quantization.py:201-219 and
  * hisq_rotation.py:50-71), the activation clamp, x * companding scale, the online block
  * Hadamard with one cast back, the HiF4 QDQ with `levels` (0: none), and x / companding
- * scale; each elementwise step rounds to the input dtype.  Rows of at most 16384 features
+ * scale; each elementwise step rounds to the input dtype.  Rows of at most 32768 features
  * (a multiple of 64), contiguous, fp32 / bf16 / fp16; one workgroup per row.  With the
- * rotation or a Hadamard block above 8 the row passes through LDS as fp32 (4 bytes a feature;
- * FAQ_EUNSUP beyond the device's LDS per workgroup).  x, y and the col_scale, rot_signs,
+ * rotation or a Hadamard block above 8 the row passes through LDS as fp32 (4.5 bytes a
+ * feature; FAQ_EUNSUP beyond the device's LDS per workgroup).  x, y and the col_scale, rot_signs,
  * rot_perm and compand vectors must be 16-byte aligned.  opts may be NULL (then this is faq_act_qdq_rows
  * without input scale or Hadamard).
  */
 int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dtype, const faq_act_opts* opts,
                       int levels, faq_stream_t stream);
+
+/*
+ * The reciprocals faq_act_prep_rows uses for its companding quotient (quantization.py:268,
+ * x / compand_scale in the activation dtype): rcp[j] = fp32(1 / compand[j]) where
+ * dtype(x * rcp) equals dtype(x / compand) for every x of `dtype` (bf16: normal scales;
+ * fp16: |scale| < 8, which holds the reference's scales exp(clamp(log, -2.079, 2.079));
+ * proved over all pairs of 16-bit values), 0 elsewhere and for fp32 (those divide).  No
+ * reference counterpart: a per-layer constant FakeQuantLinear computes once beside its
+ * companding scale.  compand and rcp are n fp32 values on the device.
+ */
+int faq_act_compand_rcp(const float* compand, float* rcp, int64_t n, int dtype, faq_stream_t stream);
 
 /*
  * V operand: x [B, H, L, 128] (strides sb, sh, sl), HiF4 QDQ with `levels` (0 = none),

@@ -42,7 +42,7 @@ def test_header_lists_the_entry_points():
          "faq_attention_fwd_split", "faq_attention_split_workspace", "faq_attention_mask_bounds",
          "faq_mfma_probe", "faq_stream_probe", "faq_pquant_groups", "faq_hadamard_rows_native", "faq_attention_fwd_split_noalloc",
          "faq_operand_prep_hif4_kv", "faq_attention_decode", "faq_attention_decode_workspace",
-         "faq_act_prep_rows"]
+         "faq_act_prep_rows", "faq_act_compand_rcp"]
     )
 
 
@@ -77,11 +77,11 @@ def test_validation_statuses_without_device_work(lib):
     assert lib.faq_act_qdq_rows(p16, p16, 1, 64, 1, None, 0, 99, None) == _lib.EINVAL
     assert "123, 12 or 13" in lib.faq_last_error().decode()
     assert lib.faq_act_qdq_rows(p16, p16, 1, 12, 1, None, 0, 123, None) == _lib.EUNSUP
-    # the full activation path: rows of at most 16384 features, a rotation needs signs and permutation,
+    # the full activation path: rows of at most 32768 features, a rotation needs signs and permutation,
     # block sizes are powers of two dividing the row, levels 0 (no quantizer) or 123 / 12 / 13
     ao = _lib.ActOpts()
     assert lib.faq_act_prep_rows(p16, p16, 1, 96, 1, None, 123, None) == _lib.EUNSUP
-    assert lib.faq_act_prep_rows(p16, p16, 1, 16384 + 64, 1, None, 123, None) == _lib.EUNSUP
+    assert lib.faq_act_prep_rows(p16, p16, 1, 32768 + 64, 1, None, 123, None) == _lib.EUNSUP
     assert lib.faq_act_prep_rows(p16, p16, 1, 64, 1, None, 99, None) == _lib.EINVAL
     assert lib.faq_act_prep_rows(p16 + 2, p16, 1, 64, 1, None, 123, None) == _lib.EINVAL
     ao.rot_signs = p16

@@ -134,7 +134,11 @@ def _prep_on_device(x, dtype, dev, levels, kw):
 
 
 def _same(got, ref):
-    return np.array_equal(np.asarray(got, np.float32), np.asarray(ref, np.float32), equal_nan=True)
+    """Bitwise equality of fp32 arrays (so -0 differs from +0), any NaN matching any NaN."""
+    g, r = np.asarray(got, np.float32), np.asarray(ref, np.float32)
+    if g.shape != r.shape:
+        return False
+    return bool(np.all((g.view(np.uint32) == r.view(np.uint32)) | (np.isnan(g) & np.isnan(r))))
 
 
 def test_act_prep_rows_matches_reference_fixtures(dev):
@@ -182,6 +186,8 @@ PREP_CONFIGS = {
     "rot4096_h4096": (4096, True, 4096, False, True, 4096, True),
     "qwen8b_down_12288": (12288, True, 1024, True, True, 0, False),
     "max_16384_norot": (16384, False, None, True, False, 1024, True),
+    "qwen32b_down_25600": (25600, True, 1024, True, True, 0, False),
+    "max_32768": (32768, True, 2048, True, True, 4096, True),
 }
 
 
@@ -269,6 +275,69 @@ def test_act_prep_rows_edges(dev):
                                compand=comp[2:])
     assert empty.shape == (0, 512)
     assert _ops.act_qdq_rows(torch.empty((0, 3, 512), device=dev, dtype=torch.bfloat16), levels="123").shape == (0, 3, 512)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+def test_act_prep_rows_streams_many_rows(dev, dtype):
+    """More rows than workgroups (each workgroup streams rows, the next one's load in flight),
+    every option on, against the oracle bitwise; then scales outside the product form's
+    proven range in a few columns (bf16: subnormal; fp16: 14 and 40), whose waves divide."""
+    from oracle import linear as OL
+
+    for cols, rows in ((4096, 1800), (1024, 5000), (12288, 600)):
+        x, kw = _random_prep_case(cols ^ rows, cols, dtype, rot=True, rot_block=1024, clamp=True, comp=True,
+                                  hadamard=0, scale=True)
+        x = np.resize(x, (rows, cols)).astype(np.float32)
+        x[::7] *= np.float32(1.5)
+        x = OQ.bf16_round(x) if dtype == "bfloat16" else (
+            x.astype(np.float16).astype(np.float32) if dtype == "float16" else x)
+        print(f"[act_prep stream] cols={cols} rows={rows} {dtype}", flush=True)
+        got = _prep_on_device(x, dtype, dev, "123", kw).float().cpu().numpy()
+        assert _same(got, OL.fake_quant_linear_input(x, dtype, levels="123", **kw))
+        if dtype != "float32" and cols == 4096:
+            comp = kw["compand"].copy()
+            comp[[5, 700, 3001]] = np.float32(2.0 ** -130) if dtype == "bfloat16" else np.float32([14.0, 40.0, 14.0])
+            kw2 = dict(kw, compand=comp)
+            print(f"[act_prep stream] divided columns {dtype}", flush=True)
+            got = _prep_on_device(x, dtype, dev, "123", kw2).float().cpu().numpy()
+            assert _same(got, OL.fake_quant_linear_input(x, dtype, levels="123", **kw2))
+
+
+def test_compand_reciprocals_and_both_quotient_forms(dev):
+    """faq_act_compand_rcp: fp32(1 / c) where the product form is exact for the dtype (bf16:
+    normal scales; fp16: |c| < 8), 0 elsewhere and for fp32; and the activation path gives the
+    same bits with the reciprocals (product form) and without them (every column divides)."""
+    from oracle import linear as OL
+    from faquant_amd import _ops
+
+    c = np.float32([0.125, 0.5, 1.0, 3.0, 7.99, 8.0, 14.0, 2.0 ** -130, 1e30, -2.5, 0.0, np.inf] + [1.5] * 4)
+    for dtype, keep in (("bfloat16", lambda a: (np.abs(a) >= 2.0 ** -126) & (a != 0)),
+                        ("float16", lambda a: np.abs(a) < 8.0), ("float32", lambda a: np.zeros(a.shape, bool))):
+        got = _ops.act_compand_rcp(to_dev(c, dev), _TORCH_DT[dtype]).cpu().numpy()
+        with np.errstate(divide="ignore"):
+            want = np.where(keep(c), np.float32(1.0) / c, np.float32(0.0)).astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), dtype
+    for dtype in ("bfloat16", "float16"):
+        x, kw = _random_prep_case(77, 2048, dtype, rot=True, rot_block=1024, clamp=True, comp=True, hadamard=0,
+                                  scale=False)
+        x = np.resize(x, (300, 2048)).astype(np.float32)
+        xt = to_dev(x, dev, _TORCH_DT[dtype])
+        comp = to_dev(kw["compand"], dev)
+        args = dict(levels="123", rot_signs=to_dev(kw["rot_signs"], dev, torch.int8),
+                    rot_perm=to_dev(kw["rot_perm"], dev, torch.int32), rot_block=1024, act_min=kw["act_min"],
+                    act_max=kw["act_max"], compand=comp)
+        prod = _ops.act_prep_rows(xt, **args, compand_rcp=_ops.act_compand_rcp(comp, _TORCH_DT[dtype]))
+        div = _ops.act_prep_rows(xt, **args, compand_rcp=torch.zeros_like(comp))
+        print(f"[compand forms] {dtype}", flush=True)
+        ref = OL.fake_quant_linear_input(x, dtype, levels="123", **kw)
+        pn, dn = prod.float().cpu().numpy(), div.float().cpu().numpy()
+        bad = np.argwhere(pn.view(np.uint32) != dn.view(np.uint32))
+        for rr, cc in bad[:8]:
+            print(f"  row {rr} col {cc}: product {pn[rr, cc]!r} division {dn[rr, cc]!r} oracle {ref[rr, cc]!r} "
+                  f"scale {kw['compand'][cc]!r}", flush=True)
+        print(f"  {len(bad)} differ; product==oracle {_same(pn, ref)} division==oracle {_same(dn, ref)}", flush=True)
+        assert torch.equal(prod.view(torch.int16), div.view(torch.int16))
+        assert _same(pn, ref)
 
 
 def test_fake_quant_linear_generalized_online_hadamard(dev):
@@ -462,7 +531,7 @@ def test_companding_scale_is_within_one_ulp_of_the_exact_exponential(dev):
                           symmetric=True, clip_ratio=1.0, activation_compand_log_scale=to_dev(log_scale, dev))
     for dtype, round_exact in ((torch.float32, lambda a: a.astype(np.float32)),
                                (torch.bfloat16, lambda a: OQ.bf16_round(a.astype(np.float32)))):
-        _, compand, _ = mod._prep_vectors(torch.zeros(1, n, device=dev, dtype=dtype))
+        _, compand, _, _ = mod._prep_vectors(torch.zeros(1, n, device=dev, dtype=dtype))
         got = compand.cpu().numpy()
         want = round_exact(exact)
         step = np.spacing(want) if dtype == torch.float32 else np.spacing(want) * 65536.0
