@@ -392,6 +392,7 @@ def linear_prep_bench(tokens: int, steps: int, warmup: int) -> dict:
         # bf16 values), as FakeQuantLinear caches them
         perm = torch.randperm(k, device=dev, generator=gen).to(torch.int32)
         comp = torch.rand((k,), device=dev, generator=gen).mul(2).sub(1).exp().to(torch.bfloat16).float()
+        comp_rcp = _ops.act_compand_rcp(comp, torch.bfloat16)  # a per-layer constant the module keeps
 
         def timed(fn):
             for _ in range(warmup):
@@ -411,7 +412,7 @@ def linear_prep_bench(tokens: int, steps: int, warmup: int) -> dict:
             ("qdq_only", lambda: _ops.act_qdq_rows(x, levels="123", out=y)),
             ("hisq_clamp_compand", lambda: _ops.act_prep_rows(x, levels="123", rot_signs=signs, rot_perm=perm,
                                                               rot_block=1024, act_min=-8.0, act_max=8.0,
-                                                              compand=comp, out=y)),
+                                                              compand=comp, compand_rcp=comp_rcp, out=y)),
             # the online Hadamard without a block size: the whole row (12 x 1024 at 12288)
             ("online_generalized", lambda: _ops.act_prep_rows(x, levels="123", hadamard_generalized=True, out=y)),
         ):
