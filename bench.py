@@ -232,12 +232,14 @@ def mfma_probe(dev) -> float:
     return blocks * 8 * iters * 4 * 32768 / (ms * 1e-3) / 1e12
 
 
-def decode_bench(cfg, context: int, steps: int, warmup: int) -> dict:
+def decode_bench(cfg, context: int, steps: int, warmup: int, layers: int = 1) -> dict:
     """One decode step (one new query position per head) of `cfg`'s heads over `context` cached
     keys, timed three ways with HIP events on the launch stream: the split-key path
     (faq_attention_fwd_split), the decode kernel over bf16 K/V and over packed HiF4 K/V.
     The roofline is HBM: algorithmic bytes = the K and V cache bytes one step must read
-    (bf16: 512 per key and KV head, packed: 144) plus Q and the output."""
+    (bf16: 512 per key and KV head, packed: 144) plus Q and the output.  With `layers` > 1 the
+    steps cycle through that many independent caches (as a model's layers do), so that the
+    caches together exceed the 256 MB last-level cache and every step reads from HBM."""
     import torch
 
     from faquant_amd import _ops
@@ -247,27 +249,47 @@ def decode_bench(cfg, context: int, steps: int, warmup: int) -> dict:
     lv = cfg["levels"]
     gen = torch.Generator(device=dev).manual_seed(1)
     q = torch.randn((B, Hq, 1, 128), device=dev, generator=gen).to(torch.bfloat16)
-    k = torch.randn((B, Hkv, L, 128), device=dev, generator=gen).to(torch.bfloat16)
-    v = torch.randn((B, Hkv, L, 128), device=dev, generator=gen).to(torch.bfloat16)
     qh, _ = _ops.operand_prep(q, levels=lv, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16)
-    kh, _ = _ops.operand_prep(k, levels=lv, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16)
-    vt = _ops.operand_prep_vt(v, levels=lv)  # the split path's V^T
-    vh, _ = _ops.operand_prep(v, levels=lv)  # the decode cache's natural rows
-    kc = _ops.pack_operand(k, levels=lv, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16,
-                           out=_ops.PackedHiF4KV(B, Hkv, L, dev, lv))
-    vc = _ops.pack_operand(v, levels=lv, out=_ops.PackedHiF4KV(B, Hkv, L, dev, lv))
-    del k, v
+    caches = []
+    for _ in range(max(1, layers)):
+        k = torch.randn((B, Hkv, L, 128), device=dev, generator=gen).to(torch.bfloat16)
+        v = torch.randn((B, Hkv, L, 128), device=dev, generator=gen).to(torch.bfloat16)
+        kh, _ = _ops.operand_prep(k, levels=lv, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16)
+        vt = _ops.operand_prep_vt(v, levels=lv)  # the split path's V^T
+        vh, _ = _ops.operand_prep(v, levels=lv)  # the decode cache's natural rows
+        kc = _ops.pack_operand(k, levels=lv, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16,
+                               out=_ops.PackedHiF4KV(B, Hkv, L, dev, lv))
+        vc = _ops.pack_operand(v, levels=lv, out=_ops.PackedHiF4KV(B, Hkv, L, dev, lv))
+        caches.append((kh, vt, vh, kc, vc))
+        del k, v
     out = torch.empty((B, 1, Hq, 128), device=dev, dtype=torch.bfloat16)
     kw = dict(causal=True, scale=128**-0.5, quant_p=True, p_levels=lv, norm_same=True, out=out.transpose(1, 2))
     cus = _ops._device_cus(dev)
     n_split = _ops._split_count(B, Hq, Hkv, 1, L, cus)
     n_dec = _ops.decode_split_count(B, Hkv, L, cus)
     n_dec_packed = _ops.decode_split_count(B, Hkv, L, cus, packed=True)
+    turn = [0]
+
+    def layer():
+        turn[0] += 1
+        return caches[turn[0] % len(caches)]
+
+    def split_step():
+        kh, vt, _, _, _ = layer()
+        return _ops.attention_fwd(qh, kh, vt, L, split=n_split, **kw)
+
+    def dec_step():
+        kh, _, vh, _, _ = layer()
+        return _ops.attention_decode(qh, L, k=kh, v=vh, split=n_dec, **kw)
+
+    def packed_step():
+        _, _, _, kc, vc = layer()
+        return _ops.attention_decode(qh, L, packed=(kc, vc), split=n_dec_packed, **kw)
+
     paths = {
-        "split_path_bf16": (lambda: _ops.attention_fwd(qh, kh, vt, L, split=n_split, **kw), 512, n_split),
-        "decode_bf16": (lambda: _ops.attention_decode(qh, L, k=kh, v=vh, split=n_dec, **kw), 512, n_dec),
-        "decode_packed_hif4": (lambda: _ops.attention_decode(qh, L, packed=(kc, vc), split=n_dec_packed, **kw), 144,
-                               n_dec_packed),
+        "split_path_bf16": (split_step, 512, n_split),
+        "decode_bf16": (dec_step, 512, n_dec),
+        "decode_packed_hif4": (packed_step, 144, n_dec_packed),
     }
     res = {}
     # steps run back to back in five blocks, one event pair around each block, so that the
@@ -302,7 +324,7 @@ def decode_bench(cfg, context: int, steps: int, warmup: int) -> dict:
         "config": {"workload": f"{cfg['workload'].split(' causal')[0]} decode step over {L} cached keys",
                    "batch": B, "q_heads": Hq, "kv_heads": Hkv, "context": L, "hif4_levels": lv,
                    "pv_normalizer": "quantized_same"},
-        "steps": steps, "warmup": warmup, "data": "synthetic",
+        "steps": steps, "warmup": warmup, "data": "synthetic", "layers": max(1, layers),
         "peak_gbps": HBM_PEAK_GBPS,
         "paths": res,
     }
@@ -485,6 +507,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode", type=int, default=0, metavar="CONTEXT",
                     help="time one decode step over CONTEXT cached keys of --config's heads instead")
+    ap.add_argument("--decode-layers", type=int, default=1, metavar="N",
+                    help="with --decode: cycle the steps through N independent K/V caches (N x the cache bytes "
+                         "beyond the 256 MB last-level cache makes every step read HBM)")
     ap.add_argument("--linear", type=int, default=0, metavar="TOKENS",
                     help="time the HiF4 W4A4 Linear at the Wan2.2 DiT block shapes over TOKENS rows instead")
     ap.add_argument("--linear-prep", type=int, default=0, metavar="TOKENS",
@@ -517,7 +542,8 @@ def main():
         return
 
     if args.decode:
-        print(json.dumps(decode_bench(CONFIGS[args.config], args.decode, args.steps, args.warmup)), flush=True)
+        print(json.dumps(decode_bench(CONFIGS[args.config], args.decode, args.steps, args.warmup, args.decode_layers)),
+              flush=True)
         return
 
     if args.calibrate_copy:
