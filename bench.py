@@ -497,9 +497,10 @@ def _ops_cus(dev) -> int:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # the GPU clock settles after a few tens of ms of load: the default warmup covers that
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=10)
+    # the GPU clock settles after a few tens of ms of load: by default the warmup runs at least
+    # 10 steps and at least 0.3 s of them (an 8k step is 0.6 ms); --warmup W runs exactly W
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", default="qwen8b_32k", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=16384)  # about 15 s on 16 cores at 32k
     # the CPU share of one GPU on the GPU boxes is 16 cores
@@ -520,6 +521,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE scaling)")
     args = ap.parse_args()
+    warmup = args.warmup if args.warmup is not None else 10  # the other modes' fixed default
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus})",
               file=sys.stderr)
@@ -530,11 +532,11 @@ def main():
     from faquant_amd import _ops
 
     if args.linear:
-        print(json.dumps(linear_bench(args.linear, args.steps, args.warmup)), flush=True)
+        print(json.dumps(linear_bench(args.linear, args.steps, warmup)), flush=True)
         return
 
     if args.linear_prep:
-        print(json.dumps(linear_prep_bench(args.linear_prep, args.steps, args.warmup)), flush=True)
+        print(json.dumps(linear_prep_bench(args.linear_prep, args.steps, warmup)), flush=True)
         return
 
     if args.stream_reference:
@@ -542,7 +544,7 @@ def main():
         return
 
     if args.decode:
-        print(json.dumps(decode_bench(CONFIGS[args.config], args.decode, args.steps, args.warmup, args.decode_layers)),
+        print(json.dumps(decode_bench(CONFIGS[args.config], args.decode, args.steps, warmup, args.decode_layers)),
               flush=True)
         return
 
@@ -589,8 +591,14 @@ def main():
             b.record()
             ev.append((a, b))
 
-    for _ in range(args.warmup):
+    warm = 0
+    t_warm = time.perf_counter()
+    while warm < (args.warmup if args.warmup is not None else 10) or (
+            args.warmup is None and time.perf_counter() - t_warm < 0.3):
         step()
+        warm += 1
+        if warm % 10 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -617,7 +625,7 @@ def main():
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warm,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
