@@ -665,6 +665,22 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
                                  Lpad, o, o_dtype, o_sb, o_sh, o_sl, B, Hq, Hkv, Lq, Lk, causal, scale, quant_p,
                                  p_levels, row_den, out_levels, opts, a, grid);
   if (rc != FAQ_OK) return rc == 1 ? FAQ_OK : rc;
+  // XCD pacing epoch: nonzero and new per launch; off on a stream being captured (a recorded
+  // launch would reuse its epoch's counters on every replay)
+  {
+    static std::atomic<uint32_t> pace_epochs{0};
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &capture) != hipSuccess ||
+                           capture != hipStreamCaptureStatusNone;
+    uint32_t e = 0;
+    const char* pace_env = std::getenv("FAQ_ATTN_PACE");  // test hook: 0 turns pacing off
+    if (!capturing && !(pace_env && pace_env[0] == '0')) {
+      do e = ++pace_epochs; while (e == 0);
+    }
+    a.pace_epoch = e;
+    const char* lead_env = std::getenv("FAQ_ATTN_PACE_LEAD");  // test hook: the lead in tiles
+    a.pace_lead = lead_env ? std::max(1, std::atoi(lead_env)) : faq::kPaceLead;
+  }
   launch_attention(a, quant_p, p_levels, norm_same, grid, static_cast<hipStream_t>(stream));
   return check_launch("faq_attention_fwd");
 }

@@ -114,7 +114,37 @@ struct AttnArgs {
   // Scores become scale s (+ softcap) + mask; the causal flag is not applied.
   const float* amask;
   int64_t am_sb, am_sh, am_sq;
+  // XCD pacing of long non-causal items (attn_pace below): the launch's epoch, 0 = off
+  uint32_t pace_epoch;
+  int pace_lead;  // tiles a workgroup may run ahead of its XCD's average
 };
+
+// XCD pacing.  Non-causal items all stream one head's K/V tiles in order, and the workgroups of
+// one XCD start consecutive position blocks of one head together, so its L2 serves each K/V
+// tile to all of them while they stay within the ~64 tiles it holds.  Over items of hundreds of
+// tiles they drift further apart than that and fetch the tiles again (Wan 720p: 56 GB per
+// launch against 3.1 GB of K, V, Q and output).  Each workgroup adds kPaceEvery to its XCD's
+// counter every kPaceEvery tiles; one that is more than kPaceLead tiles ahead of its XCD's
+// average then sleeps before its next tile, at most kPaceSpins times.  The count it compares is returned by its own add
+// during the previous tile, and re-read while it waits, by atomic adds (a plain or atomic load
+// can return a stale copy from the CU's own cache); a workgroup that has run all its items
+// adds kPaceDone, so that the XCD's last items never wait.  The counters only time the work: any value, stale or shared with another
+// launch, changes no result, and every wait is bounded.  A launch uses the 8 words of its
+// epoch and clears those of the next epoch (launches on one stream run in order).
+constexpr int kPaceEpochs = 64;
+constexpr int kPaceEvery = 4;  // tiles per count and check (each atomic's latency is waited once)
+constexpr int kPaceLead = 4;  // the default lead (AttnArgs::pace_lead)
+constexpr int kPaceMinTiles = 128;
+constexpr int kPaceSpins = 64;
+constexpr uint32_t kPaceDone = 1u << 16;
+static __device__ uint32_t attn_pace[kPaceEpochs * 8];
+
+// Whether a workgroup `step` tiles in is more than kPaceLead tiles ahead of the average of the
+// nw workgroups whose tiles add up to `seen` (wrapping differences: a stale count far ahead
+// reads as not ahead).
+__device__ __forceinline__ bool pace_ahead(int step, uint32_t seen, int nw, int lead) {
+  return static_cast<int32_t>(static_cast<uint32_t>(step * nw) - seen - static_cast<uint32_t>(lead * nw)) > 0;
+}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -578,6 +608,12 @@ void attn_fwd_kernel(AttnArgs a) {
   if (item >= n_items) return;
   Geo g = geo_of(item);
   int step = 0;  // key tiles processed by this workgroup: LDS stage parity
+  // XCD pacing (attn_pace): plain non-causal launches whose items are long
+  const int pace_nw = P / 8;
+  const bool pace = kMask == 0 && head_major && a.pace_epoch != 0 && g.t_hi - g.t_lo >= kPaceMinTiles;
+  uint32_t* const pace_ctr = attn_pace + (a.pace_epoch % kPaceEpochs) * 8 + (wid & 7);
+  if (pace && wid == 0 && tid < 8) attn_pace[((a.pace_epoch + 1) % kPaceEpochs) * 8 + tid] = 0u;
+  uint32_t pace_seen = 0;  // lane 0 of wave 0: this XCD's tile count, loaded one tile ago
   bool issued = false;  // the DMA of the current item's first tile is in flight
 
   for (;;) {
@@ -656,6 +692,15 @@ void attn_fwd_kernel(AttnArgs a) {
       // tile t has landed for every wave; every wave is done with the previous step, whose
       // stage the DMA of the next step overwrites
       wait_all_memory();
+      if (pace && w == 0 && (step & (kPaceEvery - 1)) == 1) {
+        uint32_t seen = __builtin_amdgcn_readfirstlane(pace_seen);
+        for (int spin = 0; spin < kPaceSpins && pace_ahead(step, seen, pace_nw, a.pace_lead); ++spin) {
+          __builtin_amdgcn_s_sleep(2);
+          uint32_t v = 0;
+          if (lane == 0) v = __hip_atomic_fetch_add(pace_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          seen = __builtin_amdgcn_readfirstlane(v);
+        }
+      }
       __syncthreads();
       // The two waves of a SIMD leave the barrier together, and with equal priorities the
       // older one wins every issue conflict: it finishes its P chunks far ahead and then waits
@@ -670,6 +715,8 @@ void attn_fwd_kernel(AttnArgs a) {
         load_tile(ng.b, ng.kvh, ng.t_lo, (step + 1) & 1);
         issued = true;
       }
+      if (pace && tid == 0 && (step & (kPaceEvery - 1)) == 0)
+        pace_seen = __hip_atomic_fetch_add(pace_ctr, kPaceEvery, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + kPaceEvery;
       do {
         const uint8_t* const st = lds + (step & 1) * kStageBytes;
         const uint8_t* const kp = st + kbyte;
@@ -1027,6 +1074,7 @@ void attn_fwd_kernel(AttnArgs a) {
     if (item >= n_items) break;
     g = ng;
   }
+  if (pace && tid == 0) __hip_atomic_fetch_add(pace_ctr, kPaceDone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Launch of the attention kernel for one masking form (kMask, see attn_fwd_kernel): picks

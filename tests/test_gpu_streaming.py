@@ -101,3 +101,20 @@ def test_streamed_heads_equal_head_subsets(dev):
                               vt[:, h0 : h0 + 8].contiguous(), L, False, out_dtype=torch.bfloat16)
         assert torch.equal(part, full[:, :, h0 : h0 + 8])
         assert torch.equal(part_den, full_den[:, h0 : h0 + 8])
+
+
+def test_xcd_pacing_changes_no_bits(dev, monkeypatch):
+    """Long non-causal items (128 key tiles and more) run with the XCD pacing counters, which
+    only delay workgroups that are ahead of their XCD: the outputs and row denominators equal
+    those of the same launch with pacing off (FAQ_ATTN_PACE=0), bit for bit, on consecutive
+    launches (new epochs) and with more items than workgroups."""
+    B, H, L = 1, 16, 16384
+    qh, kh, vt = _operands(41, B, H, H, L, dev)
+    print(f"[pace] B={B} H={H} L={L} non-causal", flush=True)
+    monkeypatch.setenv("FAQ_ATTN_PACE", "0")
+    ref = _run(qh, kh, vt, L, False)
+    monkeypatch.delenv("FAQ_ATTN_PACE")
+    for rep in range(2):
+        got = _run(qh, kh, vt, L, False)
+        print(f"[pace] launch {rep}", flush=True)
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])
