@@ -506,6 +506,9 @@ def main():
     # the CPU share of one GPU on the GPU boxes is 16 cores
     ap.add_argument("--cpu-workers", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--q-prologue", choices=("fused", "separate"), default="fused",
+                    help="fused: the attention kernel prepares the raw Q rows as it loads them (faq_attn_opts.q_prep); "
+                         "separate: faq_operand_prep writes the Q operand first")
     ap.add_argument("--decode", type=int, default=0, metavar="CONTEXT",
                     help="time one decode step over CONTEXT cached keys of --config's heads instead")
     ap.add_argument("--decode-layers", type=int, default=1, metavar="N",
@@ -574,19 +577,24 @@ def main():
     ev = []
     pev = []
 
+    fused_q = args.q_prologue == "fused"
+
     def step(record=False):
         if record:
             p0 = torch.cuda.Event(enable_timing=True)
             p0.record()
-        _ops.operand_prep(q, levels=levels, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16, out=qh)
+        if not fused_q:
+            _ops.operand_prep(q, levels=levels, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16, out=qh)
         _ops.operand_prep(k, levels=levels, hadamard=cfg["hadamard"], round_dtype=torch.bfloat16, out=kh)
         vt = _ops.operand_prep_vt(v, levels=levels)
         if record:
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             pev.append((p0, a))
-        _ops.attention_fwd(qh, kh, vt, L, causal=causal, scale=128**-0.5, quant_p=True, p_levels=levels,
-                           norm_same=True, out=out.transpose(1, 2))
+        # fused: the kernel applies Q's prologue (Hadamard, bf16 cast, QDQ) to the raw rows
+        _ops.attention_fwd(q if fused_q else qh, kh, vt, L, causal=causal, scale=128**-0.5, quant_p=True,
+                           p_levels=levels, norm_same=True, out=out.transpose(1, 2),
+                           q_prep=(cfg["hadamard"], levels) if fused_q else None)
         if record:
             b.record()
             ev.append((a, b))
@@ -614,8 +622,10 @@ def main():
     # the Q/K/V prologue (HBM-bound): operand reads, bf16 Q/K writes, the padded V^T write
     pro_ms = sum(a.elapsed_time(b) for a, b in pev) / len(pev)
     lpad = -(-L // 128) * 128
-    pro_bytes = (q.numel() * q.element_size() + k.numel() * k.element_size() + v.numel() * v.element_size()
-                 + 2 * (qh.numel() + kh.numel() + B * Hkv * 128 * lpad))
+    # (with the fused Q prologue the kernel reads the raw Q rows itself: no Q bytes here)
+    q_bytes = 0 if fused_q else q.numel() * q.element_size() + 2 * qh.numel()
+    pro_bytes = (q_bytes + k.numel() * k.element_size() + v.numel() * v.element_size()
+                 + 2 * (kh.numel() + B * Hkv * 128 * lpad))
     pro_gbps = pro_bytes / (pro_ms * 1e-3) / 1e9
 
     traffic, traffic_prov = traffic_record(args.config)
@@ -637,7 +647,7 @@ def main():
             "name": args.config,
             "batch": B, "q_heads": Hq, "kv_heads": Hkv, "seq_len": L, "head_dim": 128,
             "causal": causal, "qk_hadamard_block": cfg["hadamard"], "hif4_levels": levels,
-            "pv_normalizer": "quantized_same", "key_tile": 128,
+            "pv_normalizer": "quantized_same", "key_tile": 128, "q_prologue": args.q_prologue,
             "flops_per_step": flops,
         },
         "pct_mfma_peak": round(100.0 * value / MFMA_BF16_PEAK_TFLOPS, 2),

@@ -199,6 +199,10 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
       return fail(FAQ_EINVAL, "%s: the dense mask needs 16-byte aligned rows", who);
     if (opts->pv_probe && !aligned16(opts->pv_probe)) return fail(FAQ_EINVAL, "%s: misaligned pv_probe", who);
     if (opts->p_dump && !quant_p) return fail(FAQ_EINVAL, "%s: the P dump needs quant_p", who);
+    if (opts->q_prep && opts->q_hadamard != 0 && opts->q_hadamard != 64 && opts->q_hadamard != 128)
+      return fail(FAQ_EUNSUP, "%s: the Q prologue's Hadamard block must be 0, 64 or 128, got %d", who, opts->q_hadamard);
+    if (opts->q_prep && opts->q_levels != 0 && !valid_levels(opts->q_levels))
+      return fail(FAQ_EINVAL, "HiF4 levels must be 123, 12 or 13, got %d", opts->q_levels);
     if (opts->p_dump && (!aligned16(opts->p_dump) || opts->p_dump_stride % 4 ||
                          opts->p_dump_stride < 128 * ((static_cast<int64_t>(Lk) + 127) / 128)))
       return fail(FAQ_EINVAL, "%s: p_dump must be 16-byte aligned with a stride >= 128 * ceil(Lk / 128), a multiple of 4",
@@ -267,6 +271,12 @@ int attention_setup(const char* who, const uint16_t* q, int64_t q_sb, int64_t q_
     a.am_sh = opts->dm_sh;
     a.am_sq = opts->dm_sq;
     if (a.amask) a.causal = 0;  // the dense mask replaces the causal rule (sfa:731-757)
+    if (opts->q_prep) {
+      a.q_prep = 1;
+      a.q_had = opts->q_hadamard;
+      a.q_levels = opts->q_levels;
+      a.q_div = sqrt_div(opts->q_hadamard);
+    }
   }
   // the softcap and dense-mask paths scale the scores themselves, which then enter the
   // exponent unscaled

@@ -114,6 +114,11 @@ struct AttnArgs {
   // Scores become scale s (+ softcap) + mask; the causal flag is not applied.
   const float* amask;
   int64_t am_sb, am_sh, am_sq;
+  // Q operand prologue in the item setup (q_frag_prep): q then holds the raw bf16 rows, and
+  // each item applies the per-block fp32 Hadamard of q_had dims (0, 64 or 128) with the
+  // division by q_div, the bf16 cast and the HiF4 QDQ with q_levels (0: none)
+  int q_prep, q_had, q_levels;
+  SqrtDiv q_div;
   // XCD pacing of long non-causal items (attn_pace below): the launch's epoch, 0 = off
   uint32_t pace_epoch;
   int pace_lead;  // tiles a workgroup may run ahead of its XCD's average
@@ -240,6 +245,138 @@ __device__ __forceinline__ bf16x8 pack8(const float* v) {
   bf16x8 r;
   __builtin_memcpy(&r, w, 16);
   return r;
+}
+
+// ---- Q operand prologue in the item setup (AttnArgs::q_prep)
+// operand_prep_kernel's steps for Q (qwen3.py:97-130 without key offset or Smooth-QK:
+// per-block fp32 Hadamard, division by fp32(sqrt(n)), one bf16 cast, HiF4 QDQ;
+// rotation.py:14-29, hif4.py:377-390) on a wave's Q fragment, whose lane (n, half) holds
+// dims 16 c + 8 half + j (c, j < 8) of row n: the butterflies of stride 1, 2, 4 inside a
+// chunk, 8 between lanes n and n + 32, 16, 32, 64 between chunks c and c ^ 1, 2, 4, in that
+// order and each rounded once, as the prologue kernel runs them, so the fragment equals
+// its output bit for bit.  Each Q row feeds one work item: the prologue's separate pass
+// over Q (a read and a write) goes away.
+
+// lane l's copy of u at lane l ^ 32
+__device__ __forceinline__ int lane_swap32(int u) {
+  const auto r = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(u), static_cast<uint32_t>(u), false, false);
+  return (threadIdx.x & 32) ? static_cast<int>(r[0]) : static_cast<int>(r[1]);
+}
+
+// The stride-8 butterfly (left + right at lane n, left - right at lane n + 32) of two values
+// x and y at once: one v_permlane32_swap brings lane n + 32's x next to lane n's and lane n's
+// y next to lane n + 32's, the sum and difference are formed in place, and a second swap
+// puts each result in its lane.
+__device__ __forceinline__ void butterfly32_pair(float& x, float& y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  const float xs = __uint_as_float(r[0]), ys = __uint_as_float(r[1]);
+  const float sum = xs + ys, dif = xs - ys;
+  const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(dif), false, false);
+  x = __uint_as_float(r2[0]);
+  y = __uint_as_float(r2[1]);
+}
+
+// HiF4 QDQ of the fragment: 64-value group g (dims 64 g ..) is chunks 4 g .. 4 g + 3 of lanes
+// n and n + 32; the steps of qdq8 (group maximum of the 4-value maxima, E6M2 scale, micro
+// exponents, elements, a NaN anywhere makes the group NaN).  The sign of qdq8's
+// `w < 0 ? -y : y` is the sign bit of w + 0 (which turns -0 into +0, the one value where
+// the sign bit and w < 0 differ), ORed into y (>= +0); the NaN select runs only when some
+// lane of the wave holds a NaN group.  Both replace per-value v_cndmask, bit for bit.
+template <int LV>
+__device__ __forceinline__ void q_frag_qdq(float (&v)[8][8]) {
+  int nan_any = 0;
+  int nan_g[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    float m3a[4], m3b[4];
+    int nan = 0, mx = 0;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const float* w = v[4 * g + cc];
+      m3a[cc] = fmaxf(fmaxf(fabsf(w[0]), fabsf(w[1])), fmaxf(fabsf(w[2]), fabsf(w[3])));
+      m3b[cc] = fmaxf(fmaxf(fabsf(w[4]), fabsf(w[5])), fmaxf(fabsf(w[6]), fabsf(w[7])));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) nan |= w[j] != w[j];
+      mx = max(mx, __float_as_int(fmaxf(m3a[cc], m3b[cc])));
+    }
+    mx = max(mx, lane_swap32(mx));
+    nan |= lane_swap32(nan);
+    float sc, rec;
+    hif4_scale<LV>(__int_as_float(mx), sc, rec);
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      float* w = v[4 * g + cc];
+      int ka, kb;
+      hif4_micro<LV>(m3a[cc], m3b[cc], rec, ka, kb);
+      float qa, da, qb, db;
+      hif4_group_mults(sc, rec, ka, qa, da);
+      hif4_group_mults(sc, rec, kb, qb, db);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float y = hif4_element(fabsf(w[j]), j < 4 ? qa : qb, j < 4 ? da : db);
+        w[j] = __uint_as_float(__float_as_uint(y) | (__float_as_uint(w[j] + 0.0f) & 0x80000000u));
+      }
+    }
+    nan_g[g] = nan;
+    nan_any |= nan;
+  }
+  if (__builtin_amdgcn_ballot_w64(nan_any != 0) != 0) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (nan_g[c >> 2]) v[c][j] = __builtin_nanf("");
+  }
+}
+
+template <int QLV>
+__device__ __forceinline__ void q_frag_prep_lv(bf16x8 (&qf)[8], const AttnArgs& a) {
+  float v[8][8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[c][j] = static_cast<float>(qf[c][j]);
+  if (a.q_had) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      fwht_inlane_stage<1>(v[c]);
+      fwht_inlane_stage<2>(v[c]);
+      fwht_inlane_stage<4>(v[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) butterfly32_pair(v[c][j], v[c][j + 1]);
+#pragma unroll
+    for (int st = 1; st <= 4; st <<= 1) {
+      if (st == 4 && a.q_had != 128) break;
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (!(c & st))
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float l = v[c][j], h = v[c + st][j];
+            v[c][j] = l + h;
+            v[c + st][j] = l - h;
+          }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) div_sqrt_n(v[c], a.q_div);
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[c][j] = bf16_round_hw(v[c][j]);
+  if constexpr (QLV != 0) q_frag_qdq<QLV>(v);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) qf[c] = pack8<true>(v[c]);
+}
+
+__device__ __forceinline__ void q_frag_prep(bf16x8 (&qf)[8], const AttnArgs& a) {
+  if (a.q_levels == 123) q_frag_prep_lv<123>(qf, a);
+  else if (a.q_levels == 12) q_frag_prep_lv<12>(qf, a);
+  else if (a.q_levels == 13) q_frag_prep_lv<13>(qf, a);
+  else q_frag_prep_lv<0>(qf, a);
 }
 
 // Exponent argument of P = exp2(s c1 - m), m = the running maximum of RN(s c1) (log2 units).
@@ -614,6 +751,7 @@ void attn_fwd_kernel(AttnArgs a) {
   uint32_t* const pace_ctr = attn_pace + (a.pace_epoch % kPaceEpochs) * 8 + (wid & 7);
   if (pace && wid == 0 && tid < 8) attn_pace[((a.pace_epoch + 1) % kPaceEpochs) * 8 + tid] = 0u;
   uint32_t pace_seen = 0;  // lane 0 of wave 0: this XCD's tile count, loaded one tile ago
+
   bool issued = false;  // the DMA of the current item's first tile is in flight
 
   for (;;) {
@@ -667,6 +805,8 @@ void attn_fwd_kernel(AttnArgs a) {
           qf[c] = bf16x8{};
         }
       }
+      // the raw rows: Q's operand prologue here (q_frag_prep)
+      if (a.q_prep) q_frag_prep(qf, a);
     }
 
     floatx16 acc[4];
@@ -1051,18 +1191,21 @@ void attn_fwd_kernel(AttnArgs a) {
       }
 
     }
+    // bf16 rows through LDS: this wave's rows p0w .. p0w + 31, lane l takes 8 bytes (l % 32)
+    // of row 2 it + l / 32, two whole rows per instruction (output rows need only 8-byte
+    // alignment); each wave reads back only what it wrote, and the LDS wait orders its own
+    // accesses.  All reads come before the stores: an LDS read may alias the in-flight
+    // LDS-DMA of the next tile, so each one waits on the whole vector-memory counter, stores
+    // included.
+    const int piece = lane & 31;
+    uint2 rows_v[16];
     if (lds_out) {
-      // this wave's rows p0w .. p0w + 31: lane l takes 8 bytes (l % 32) of row 2 it + l / 32,
-      // two whole rows per instruction (output rows need only 8-byte alignment); each wave
-      // reads back only what it wrote, and the LDS wait orders its own accesses.  All reads
-      // come before the stores: an LDS read may alias the in-flight LDS-DMA of the next
-      // tile, so each one waits on the whole vector-memory counter, stores included.
-      uint16_t* const o16 = static_cast<uint16_t*>(a.o) + b * a.o_sb + hq * a.o_sh;
-      const int piece = lane & 31;
-      uint2 rows_v[16];
 #pragma unroll
       for (int it = 0; it < 16; ++it)
         rows_v[it] = *reinterpret_cast<const uint2*>(out_rows + (2 * it + (lane >> 5)) * kOutPitch + 4 * piece);
+    }
+    if (lds_out) {
+      uint16_t* const o16 = static_cast<uint16_t*>(a.o) + b * a.o_sb + hq * a.o_sh;
 #pragma unroll
       for (int it = 0; it < 16; ++it) {
         const int p = p0w + 2 * it + (lane >> 5);

@@ -353,18 +353,6 @@ __global__ __launch_bounds__(256) void unpack_rows_kernel(UnpackArgs a) {
 // cross-lane stages of stride 8 m for m = 1, 2, ... < n / 8, pairing lane l with l ^ m.
 // Each stage writes (left + right, left - right) with the left half at the lower
 // index, the order of rotation.py:21-28.
-template <int S>
-__device__ __forceinline__ void fwht_inlane_stage(float* v) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if ((i & S) == 0) {
-      const float l = v[i];
-      const float r = v[i + S];
-      v[i] = l + r;
-      v[i + S] = l - r;
-    }
-  }
-}
 
 // Cross-lane stage of stride 8 M: (left + right, left - right) with the left half at the
 // lower lane; the upper lane of a pair computes other - v as fma(-1, v, other), the lower
@@ -415,43 +403,6 @@ __device__ __forceinline__ void fwht8_lanes(float* v, int n) {
   if (n > 256) fwht_lane_stage<32>(v);
 }
 
-// Division by d = fp32(sqrt(n)) with the result of the IEEE division x / d (the reference
-// divides by math.sqrt(n), rotation.py:28).  For square n the divisor is a power of two
-// and x * (1/d) is exact.  Otherwise q = x r (r = fp32(1/d)), e = fma(-q, d, x) (the exact
-// remainder) and fma(e, r, q) equal x / d for every fp32 x whose exponent field lies in
-// [22, 254] (checked exhaustively for n = 2, 8, 32, 128, 512: tests/fp_div_check.c); a
-// lane holding a smaller magnitude (zeros included), an infinity or a NaN takes the IEEE
-// division for its 8 values.
-struct SqrtDiv {
-  float d;   // fp32(sqrt(n))
-  float r;   // fp32(1 / d)
-  int pow2;  // d is a power of two
-};
-
-__device__ __forceinline__ void div_sqrt_n(float* v, const SqrtDiv& s) {
-  if (s.pow2) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = v[i] * s.r;
-    return;
-  }
-  float y[8];
-  float lo = fabsf(v[0]), hi = fabsf(v[0]);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float q = v[i] * s.r;
-    const float e = __builtin_fmaf(-q, s.d, v[i]);
-    y[i] = __builtin_fmaf(e, s.r, q);
-    lo = fminf(lo, fabsf(v[i]));
-    hi = fmaxf(hi, fabsf(v[i]));
-  }
-  // exponent field >= 22 is |x| >= 2^-105; a NaN fails the comparisons
-  if (!(lo >= 0x1p-105f && hi <= 3.40282347e38f)) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = v[i] / s.d;
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = y[i];
-}
 
 struct HadamardRowsArgs {
   const void* x;

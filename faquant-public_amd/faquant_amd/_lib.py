@@ -45,6 +45,9 @@ class AttnOpts(ctypes.Structure):
         ("dm_sq", _c_i64),
         ("p_dump", _vp),
         ("p_dump_stride", _c_i64),
+        ("q_prep", _c_int),
+        ("q_hadamard", _c_int),
+        ("q_levels", _c_int),
     ]
 
 

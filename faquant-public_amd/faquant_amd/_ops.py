@@ -537,11 +537,26 @@ def dense_attention_mask(mask: torch.Tensor, batch: int, heads: int, query_lengt
     return out
 
 
+def raw_q_operand_ok(q: torch.Tensor, hadamard: int | None) -> bool:
+    """Whether attention_fwd's q_prep can take these query rows as they are: bf16 [B, H, L,
+    128] with unit stride along head_dim, strides of multiples of 8 elements, 16-byte
+    aligned, and a Hadamard block of 0, 64 or 128."""
+    return (q.dtype == torch.bfloat16 and q.ndim == 4 and q.shape[-1] == HEAD_DIM and q.stride(-1) == 1
+            and all(q.stride(i) % 8 == 0 for i in range(3)) and q.data_ptr() % 16 == 0
+            and int(hadamard or 0) in (0, 64, 128))
+
+
 def _attn_opts(ranges: KeyRanges | None, softcap: float | None, pv_probe: torch.Tensor | None = None,
-               dense_mask: torch.Tensor | None = None, p_dump: torch.Tensor | None = None):
-    if ranges is None and not softcap and pv_probe is None and dense_mask is None and p_dump is None:
+               dense_mask: torch.Tensor | None = None, p_dump: torch.Tensor | None = None,
+               q_prep: tuple[int, str | None] | None = None):
+    if (ranges is None and not softcap and pv_probe is None and dense_mask is None and p_dump is None
+            and q_prep is None):
         return None
     opts = _lib.AttnOpts()
+    if q_prep is not None:
+        opts.q_prep = 1
+        opts.q_hadamard = int(q_prep[0] or 0)
+        opts.q_levels = int(q_prep[1]) if q_prep[1] else 0
     opts.pv_probe = _lib.ptr(pv_probe)
     if p_dump is not None:
         opts.p_dump = p_dump.data_ptr()
@@ -580,6 +595,7 @@ def attention_fwd(
     pv_probe: torch.Tensor | None = None,
     dense_mask: torch.Tensor | None = None,
     p_dump: torch.Tensor | None = None,
+    q_prep: tuple[int, str | None] | None = None,
 ) -> torch.Tensor:
     """Attention over bf16 operands q [B, Hq, Lq, 128], k [B, Hkv, Lk, 128] and
     vt [B, Hkv, 128, Lpad]; writes ``out`` (a [B, Hq, Lq, 128] view, fp32 or bf16).
@@ -593,7 +609,11 @@ def attention_fwd(
     place of the causal rule (sfa:730-757).  ``p_dump`` (fp32 [B, Hq, Lq, 2, W], W a
     multiple of 4 and >= 128 * ceil(Lk / 128), needs ``quant_p``) receives the kernel's P
     and P^ for every key of every key tile a row processes (verification of the in-register
-    quantizer); it runs one pass."""
+    quantizer); it runs one pass.  ``q_prep = (hadamard, levels)`` takes the raw bf16 query
+    rows and applies ``operand_prep(q, levels=levels, hadamard=hadamard,
+    round_dtype=torch.bfloat16)``'s steps inside the kernel as each work item loads them
+    (hadamard 0, 64 or 128; levels None for no QDQ): the same bits without the separate pass
+    over Q."""
     _lib.require_device(q, k, vt, out, row_den)
     if softcap is not None and softcap < 0:
         raise ValueError("softcap must be non-negative")
@@ -626,7 +646,7 @@ def attention_fwd(
                 or not p_dump.is_contiguous() or width % 4 or width < _pad_keys(int(key_length))):
             raise ValueError("p_dump must be a contiguous fp32 [B, Hq, Lq, 2, W] tensor, W >= 128 * ceil(Lk / 128)")
         split = 1
-    held = _attn_opts(ranges, softcap, pv_probe, dense_mask, p_dump)
+    held = _attn_opts(ranges, softcap, pv_probe, dense_mask, p_dump, q_prep)
     opts = held[0] if held else None
     lib = _lib.load()
     B, Hq, Lq, D = q.shape

@@ -167,8 +167,14 @@ def attention_core(
     qk_group = _hif4_group(getattr(module, "faquant_qk_matmul_quant_kwargs", quant_kwargs), "QK") if qk_quant else 64
     pv_group = _hif4_group(getattr(module, "faquant_pv_matmul_quant_kwargs", quant_kwargs), "PV") if pv_quant else 64
     levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
-    q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None, hadamard=block,
-                                smooth=smooth_scale, round_dtype=torch.bfloat16)
+    q_levels = levels["q"] if qk_quant else None
+    # bf16 rows without Smooth-QK: the attention kernel applies Q's prologue as it loads them
+    q_prep = ((block or 0), q_levels) if smooth_scale is None and _ops.raw_q_operand_ok(query, block) else None
+    if q_prep is not None:
+        q_op = query
+    else:
+        q_op, _ = _ops.operand_prep(query, levels=q_levels, hadamard=block, smooth=smooth_scale,
+                                    round_dtype=torch.bfloat16)
     B, Hq, Lq, D = query.shape
     Lk = key.shape[2]
     scale = float(scaling if scaling is not None else D**-0.5)
@@ -181,7 +187,7 @@ def attention_core(
     k_prep = dict(hadamard=block, key_offset=key_offset, smooth=smooth_scale, smooth_divide=True,
                   round_dtype=torch.bfloat16)
     kv_operands_and_attend(module, q_op, key, value, query_length=Lq, qk_quant=qk_quant, pv_quant=pv_quant,
-                           levels=levels, k_prep=k_prep, causal=causal, scale=scale, quant_p=pv_quant,
+                           levels=levels, k_prep=k_prep, q_prep=q_prep, causal=causal, scale=scale, quant_p=pv_quant,
                            p_levels=levels["p"], norm_same=mode == "quantized_same", out=out.transpose(1, 2),
                            out_levels=_output_quant_levels(module), ranges=ranges)
     count_tiles(

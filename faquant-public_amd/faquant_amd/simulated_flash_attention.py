@@ -366,12 +366,22 @@ def _packed_operands(module, key: torch.Tensor, value: torch.Tensor, *, query_le
 
 
 def kv_operands_and_attend(module, q_op: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, query_length: int,
-                           qk_quant: bool, pv_quant: bool, levels, k_prep: dict, **attn) -> torch.Tensor:
+                           qk_quant: bool, pv_quant: bool, levels, k_prep: dict, q_prep=None, **attn) -> torch.Tensor:
     """K/V operands through the module's decode caches (sfa:243-289), then the attention
     kernel (``attn``: the keyword arguments of _ops.attention_fwd).  With packed caches the
     calls that attention_fwd runs on the decode kernel (decode-shaped, no mask beyond the
     causal rule) run on the packed rows; any other call takes bf16 operands of the same
-    values, so both cache forms give the same bits."""
+    values, so both cache forms give the same bits.  ``q_prep = (hadamard, levels)``: q_op
+    holds the raw bf16 query rows, prepared inside the attention kernel (its q_prep) or, for
+    the decode kernel, by operand_prep first; the same bits either way."""
+    if q_prep is not None:
+        attn = dict(attn, q_prep=q_prep)
+
+    def prepared_q():
+        if q_prep is None:
+            return q_op
+        return _ops.operand_prep(q_op, levels=q_prep[1], hadamard=q_prep[0], round_dtype=torch.bfloat16)[0]
+
     key_length = key.shape[2]
     B, Hq, Hkv = q_op.shape[0], q_op.shape[1], key.shape[1]
     plain = not (attn.get("ranges") is not None or attn.get("softcap") or attn.get("pv_probe") is not None
@@ -385,14 +395,14 @@ def kv_operands_and_attend(module, q_op: torch.Tensor, key: torch.Tensor, value:
     if _packed_cache_enabled(module, qk_quant, pv_quant):
         kp, vp = _packed_operands(module, key, value, query_length=query_length, levels=levels, prep=k_prep)
         if decode:
-            return _ops.attention_decode(q_op, key_length, packed=(kp, vp), **dkw)
+            return _ops.attention_decode(prepared_q(), key_length, packed=(kp, vp), **dkw)
         k_op, _ = _ops.operand_prep(key, levels=levels["k"], **k_prep)
         vt = _ops.operand_prep_vt(value, levels=levels["v"])
         return _ops.attention_fwd(q_op, k_op, vt, key_length, **attn)
     k_op = _key_operand(module, key, enabled=qk_quant, query_length=query_length, levels=levels["k"], **k_prep)
     v_op = _value_operand(module, value, enabled=pv_quant, query_length=query_length, levels=levels["v"])
     if decode:
-        return _ops.attention_decode(q_op, key_length, k=k_op, v=v_op, **dkw)
+        return _ops.attention_decode(prepared_q(), key_length, k=k_op, v=v_op, **dkw)
     return _ops.attention_fwd(q_op, k_op, transposed_values(v_op), key_length, **attn)
 
 
@@ -490,7 +500,10 @@ def simulated_flash_attention_forward(
     collect = pv_quant and isinstance(diagnostics, dict)
 
     levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
-    q_op, _ = _ops.operand_prep(query, levels=levels["q"] if qk_quant else None)
+    q_levels = levels["q"] if qk_quant else None
+    # bf16 rows: the attention kernel applies Q's QDQ as it loads them
+    q_prep = (0, q_levels) if _ops.raw_q_operand_ok(query, 0) else None
+    q_op = query if q_prep is not None else _ops.operand_prep(query, levels=q_levels)[0]
 
     dense = None
     if attention_mask is not None and attention_mask.ndim in (3, 4):
@@ -506,7 +519,7 @@ def simulated_flash_attention_forward(
              if collect else None)
     kv_operands_and_attend(
         module, q_op, key, value, query_length=query_length, qk_quant=qk_quant, pv_quant=pv_quant, levels=levels,
-        k_prep={}, causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
+        k_prep={}, q_prep=q_prep, causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
         norm_same=mode == "quantized_same", out=output.transpose(1, 2), ranges=ranges, softcap=softcap,
         pv_probe=probe, dense_mask=dense,
     )

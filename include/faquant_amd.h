@@ -270,6 +270,12 @@ typedef struct faq_attn_opts {
   int64_t dm_sb, dm_sh, dm_sq;
   float* p_dump;
   int64_t p_dump_stride;
+  /* q_prep = 1: q holds the raw bf16 query rows, and the kernel applies the operand
+     prologue of faq_operand_prep to them as it loads them (the per-block fp32 Hadamard of
+     q_hadamard = 0, 64 or 128 dims, one bf16 cast, the HiF4 QDQ with q_levels = 0 (none),
+     123, 12 or 13; no key offset or Smooth-QK): bit for bit the attention of the prepared
+     operand, without its separate pass over Q (qwen3.py:97-130) */
+  int q_prep, q_hadamard, q_levels;
 } faq_attn_opts;
 
 /*
