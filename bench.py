@@ -40,11 +40,11 @@ KERNEL_SOURCES = ("faquant-public_amd/csrc/hif4_attention.hip", "faquant-public_
                   "faquant-public_amd/csrc/hif4_device.h")
 MEASURED_TRAFFIC = {
     # config: (bytes per launch, kernel source sha256 prefix, profile)
-    "qwen8b_32k": (1.676e9, "9cbc55ea932e01e9", "profiles/attn_fwd_qwen8b_32k_counters.md"),
-    "qwen8b_8k": (2.141e8, "9cbc55ea932e01e9", "profiles/attn_fwd_qwen8b_8k_kernel_trace.md"),
-    "qwen32b_16k": (1.097e9, "9cbc55ea932e01e9", "profiles/attn_fwd_qwen32b_16k_kernel_trace.md"),
-    "wan480p": (3.367e9, "9cbc55ea932e01e9", "profiles/attn_fwd_wan480p_kernel_trace.md"),
-    "wan720p": (5.617e10, "9cbc55ea932e01e9", "profiles/attn_fwd_wan720p_kernel_trace.md"),
+    "qwen8b_32k": (1.675e9, "00a76ba3d16761b7", "profiles/attn_fwd_qwen8b_32k_counters.md"),
+    "qwen8b_8k": (2.159e8, "00a76ba3d16761b7", "profiles/attn_fwd_qwen8b_8k_kernel_trace.md"),
+    "qwen32b_16k": (1.099e9, "00a76ba3d16761b7", "profiles/attn_fwd_qwen32b_16k_kernel_trace.md"),
+    "wan480p": (3.367e9, "00a76ba3d16761b7", "profiles/attn_fwd_wan480p_kernel_trace.md"),
+    "wan720p": (1.873e10, "00a76ba3d16761b7", "profiles/attn_fwd_wan720p_kernel_trace.md"),
 }
 
 
