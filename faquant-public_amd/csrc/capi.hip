@@ -75,7 +75,8 @@ void launch_act(const faq::ActQdqArgs& a, int levels, int64_t threads, hipStream
 template <typename T, int R, int NT, bool G>
 void launch_act_row_g(const faq::ActRowArgs& a, int levels, size_t lds, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.rows));
-  if (levels == 12) hipLaunchKernelGGL((faq::act_row_kernel<T, 12, R, NT, G>), grid, dim3(NT), lds, st, a);
+  if (a.stage_round) hipLaunchKernelGGL((faq::act_row_kernel<T, 123, R, NT, G, true>), grid, dim3(NT), lds, st, a);
+  else if (levels == 12) hipLaunchKernelGGL((faq::act_row_kernel<T, 12, R, NT, G>), grid, dim3(NT), lds, st, a);
   else if (levels == 13) hipLaunchKernelGGL((faq::act_row_kernel<T, 13, R, NT, G>), grid, dim3(NT), lds, st, a);
   else hipLaunchKernelGGL((faq::act_row_kernel<T, 123, R, NT, G>), grid, dim3(NT), lds, st, a);
 }
@@ -566,6 +567,9 @@ int faq_act_prep_rows(const void* x, void* y, int64_t rows, int64_t cols, int dt
   a.act_max = o.act_max;
   a.compand = o.compand;
   a.compand_rcp = o.compand_rcp;
+  a.stage_round = o.stage_round != 0;
+  if (a.stage_round && (levels != 0 || o.col_scale || o.rot_signs || o.has_min || o.has_max || o.compand))
+    return fail(FAQ_EUNSUP, "%s: the in-dtype transform (stage_round) takes no other step", who);
   a.n = online;
   a.gen12 = gen12;
   a.div = sqrt_div(gen12 ? static_cast<int>(cols) : online);

@@ -534,6 +534,8 @@ struct ActRowArgs {
   float act_min, act_max;   // clamp bounds (rounded to T in the kernel)
   const float* compand;     // [cols] companding scale (values of T), or null
   const float* compand_rcp; // [cols] fp32(1 / compand) where the product form is exact, else 0; or null
+  int stage_round;          // 1: the online transform in T (every butterfly stage and the 12-point
+                            // mix rounded to T, as torch runs it on a T tensor)
   int n;                    // 0, or the online block Hadamard size (with gen12: cols / 12)
   int gen12;                // 1: the generalized transform of a row of 12 n values
   SqrtDiv div;              // division by fp32(sqrt(n)) (with gen12: of the row length)
@@ -561,7 +563,7 @@ __device__ __forceinline__ int act_c0(int tid, int r) {
 
 // Butterflies (left + right, left - right) of the stages of stride 1 .. S (S = 1, 2 or 4)
 // on each lane's chunks (their pairs lie inside one chunk).
-template <int R, int S>
+template <int R, int S, typename RT = float>
 __device__ __forceinline__ void fwht_in_chunks(float (&v)[R][8]) {
 #pragma unroll
   for (int s = 1; s <= S; s <<= 1)
@@ -571,8 +573,8 @@ __device__ __forceinline__ void fwht_in_chunks(float (&v)[R][8]) {
       for (int i = 0; i < 8; ++i)
         if (!(i & s)) {
           const float l = v[r][i], h = v[r][i + s];
-          v[r][i] = l + h;
-          v[r][i + s] = l - h;
+          v[r][i] = Io<RT>::round(l + h);
+          v[r][i + s] = Io<RT>::round(l - h);
         }
 }
 
@@ -582,7 +584,7 @@ constexpr int kActRadix = 4;
 
 // One pass over the LDS row of the LR stages of stride s, 2 s, .. (LR = 1 .. 4; s a
 // multiple of 8, 2^LR s dividing the block): group g holds the 2^LR values j0 + m s.
-template <int LR, int NT>
+template <int LR, int NT, typename RT = float>
 __device__ __forceinline__ void fwht_lds_pass(float* lds, int cols, int ls, int tid) {
   constexpr int kRad = 1 << LR;
   const int s = 1 << ls;
@@ -598,8 +600,8 @@ __device__ __forceinline__ void fwht_lds_pass(float* lds, int cols, int ls, int 
       for (int m = 0; m < kRad; ++m)
         if (!(m & t)) {
           const float l = w[m], h = w[m + t];
-          w[m] = l + h;
-          w[m + t] = l - h;
+          w[m] = Io<RT>::round(l + h);
+          w[m + t] = Io<RT>::round(l - h);
         }
 #pragma unroll
     for (int m = 0; m < kRad; ++m) lds[a0 + m * as] = w[m];
@@ -634,21 +636,21 @@ __device__ __forceinline__ void row_from_lds(float (&v)[R][8], const float* lds,
 // strides in passes over LDS of up to kActRadix stages (s, 2 s, 4 s, ..) on the values
 // j0 + m s read into registers: the same additions as one stage at a time.  Ends with the
 // transformed row in v.
-template <int R, int NT>
+template <int R, int NT, typename RT = float>
 __device__ __forceinline__ void fwht_row_raw(float (&v)[R][8], float* lds, int cols, int b, int tid) {
-  if (b == 2) fwht_in_chunks<R, 1>(v);
-  else if (b == 4) fwht_in_chunks<R, 2>(v);
-  else fwht_in_chunks<R, 4>(v);
+  if (b == 2) fwht_in_chunks<R, 1, RT>(v);
+  else if (b == 4) fwht_in_chunks<R, 2, RT>(v);
+  else fwht_in_chunks<R, 4, RT>(v);
   if (b > 8) {
     row_to_lds<R, NT>(v, lds, cols, tid);
     const int lb = __builtin_ctz(b);
     for (int ls = 3; ls < lb; ls += kActRadix) {
       __syncthreads();
       const int lr = min(kActRadix, lb - ls);
-      if (lr == 4) fwht_lds_pass<4, NT>(lds, cols, ls, tid);
-      else if (lr == 3) fwht_lds_pass<3, NT>(lds, cols, ls, tid);
-      else if (lr == 2) fwht_lds_pass<2, NT>(lds, cols, ls, tid);
-      else fwht_lds_pass<1, NT>(lds, cols, ls, tid);
+      if (lr == 4) fwht_lds_pass<4, NT, RT>(lds, cols, ls, tid);
+      else if (lr == 3) fwht_lds_pass<3, NT, RT>(lds, cols, ls, tid);
+      else if (lr == 2) fwht_lds_pass<2, NT, RT>(lds, cols, ls, tid);
+      else fwht_lds_pass<1, NT, RT>(lds, cols, ls, tid);
     }
     __syncthreads();
     row_from_lds<R, NT>(v, lds, cols, tid);
@@ -659,9 +661,9 @@ __device__ __forceinline__ void fwht_row_raw(float (&v)[R][8], float* lds, int c
 
 // The normalized transform of every b-block: fwht_row_raw, then the division by
 // fp32(sqrt(b)) (b a power of two: the fma form equals the IEEE division on its range).
-template <int R, int NT>
+template <int R, int NT, typename RT = float>
 __device__ __forceinline__ void fwht_row(float (&v)[R][8], float* lds, int cols, int b, const SqrtDiv& dv, int tid) {
-  fwht_row_raw<R, NT>(v, lds, cols, b, tid);
+  fwht_row_raw<R, NT, RT>(v, lds, cols, b, tid);
 #pragma unroll
   for (int r = 0; r < R; ++r) div_sqrt_n(v[r], dv);
 }
@@ -675,10 +677,13 @@ constexpr uint16_t kH12NegMask[12] = {0xFFE, 0x474, 0x8E8, 0x1D2, 0x3A4, 0x748,
 // of two): the reference pairs elements 2i, 2i + 1 and concatenates sums before differences,
 // which is the unnormalized FWHT of every b-block; then out[r b + c] = sum_h H12[r][h]
 // W[h b + c], accumulated in h order from 0 as the matmul does (each step one rounding), then
-// the IEEE division by fp32(sqrt(n)) (the fma form is not exact for these divisors).
-template <int R, int NT>
+// the IEEE division by fp32(sqrt(n)) (the fma form is not exact for these divisors).  With
+// RT = T (the transform on a T tensor) every stage and the mix's fp32 sum are rounded to T
+// (torch's T matmul accumulates in fp32 and rounds once; the 12 terms of +-1 times T values
+// sum exactly in fp32 unless their exponents span more than 16 binades).
+template <int R, int NT, typename RT = float>
 __device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, int cols, int b, float d, int tid) {
-  fwht_row_raw<R, NT>(v, lds, cols, b, tid);
+  fwht_row_raw<R, NT, RT>(v, lds, cols, b, tid);
   row_to_lds<R, NT>(v, lds, cols, tid);
   __syncthreads();
   for (int c = tid; c < b; c += NT) {
@@ -690,7 +695,7 @@ __device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, in
       float acc = 0.0f;
 #pragma unroll
       for (int h = 0; h < 12; ++h) acc = __builtin_fmaf((kH12NegMask[r] >> h) & 1u ? -1.0f : 1.0f, w[h], acc);
-      lds[lds_pad(r * b + c)] = acc;
+      lds[lds_pad(r * b + c)] = Io<RT>::round(acc);
     }
   }
   __syncthreads();
@@ -729,7 +734,9 @@ __global__ __launch_bounds__(256) void compand_rcp_kernel(const float* c, float*
 // With R <= 2 the kernel asks for 8 waves per SIMD (at most 64 VGPRs): two 1024-thread or
 // eight 256-thread workgroups per CU (at 67 VGPRs one fewer fits, and a 12288-feature row
 // with a 1024-block rotation took 126 instead of 103 us).
-template <typename T, int LV, int R, int NT, bool kGen12>
+// kStage: the online transform in T (ActRowArgs::stage_round), its own instance (the
+// roundings cost registers) for the standalone transforms, which quantize nothing.
+template <typename T, int LV, int R, int NT, bool kGen12, bool kStage = false>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 8 : 1))) void act_row_kernel(
     ActRowArgs a) {
   extern __shared__ float act_row_lds[];
@@ -807,8 +814,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 8 :
   }
   if (a.n) {
     // the generalized form is its own instance: its 12-point mix costs registers
-    if constexpr (kGen12) generalized_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div.d, tid);
-    else fwht_row<R, NT>(v, act_row_lds, a.cols, a.n, a.div, tid);
+    using RT = typename std::conditional<kStage, T, float>::type;
+    if constexpr (kGen12) generalized_row<R, NT, RT>(v, act_row_lds, a.cols, a.n, a.div.d, tid);
+    else fwht_row<R, NT, RT>(v, act_row_lds, a.cols, a.n, a.div, tid);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll

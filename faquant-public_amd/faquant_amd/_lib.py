@@ -79,6 +79,7 @@ class ActOpts(ctypes.Structure):
         ("hadamard", _c_int),
         ("hadamard_generalized", _c_int),
         ("compand_rcp", _vp),
+        ("stage_round", _c_int),
     ]
 
 

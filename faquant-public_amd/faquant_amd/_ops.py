@@ -155,6 +155,7 @@ def act_prep_rows(
     hadamard_generalized: bool = False,
     out: torch.Tensor | None = None,
     compand_rcp: torch.Tensor | None = None,
+    stage_round: bool = False,
 ) -> torch.Tensor:
     """The full activation path of a quantized Linear along the last axis of ``x``
     (faq_act_prep_rows): x * dtype(col_scale); the HiSQ input rotation (fp32 x times
@@ -164,7 +165,9 @@ def act_prep_rows(
     with ``hadamard_generalized`` the generalized transform of the whole row (rotation.py:
     53-69: a power of two or 12 times one); HiF4 QDQ with ``levels``; x / ``compand``.
     Output in x's dtype.  ``compand_rcp`` is ``act_compand_rcp(compand, x.dtype)``, computed
-    here when not given (callers that keep the scale keep it too)."""
+    here when not given (callers that keep the scale keep it too).  ``stage_round`` runs the
+    online transform in x's dtype (each butterfly stage and the 12-point mix rounded to it,
+    as the reference's transforms on a bf16 / fp16 tensor)."""
     _lib.require_device(x, col_scale, rot_signs, rot_perm, compand, compand_rcp)
     lib = _lib.load()
     if x.ndim == 0:
@@ -203,6 +206,7 @@ def act_prep_rows(
         hadamard=int(hadamard or 0),
         hadamard_generalized=int(bool(hadamard_generalized)),
         compand_rcp=vec(compand_rcp, torch.float32, "companding reciprocal") if compand is not None else None,
+        stage_round=int(bool(stage_round)),
     )
     _lib.check(
         lib.faq_act_prep_rows(

@@ -23,8 +23,8 @@ def _is_power_of_two(value: int) -> bool:
 def hadamard_transform(x: torch.Tensor) -> torch.Tensor:
     """Normalized Walsh-Hadamard transform over the final axis, computed in ``x.dtype`` as
     the reference's butterflies are (rotation.py:14-29): fp32 exactly, bf16 / fp16 with
-    every stage rounded to that dtype.  Sizes up to 512 (the head_dim and Linear-block
-    range of the hot path)."""
+    every stage rounded to that dtype.  Sizes up to 512 on the Hadamard kernels, larger ones
+    (a multiple of 64, up to 32768) on the activation row kernel."""
     size = x.shape[-1]
     if not _is_power_of_two(size):
         raise ValueError(f"Hadamard dimension must be a power of two, got {size}")
@@ -33,6 +33,8 @@ def hadamard_transform(x: torch.Tensor) -> torch.Tensor:
             return _row_path(x, hadamard=size)
         return _ops.hadamard_rows(x, size, torch.float32)
     if x.dtype in (torch.bfloat16, torch.float16):
+        if size > 512:
+            return _row_path(x, hadamard=size, stage_round=True)
         return _ops.hadamard_rows_native(x)
     raise NotImplementedError(f"hadamard_transform on the MI355X takes fp32, bf16 or fp16 input, got {x.dtype}")
 
@@ -65,16 +67,17 @@ def _row_path(x: torch.Tensor, **kw) -> torch.Tensor:
 
 def generalized_hadamard_transform(x: torch.Tensor) -> torch.Tensor:
     """Normalized Hadamard transform for power-of-two or 12 * power-of-two axes
-    (rotation.py:53-69).  The reference computes in x's dtype; this build takes fp32 input
-    (exact), and other dtypes through ``chunked_generalized_hadamard_transform``."""
+    (rotation.py:53-69), computed in x's dtype as the reference does: fp32 exactly; bf16 /
+    fp16 with every butterfly stage and the 12-point mix (a matmul accumulating in fp32)
+    rounded to that dtype, then the division rounded to it."""
     size = x.shape[-1]
     if _is_power_of_two(size):
         return hadamard_transform(x)
     if size % 12 or not _is_power_of_two(size // 12):
         raise ValueError(f"unsupported generalized Hadamard dimension: {size}")
-    if x.dtype != torch.float32:
-        raise NotImplementedError(f"generalized_hadamard_transform on the MI355X takes fp32 input, got {x.dtype}")
-    return _row_path(x, hadamard_generalized=True)
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"generalized_hadamard_transform takes fp32, bf16 or fp16 input, got {x.dtype}")
+    return _row_path(x, hadamard_generalized=True, stage_round=x.dtype != torch.float32)
 
 
 def chunked_generalized_hadamard_transform(x: torch.Tensor, *, chunk_rows: int = 256) -> torch.Tensor:

@@ -185,6 +185,10 @@ typedef struct faq_act_opts {
                                rotation.py:53-69); hadamard must then be 0 */
   const float* compand_rcp; /* optional, with compand: faq_act_compand_rcp of the companding
                                scale; the final x / compand is then a product where exact */
+  int stage_round;          /* 1: the online transform in the input dtype, as the reference's
+                               hadamard_transform / generalized_hadamard_transform run on a
+                               bf16 / fp16 tensor (rotation.py:14-69): every butterfly stage and
+                               the 12-point mix rounded to the dtype */
 } faq_act_opts;
 
 /*

@@ -81,7 +81,7 @@ def hadamard12() -> np.ndarray:
     return np.array([[(-1.0 if (m >> h) & 1 else 1.0) for h in range(12)] for m in H12_NEG_MASKS], dtype=_F32)
 
 
-def generalized_hadamard_transform(x: np.ndarray) -> np.ndarray:
+def generalized_hadamard_transform(x: np.ndarray, stage_round=None) -> np.ndarray:
     """``generalized_hadamard_transform`` (rotation.py:53-69) in float32 over the last axis.
 
     A power-of-two size is ``hadamard_transform``.  For n = 12 b (b a power of two) the
@@ -90,11 +90,16 @@ def generalized_hadamard_transform(x: np.ndarray) -> np.ndarray:
     order; then the 12 x 12 matrix mixes the blocks (out[r b + c] = sum_h H12[r, h] W[h b + c]),
     summed in h order from 0 as the CPU matmul does (an fma chain: each step one rounding),
     then a true division by fp32(sqrt(n)).
+
+    ``stage_round`` (e.g. ``hif4.bf16_round``) is the transform on a bf16 / fp16 tensor: each
+    butterfly stage rounded to the dtype, the matmul's fp32 sum rounded once to it, the
+    division computed in fp32 and rounded to it.
     """
     x = np.asarray(x, dtype=_F32)
+    rnd = stage_round if stage_round is not None else (lambda a: a)
     n = x.shape[-1]
     if _is_power_of_two(n):
-        return hadamard_transform(x)
+        return hadamard_transform(x, stage_round=stage_round)
     if n % 12 or not _is_power_of_two(n // 12):
         raise ValueError(f"unsupported generalized Hadamard dimension: {n}")
     b = n // 12
@@ -105,14 +110,15 @@ def generalized_hadamard_transform(x: np.ndarray) -> np.ndarray:
         left = v[:, :, 0, :]
         right = v[:, :, 1, :]
         w = np.concatenate(((left + right)[:, :, None, :], (left - right)[:, :, None, :]), axis=2)
-        w = w.reshape(-1, b).astype(_F32)
+        w = rnd(w.reshape(-1, b).astype(_F32))
         stride *= 2
     w = w.reshape(-1, 12, b)
     h12 = hadamard12()
     out = np.zeros_like(w)
     for h in range(12):
         out = (out + h12[None, :, h, None] * w[:, h : h + 1, :]).astype(_F32)
-    out = (out.reshape(x.shape) / _F32(math.sqrt(n))).astype(_F32)
+    out = rnd(out)
+    out = rnd((out.reshape(x.shape) / _F32(math.sqrt(n))).astype(_F32))
     return out
 
 

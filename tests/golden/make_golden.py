@@ -21,7 +21,9 @@ Fixtures (numpy .npz, float32 unless noted):
   attention.npz       simulated_flash_attention_forward with HiF4 Q/K/P/V at the
                       configuration shapes listed in CASES.
   hadamard_native.npz hadamard_transform on bf16 and fp16 tensors (the butterflies run
-                      in the tensor's dtype, each stage rounded), n = 8, 64, 128, 512.
+                      in the tensor's dtype, each stage rounded), n = 8, 64, 128, 512;
+                      as 16-bit patterns, n = 1024, 4096 (keys px_/ph_) and
+                      generalized_hadamard_transform, n = 192, 768, 3072, 12288 (gx_/gh_).
   linear_act.npz      the activation FakeQuantLinear.forward hands to F.linear (F.linear
                       replaced by the identity while it runs): input scale, HiSQ rotation
                       from derive_hisq_rotation with and without its block Hadamard,
@@ -217,6 +219,21 @@ def make_hadamard_native() -> dict[str, np.ndarray]:
             t = torch.from_numpy(x).to(dt)
             out[f"x_{name}_{n}"] = t.float().numpy()
             out[f"h_{name}_{n}"] = hadamard_transform(t).float().numpy()
+    # in the tensor's dtype above 512 (the activation row kernel's sizes) and the generalized
+    # transform of 12 * 2^k values (rotation.py:53-69: butterflies and the 12 x 12 matmul in
+    # the dtype, then the division), stored as 16-bit patterns
+    from faquant.rotation import generalized_hadamard_transform
+
+    g2 = inputs.rng(29)
+    for kind, sizes in (("p", ((1024, 4), (4096, 2))), ("g", ((192, 16), (768, 8), (3072, 4), (12288, 2)))):
+        for n, rows in sizes:
+            x = (g2.standard_normal((rows, n)) * g2.uniform(0.01, 100, size=(rows, 1))).astype(np.float32)
+            for name, dt in (("bf16", torch.bfloat16), ("fp16", torch.float16)):
+                t = torch.from_numpy(x).to(dt)
+                y = hadamard_transform(t) if kind == "p" else generalized_hadamard_transform(t)
+                assert y.dtype == dt
+                out[f"{kind}x_{name}_{n}"] = t.view(torch.int16).numpy().view(np.uint16)
+                out[f"{kind}h_{name}_{n}"] = y.view(torch.int16).numpy().view(np.uint16)
     return out
 
 

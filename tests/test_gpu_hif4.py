@@ -276,3 +276,32 @@ def test_empty_batches_return_empty(dev):
         assert fake_quantize_hif4(x, levels="123").shape == (0, 3, 128)
         assert _ops.act_qdq_rows(x, levels="123", hadamard=64).shape == (0, 3, 128)
     assert hadamard_transform(torch.empty((0, 64), device=dev)).shape == (0, 64)
+
+
+def _from_bits(u, dt):
+    if dt == "bf16":
+        return (u.astype(np.uint32) << 16).view(np.float32)
+    return u.view(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+def test_in_dtype_transforms_on_the_row_kernel_match_reference_goldens(dev, dt):
+    """rotation.hadamard_transform above 512 and rotation.generalized_hadamard_transform on
+    bf16 / fp16 tensors run in the tensor's dtype on the activation row kernel (every stage
+    and the 12-point mix rounded to it, faq_act_opts.stage_round): bitwise the reference's
+    vectors (tests/golden/hadamard_native.npz, keys p*/g*)."""
+    from faquant_amd.rotation import generalized_hadamard_transform, hadamard_transform
+    from tests.conftest import load_golden
+
+    g = load_golden("hadamard_native.npz")
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    for kind in ("p", "g"):
+        for k in sorted(k for k in g if k.startswith(f"{kind}x_{dt}_")):
+            n = k.rsplit("_", 1)[1]
+            x = to_dev(_from_bits(g[k], dt), dev, tdt)
+            fn = hadamard_transform if kind == "p" else generalized_hadamard_transform
+            print(f"[in-dtype] {kind} {dt} n={n}", flush=True)
+            got = fn(x)
+            assert got.dtype == tdt
+            np.testing.assert_array_equal(got.float().cpu().numpy().view(np.uint32),
+                                          _from_bits(g[f"{kind}h_{dt}_{n}"], dt).view(np.uint32))

@@ -88,3 +88,33 @@ def test_stage_rounded_transform_matches_reference_goldens(dt, n):
     # and the per-stage rounding matters: one rounding at the end differs somewhere
     once = rnd(OH.hadamard_transform(g[f"x_{dt}_{n}"]))
     assert not np.array_equal(once, g[f"h_{dt}_{n}"])
+
+
+def _from_bits(u, dt):
+    if dt == "bf16":
+        return (u.astype(np.uint32) << 16).view(np.float32)
+    return u.view(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+def test_in_dtype_transforms_match_reference_goldens(dt):
+    """hadamard_transform above 512 and generalized_hadamard_transform (12 * 2^k) on bf16 /
+    fp16 tensors, which the reference runs in the tensor's dtype (rotation.py:14-69: every
+    butterfly stage and the 12 x 12 matmul rounded to it, then the division): the oracle's
+    stage-rounded forms equal the reference's vectors bit for bit, and the fp32 forms do not
+    (the vectors tell the two apart)."""
+    from tests.conftest import load_golden
+
+    g = load_golden("hadamard_native.npz")
+    rnd = OQ.bf16_round if dt == "bf16" else OQ.fp16_round
+    for kind in ("p", "g"):
+        keys = sorted(k for k in g if k.startswith(f"{kind}x_{dt}_"))
+        assert keys
+        for k in keys:
+            n = k.rsplit("_", 1)[1]
+            x = _from_bits(g[k], dt)
+            want = _from_bits(g[f"{kind}h_{dt}_{n}"], dt)
+            fn = OH.hadamard_transform if kind == "p" else OH.generalized_hadamard_transform
+            got = fn(x, stage_round=rnd)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), k
+            assert not np.array_equal(rnd(fn(x)).view(np.uint32), want.view(np.uint32)), k
