@@ -39,6 +39,9 @@
 // one fma of the nibble with per-4-group constants (exact: at most six significant
 // bits), so the unpacked operands are bitwise the bf16 operands of the bf16 path and the
 // outputs are bitwise equal.  Both unpack per key row on their way into LDS.
+#include <cstdlib>
+#include <cstring>
+
 #include "attn_decode.h"
 #include "hif4_attention.hip"
 
@@ -361,6 +364,93 @@ void dec_scores_kernel(DecodeArgs a) {
         s[kb] = floatx16{};
 #pragma unroll
         for (int c = 0; c < 8; ++c) s[kb] = mfma32(lds_read_at(kp, 32 * c), qf[c], s[kb]);
+      }
+    }
+    if (key0 + kKeyTile > a.Lk || (a.causal && key0 + kKeyTile - 1 > w.pmin + off)) {
+      const int lim = a.causal ? min(a.Lk - 1, w.pos + off) : a.Lk - 1;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (key0 + 64 * half + 16 * kb + i > lim) s[kb][i] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+    if (w.live) {
+      float* sp = a.s + w.row * a.s_stride + key0 + 64 * half;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          *reinterpret_cast<float4*>(sp + 16 * kb + 4 * u) =
+              make_float4(s[kb][4 * u], s[kb][4 * u + 1], s[kb][4 * u + 2], s[kb][4 * u + 3]);
+      a.gmx[(w.row * a.ntiles + t) * 2 + half] = mx;
+    }
+    smax = fmaxf(smax, mx);
+  }
+  const float sm = halves_max(smax);
+  if (w.live && half == 0) a.smx[w.row * a.nsplit + w.j] = sm;
+}
+
+// Scores pass over packed rows without LDS: lane (n, half) unpacks the A operand of its MFMA
+// rows itself.  Key block kb's row n is key pi = krow0 + 16 kb of the tile (the prefill
+// layout above), and the lane's chunk c is dims 16 c + 8 half .. + 7 of that key: code word
+// 8 half + c (the lane's 32 code bytes are contiguous) unpacked with its 64-dim group's meta
+// word, exactly as store_rows unpacks it.  The loads go through buffer resources that end at
+// key Lk (rows past it read as zeros and are masked), and the MFMAs take the same operands
+// in the same order as the staged form, so the scores are bitwise equal.  Same-box decode
+// steps: 61.2 -> 60.3 us at 128k keys, 29.3 -> 28.0 us at 32k read from HBM.  (The same
+// form over bf16 rows was slower, 139 against 120 us at 128k: its 16-byte loads touch 32
+// rows each, where the staged form reads 1 KiB runs.)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void dec_scores_packed_direct_kernel(DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31;
+  const int half = lane >> 5;
+  const int wave_id = dec_wave_id();
+  if (wave_id >= a.B * a.Hkv * a.n_rb * a.nsplit) return;
+  const DecWave w = dec_wave(a, wave_id, n);
+  const int off = a.Lk - a.Lq;
+  const RowSrc ksrc = k_source<true>(a, w);
+
+  bf16x8 qf[8];
+  {
+    const uint16_t* qp = a.q + w.b * a.q_sb + w.hq * a.q_sh + static_cast<int64_t>(w.live ? w.pos : 0) * a.q_sl + 8 * half;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) qf[c] = w.live ? *reinterpret_cast<const bf16x8*>(qp + 16 * c) : bf16x8{};
+  }
+  const int krow0 = 64 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+  float smax = -INFINITY;
+  for (int t = w.t_lo; t < w.t_hi; ++t) {
+    const int key0 = t * kKeyTile;
+    floatx16 s[4];
+    {
+      const __amdgpu_buffer_rsrc_t rc = rows_rsrc(ksrc.base + static_cast<int64_t>(key0) * 64, a.Lk - key0, 64u);
+      const __amdgpu_buffer_rsrc_t rm = rows_rsrc(ksrc.meta + static_cast<int64_t>(key0) * 8, a.Lk - key0, 8u);
+      u32x4 cw[4][2];
+      uint32_t mw[4][2];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint32_t pi = static_cast<uint32_t>(krow0 + 16 * kb);
+        cw[kb][0] = __builtin_amdgcn_raw_buffer_load_b128(rc, pi * 64u + 32u * half, 0, 0);
+        cw[kb][1] = __builtin_amdgcn_raw_buffer_load_b128(rc, pi * 64u + 32u * half + 16u, 0, 0);
+        const auto mm = __builtin_amdgcn_raw_buffer_load_b64(rm, pi * 8u, 0, 0);
+        mw[kb][0] = mm[0];
+        mw[kb][1] = mm[1];
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const float s4[2] = {hif4_group_s4(mw[kb][0]), hif4_group_s4(mw[kb][1])};
+        s[kb] = floatx16{};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          float v[8];
+          hif4_unpack8(cw[kb][c >> 2][c & 3], s4[c >> 2], mw[kb][c >> 2], 2 * (c & 3) + half, v);
+          s[kb] = mfma32(pack8<true>(v), qf[c], s[kb]);
+        }
       }
     }
     if (key0 + kKeyTile > a.Lk || (a.causal && key0 + kKeyTile - 1 > w.pmin + off)) {
@@ -1245,7 +1335,11 @@ void launch_decode_fused(const DecodeArgs& a, int packed, int p_levels, uint32_t
 void launch_decode(const DecodeArgs& a, int packed, int quant_p, int p_levels, int norm_same, hipStream_t st) {
   const int64_t waves = static_cast<int64_t>(a.B) * a.Hkv * a.n_rb * a.nsplit;
   const dim3 grid(static_cast<unsigned>((waves + kDecWaves - 1) / kDecWaves));
-  if (packed) hipLaunchKernelGGL((dec_scores_kernel<true>), grid, dim3(256), 0, st, a);
+  // packed rows: the scores pass without LDS (test hook: FAQ_DEC_SCORES=lds stages them)
+  const char* sc_env = std::getenv("FAQ_DEC_SCORES");
+  const bool staged = sc_env && std::strcmp(sc_env, "lds") == 0;
+  if (packed && !staged) hipLaunchKernelGGL(dec_scores_packed_direct_kernel, grid, dim3(256), 0, st, a);
+  else if (packed) hipLaunchKernelGGL((dec_scores_kernel<true>), grid, dim3(256), 0, st, a);
   else hipLaunchKernelGGL((dec_scores_kernel<false>), grid, dim3(256), 0, st, a);
   const int lv = quant_p ? p_levels : 123;
   if (lv == 12) launch_values_lv<12>(a, packed, quant_p, norm_same, grid, st);

@@ -157,6 +157,31 @@ def test_decode_equals_split_path_bitwise(dev, case):
         assert_close_attention(dec_o.cpu().numpy(), ref, f"decode {case}", **TIGHT)
 
 
+@pytest.mark.parametrize("case", [DECODE_CASES[0], DECODE_CASES[2], DECODE_CASES[7], DECODE_CASES[8], DECODE_CASES[9]],
+                         ids=lambda c: "x".join(map(str, c[:5])) + f"_{c[9]}")
+def test_packed_scores_without_lds_equal_staged_scores(dev, case, monkeypatch):
+    """Packed K rows: the scores pass that unpacks each lane's A operand from HBM (the
+    default) gives the staged pass's output and row denominators bitwise (ragged last
+    tile, more ranges than tiles, one key, several positions)."""
+    from faquant_amd import _ops
+
+    B, Hq, Hkv, Lq, Lk, causal, mode, qp, lv, nsplit = case
+    (q, k, v), (qh, kh, vh, vt), kw = _decode_inputs(case, dev)
+    kc = _ops.pack_operand(to_dev(k, dev, torch.bfloat16), levels=lv, out=_ops.PackedHiF4KV(B, Hkv, Lk, dev, lv))
+    vc = _ops.pack_operand(to_dev(v, dev, torch.bfloat16), levels=lv, out=_ops.PackedHiF4KV(B, Hkv, Lk, dev, lv))
+    print(f"[scores] {case}", flush=True)
+    monkeypatch.setenv("FAQ_DECODE_FUSED", "0")
+    runs = {}
+    for form in ("direct", "lds"):
+        monkeypatch.delenv("FAQ_DEC_SCORES", raising=False)
+        if form == "lds":
+            monkeypatch.setenv("FAQ_DEC_SCORES", "lds")
+        runs[form] = _run(lambda **a: _ops.attention_decode(qh, Lk, packed=(kc, vc), split=nsplit, **kw, **a),
+                          case, dev)
+    assert torch.equal(runs["direct"][0], runs["lds"][0])
+    assert torch.equal(runs["direct"][1], runs["lds"][1])
+
+
 FUSED_CASES = [
     # decode steps the one-pass kernel takes (P quantized, quantized-same, G x positions <= 8,
     # one key tile per split, at most 64 tiles)
