@@ -232,14 +232,15 @@ def mfma_probe(dev) -> float:
     return blocks * 8 * iters * 4 * 32768 / (ms * 1e-3) / 1e12
 
 
-def decode_bench(cfg, context: int, steps: int, warmup: int, layers: int = 1) -> dict:
+def decode_bench(cfg, context: int, steps: int, warmup: int, layers: int = 1, ranges: int | None = None) -> dict:
     """One decode step (one new query position per head) of `cfg`'s heads over `context` cached
     keys, timed three ways with HIP events on the launch stream: the split-key path
     (faq_attention_fwd_split), the decode kernel over bf16 K/V and over packed HiF4 K/V.
     The roofline is HBM: algorithmic bytes = the K and V cache bytes one step must read
     (bf16: 512 per key and KV head, packed: 144) plus Q and the output.  With `layers` > 1 the
     steps cycle through that many independent caches (as a model's layers do), so that the
-    caches together exceed the 256 MB last-level cache and every step reads from HBM."""
+    caches together exceed the 256 MB last-level cache and every step reads from HBM.  `ranges`
+    replaces decode_split_count's number of key ranges for both decode-kernel paths."""
     import torch
 
     from faquant_amd import _ops
@@ -266,8 +267,8 @@ def decode_bench(cfg, context: int, steps: int, warmup: int, layers: int = 1) ->
     kw = dict(causal=True, scale=128**-0.5, quant_p=True, p_levels=lv, norm_same=True, out=out.transpose(1, 2))
     cus = _ops._device_cus(dev)
     n_split = _ops._split_count(B, Hq, Hkv, 1, L, cus)
-    n_dec = _ops.decode_split_count(B, Hkv, L, cus)
-    n_dec_packed = _ops.decode_split_count(B, Hkv, L, cus, packed=True)
+    n_dec = _ops.decode_split_count(B, Hkv, L, cus) if ranges is None else ranges
+    n_dec_packed = _ops.decode_split_count(B, Hkv, L, cus, packed=True) if ranges is None else ranges
     turn = [0]
 
     def layer():
@@ -514,6 +515,8 @@ def main():
     ap.add_argument("--decode-layers", type=int, default=1, metavar="N",
                     help="with --decode: cycle the steps through N independent K/V caches (N x the cache bytes "
                          "beyond the 256 MB last-level cache makes every step read HBM)")
+    ap.add_argument("--decode-ranges", type=int, default=None, metavar="N",
+                    help="with --decode: N key ranges for the decode kernel (default: decode_split_count)")
     ap.add_argument("--linear", type=int, default=0, metavar="TOKENS",
                     help="time the HiF4 W4A4 Linear at the Wan2.2 DiT block shapes over TOKENS rows instead")
     ap.add_argument("--linear-prep", type=int, default=0, metavar="TOKENS",
@@ -547,7 +550,8 @@ def main():
         return
 
     if args.decode:
-        print(json.dumps(decode_bench(CONFIGS[args.config], args.decode, args.steps, warmup, args.decode_layers)),
+        print(json.dumps(decode_bench(CONFIGS[args.config], args.decode, args.steps, warmup, args.decode_layers,
+                                      args.decode_ranges)),
               flush=True)
         return
 
