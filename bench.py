@@ -394,6 +394,92 @@ def linear_bench(tokens: int, steps: int, warmup: int) -> dict:
 QWEN8B_LINEAR_INPUTS = (("q/k/v/o_proj, gate/up_proj", 4096), ("down_proj", 12288))
 
 
+# Qwen3-8B projection shapes (out_features, in_features) of one decoder layer
+QWEN8B_PROJECTIONS = (("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096),
+                      ("o_proj", 4096, 4096), ("gate_proj", 12288, 4096), ("up_proj", 12288, 4096),
+                      ("down_proj", 4096, 12288))
+
+
+def linear_decode_bench(rows: int, steps: int, warmup: int, layers: int = 4) -> dict:
+    """The HiF4 W4A4 Linear's contraction at the Qwen3-8B projection shapes over `rows` input
+    rows (decode steps, small batches): F.linear on the bf16 weight QDQ (the drop-in's path,
+    hipBLASLt) against faq_hif4_linear_packed on the packed weight (4.5 bits per weight).  Each
+    timed sequence runs the seven projections of `layers` layers (distinct weights, so that
+    every call reads its weight from HBM: 4 layers hold 436 MB packed, 1.55 GB bf16), captured
+    in a HIP graph and replayed, so that host launch time does not enter; HIP events around
+    `steps` replays.  Roofline: HBM, algorithmic bytes = the weight (2 or 0.5625 bytes per
+    weight) plus x and y."""
+    import torch
+
+    from faquant_amd import _ops
+    from faquant_amd.quantization import fake_quantize
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(5)
+    shapes = QWEN8B_PROJECTIONS
+    bf = [[None] * len(shapes) for _ in range(layers)]
+    pk = [[None] * len(shapes) for _ in range(layers)]
+    xs = {}
+    for li in range(layers):
+        for si, (_, n, k) in enumerate(shapes):
+            w = (torch.randn((n, k), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+            pk[li][si] = _ops.PackedHiF4Weight(w, "123")
+            bf[li][si] = fake_quantize(w, quant_format="hif4", bits=4, group_size=64, hif4_levels="123")
+            xs.setdefault(k, _ops.act_qdq_rows(torch.randn((rows, k), device=dev, generator=gen).to(torch.bfloat16),
+                                              levels="123"))
+            del w
+
+    def seq_bf16():
+        for li in range(layers):
+            for si, (_, n, k) in enumerate(shapes):
+                torch.nn.functional.linear(xs[k], bf[li][si])
+
+    def seq_packed():
+        for li in range(layers):
+            for si, (_, n, k) in enumerate(shapes):
+                _ops.linear_packed(xs[k], pk[li][si])
+
+    def timed(fn):
+        for _ in range(2):
+            fn()  # buffers (the packed path's counters and workspace) exist before capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1000 / steps / layers  # us per layer (seven projections)
+
+    us_bf16, us_packed = timed(seq_bf16), timed(seq_packed)
+    w_elems = sum(n * k for _, n, k in shapes)
+    io = sum(rows * (k + n) * 2 for _, n, k in shapes)
+    out = {
+        "metric": "HiF4 W4A4 Linear decode contraction: one Qwen3-8B layer's seven projections, 1 GPU",
+        "unit": "us per layer",
+        "higher_is_better": False,
+        "rows": rows,
+        "layers_rotated": layers,
+        "steps": steps,
+        "warmup": warmup,
+        "data": "synthetic",
+        "paths": {
+            "f_linear_bf16_weight": {"us": round(us_bf16, 2), "bytes": w_elems * 2 + io,
+                                     "hbm_frac": round((w_elems * 2 + io) / (us_bf16 * 1e-6) / 8e12, 4)},
+            "packed_hif4_weight": {"us": round(us_packed, 2), "bytes": w_elems * 9 // 16 + io,
+                                   "hbm_frac": round((w_elems * 9 // 16 + io) / (us_packed * 1e-6) / 8e12, 4)},
+        },
+        "speedup": round(us_bf16 / us_packed, 3),
+    }
+    return out
+
+
 def linear_prep_bench(tokens: int, steps: int, warmup: int) -> dict:
     """The quantized Linear's activation path over `tokens` bf16 rows at the Qwen3-8B input
     widths: the fused prologue without extras (act_qdq_rows: HiF4 QDQ only), the full path
@@ -519,6 +605,9 @@ def main():
                     help="with --decode: N key ranges for the decode kernel (default: decode_split_count)")
     ap.add_argument("--linear", type=int, default=0, metavar="TOKENS",
                     help="time the HiF4 W4A4 Linear at the Wan2.2 DiT block shapes over TOKENS rows instead")
+    ap.add_argument("--linear-decode", type=int, default=0, metavar="ROWS",
+                    help="time the HiF4 W4A4 Linear's contraction at the Qwen3-8B projection shapes over ROWS "
+                         "input rows: F.linear on bf16 weights against the packed-weight kernel")
     ap.add_argument("--linear-prep", type=int, default=0, metavar="TOKENS",
                     help="time the quantized Linear's activation path (HiSQ rotation, clamp, companding) "
                          "at the Qwen3-8B input widths over TOKENS rows instead")
@@ -543,6 +632,10 @@ def main():
 
     if args.linear_prep:
         print(json.dumps(linear_prep_bench(args.linear_prep, args.steps, warmup)), flush=True)
+        return
+
+    if args.linear_decode:
+        print(json.dumps(linear_decode_bench(args.linear_decode, args.steps, warmup)), flush=True)
         return
 
     if args.stream_reference:

@@ -13,6 +13,7 @@
 #include "../../include/faquant_amd.h"
 #include "attn_aux.hip"
 #include "attn_decode.h"
+#include "hif4_linear.h"
 #include "hif4_attention.hip"
 #include "hif4_quant.hip"
 #include "mfma_probe.hip"
@@ -986,6 +987,52 @@ int faq_pquant_groups(const float* p, float* p_hat, int64_t groups, int levels, 
   else if (levels == 12) hipLaunchKernelGGL(faq::pquant_groups_kernel<12>, grid, dim3(256), 0, st, p, p_hat, groups);
   else hipLaunchKernelGGL(faq::pquant_groups_kernel<13>, grid, dim3(256), 0, st, p, p_hat, groups);
   return check_launch("faq_pquant_groups");
+}
+
+int faq_hif4_linear_packed(const uint16_t* x, int64_t x_sm, const uint32_t* w_codes, const uint32_t* w_meta,
+                           const void* bias, int bias_dtype, void* y, int y_dtype, int64_t y_sm, int M, int N, int K,
+                           faq_stream_t stream) {
+  const char* who = "faq_hif4_linear_packed";
+  if (M < 0 || N < 1 || K < 1) return fail(FAQ_EINVAL, "%s: bad sizes", who);
+  if (K % 128) return fail(FAQ_EUNSUP, "%s: in_features must be a multiple of 128, got %d", who, K);
+  if (M > faq::kLinMaxRows) return fail(FAQ_EUNSUP, "%s: at most %d rows of x, got %d", who, faq::kLinMaxRows, M);
+  if (M == 0) return FAQ_OK;
+  if (!x || !w_codes || !w_meta || !y) return fail(FAQ_EINVAL, "%s: null operand", who);
+  if (y_dtype != FAQ_F32 && y_dtype != FAQ_BF16) return fail(FAQ_EUNSUP, "%s: output must be fp32 or bf16", who);
+  if (bias && bias_dtype != FAQ_F32 && bias_dtype != FAQ_BF16)
+    return fail(FAQ_EUNSUP, "%s: bias must be fp32 or bf16", who);
+  if (!aligned16(x) || x_sm < K || x_sm % 8)
+    return fail(FAQ_EINVAL, "%s: x must be 16-byte aligned with a row stride >= K, a multiple of 8", who);
+  if (!aligned16(w_codes) || (reinterpret_cast<uintptr_t>(w_meta) & 7u))
+    return fail(FAQ_EINVAL, "%s: packed codes must be 16-byte and meta 8-byte aligned", who);
+  if (y_sm < N || (reinterpret_cast<uintptr_t>(y) & (y_dtype == FAQ_F32 ? 3u : 1u)))
+    return fail(FAQ_EINVAL, "%s: y must be aligned to its dtype with a row stride >= N", who);
+  if (static_cast<int64_t>(N) * (K / 128) > (int64_t(1) << 40)) return fail(FAQ_EUNSUP, "%s: weight too large", who);
+  faq::LinArgs a{};
+  a.x = x;
+  a.x_sm = x_sm;
+  a.wc = w_codes;
+  a.wm = w_meta;
+  a.bias = bias;
+  a.bias_f32 = bias_dtype == FAQ_F32;
+  a.y = y;
+  a.y_f32 = y_dtype == FAQ_F32;
+  a.y_sm = y_sm;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.nkb = K / 128;
+  // output features per wave: two waves per SIMD or more; per-call A/B at the Qwen3-8B shapes
+  // (kernel traces): with one or two rows of x, two features per wave from N = 4096 up (gate /
+  // up_proj 9.9 against 11.5 us with four); with more rows, four from N = 8192 up (16.7 against
+  // 18.8 us) and two below
+  int rows_per_wave = M <= 2 ? (N >= 4096 ? 2 : 1) : (N >= 8192 ? 4 : 2);
+  if (const char* e = std::getenv("FAQ_LIN_RPW")) {  // test hook: 1, 2 or 4 output features per wave
+    const int r = std::atoi(e);
+    if (r == 1 || r == 2 || r == 4) rows_per_wave = r;
+  }
+  faq::launch_linear_packed(a, rows_per_wave, static_cast<hipStream_t>(stream));
+  return check_launch(who);
 }
 
 int faq_mfma_probe(float* out, int blocks, int iters, faq_stream_t stream) {

@@ -129,6 +129,10 @@ _SIGNATURES = {
         ],
         _c_int,
     ),
+    "faq_hif4_linear_packed": (
+        [_vp, _c_i64, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _vp],
+        _c_int,
+    ),
     "faq_attention_split_workspace": ([_c_int, _c_int, _c_int, _c_int, _c_int], _c_i64),
     "faq_mfma_probe": ([_vp, _c_int, _c_int, _vp], _c_int),
     "faq_stream_probe": ([_vp, _c_i64, _vp, _c_int, _vp], _c_int),

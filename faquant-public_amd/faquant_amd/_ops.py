@@ -420,6 +420,69 @@ def pack_operand(
     return out
 
 
+class PackedHiF4Weight:
+    """A Linear weight W [N, K] kept as packed HiF4 rows (4.5 bits per weight) for
+    ``linear_packed``: row n * (K / 128) + j of ``rows`` (a PackedHiF4KV of one batch and head)
+    holds columns 128 j .. 128 j + 127 of output feature n.  Packed from the weight before its
+    QDQ (``pack_operand`` with the weight's levels), so it decodes to the HiF4 weight QDQ of
+    FakeQuantLinear (quantization.py:164-191) bitwise; packing an already quantized weight
+    would not (a second QDQ can pick a finer E6M2 scale)."""
+
+    def __init__(self, weight: torch.Tensor, levels: str) -> None:
+        _lib.require_device(weight)
+        if weight.ndim != 2 or weight.shape[1] % HEAD_DIM:
+            raise NotImplementedError("packed HiF4 weights need [out_features, in_features] with in_features a "
+                                      "multiple of 128")
+        N, K = weight.shape
+        self.shape = (N, K)
+        self.levels = levels
+        self.rows = PackedHiF4KV(1, 1, N * (K // HEAD_DIM), weight.device, levels)
+        w = weight.detach().contiguous()
+        pack_operand(w.view(1, 1, N * (K // HEAD_DIM), HEAD_DIM), levels=levels, out=self.rows, round_dtype=w.dtype)
+
+    @property
+    def device(self) -> torch.device:
+        return self.rows.device
+
+    def nbytes(self) -> int:
+        return self.rows.nbytes()
+
+
+LINEAR_PACKED_MAX_ROWS = 8  # faq_hif4_linear_packed takes at most this many rows of x
+
+
+def linear_packed(x: torch.Tensor, weight: PackedHiF4Weight, bias: torch.Tensor | None = None, *,
+                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """y = x W^T (+ bias) with W packed (faq_hif4_linear_packed): x bf16 [..., K] (the HiF4
+    activation QDQ) with at most LINEAR_PACKED_MAX_ROWS rows, y [..., N] in ``out_dtype``
+    (default x's dtype; fp32 or bf16).  fp32 sums in a fixed order on every call; not bitwise
+    the library GEMM of F.linear, whose fp32 sums run in another order."""
+    _lib.require_device(x, bias)
+    lib = _lib.load()
+    N, K = weight.shape
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError("the packed-weight Linear takes bf16 activations")
+    if x.shape[-1] != K:
+        raise ValueError(f"x has {x.shape[-1]} features, the weight {K}")
+    out_dtype = out_dtype or x.dtype
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, N), device=x.device, dtype=out_dtype)
+    if M:
+        b = None if bias is None else bias.detach().contiguous()
+        d = weight.rows.descriptor()
+        _lib.check(
+            lib.faq_hif4_linear_packed(
+                x2.data_ptr(), x2.stride(0), d.codes, d.meta, None if b is None else b.data_ptr(),
+                0 if b is None else _lib.dtype_code(b.dtype), y.data_ptr(), _lib.dtype_code(out_dtype), y.stride(0),
+                M, N, K, _lib.stream_ptr(x.device),
+            )
+        )
+    return y.view(*x.shape[:-1], N)
+
+
 def _per_head(t, H: int, device):
     """A per-dim fp32 tensor of 128 or H*128 values as (tensor, head stride)."""
     if t is None:

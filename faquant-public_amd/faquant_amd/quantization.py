@@ -63,6 +63,13 @@ class FakeQuantLinear(torch.nn.Module):
     is computed with torch as the reference computes it (clamp to +-2.079, exp, cast to the
     input dtype).  Without a block size the online transform is the generalized one of the
     whole row (rotation.py:53-69), also in ``act_prep_rows``.
+
+    ``packed_weight=True`` (an option of this library; in_features a multiple of 128) also
+    keeps the weight as packed HiF4 rows (4.5 bits per weight, packed from the weight before
+    its QDQ, so they decode to ``weight``), and inputs of at most ``packed_max_rows`` rows
+    (decode steps, small batches) run the contraction from them (``linear_packed``,
+    faq_hif4_linear_packed) instead of ``F.linear``: the same operands, fp32 sums in another
+    (fixed) order.
     """
 
     faquant_quantizes_input = True
@@ -88,6 +95,8 @@ class FakeQuantLinear(torch.nn.Module):
         activation_min: float | None = None,
         activation_max: float | None = None,
         activation_compand_log_scale: torch.Tensor | None = None,
+        packed_weight: bool = False,
+        packed_max_rows: int = 4,
     ) -> None:
         super().__init__()
         if quant_format != "hif4":
@@ -133,11 +142,22 @@ class FakeQuantLinear(torch.nn.Module):
             None if activation_compand_log_scale is None else activation_compand_log_scale.detach().float().clone(),
         )
         weight = linear.weight.detach() if weight_override is None else weight_override.detach()
+        self._packed = None
+        self.packed_max_rows = int(packed_max_rows)
+        if packed_weight and not quantize_weight:
+            raise ValueError("packed_weight packs the weight's HiF4 QDQ: it needs quantize_weight=True")
+        if packed_weight and not 0 <= self.packed_max_rows <= 8:
+            raise ValueError("packed_max_rows must be in 0..8 (the packed contraction takes at most 8 rows)")
         if quantize_weight:
+            from . import _ops
             from .hif4 import HIF4_SCALE_LEVELS
 
             source_device = weight.device
             gpu = weight if weight.device.type == "cuda" else weight.to("cuda")
+            if packed_weight:
+                # packed from the weight before its QDQ (a second QDQ of the result could
+                # choose another scale), with the QDQ's levels: decodes to the weight below
+                self._packed = _ops.PackedHiF4Weight(gpu, HIF4_SCALE_LEVELS)
             weight = fake_quantize(gpu, quant_format=quant_format, bits=bits, group_size=weight_group_size,
                                    symmetric=symmetric, clip_ratio=clip_ratio, hif4_levels=HIF4_SCALE_LEVELS)
             weight = weight.to(device=source_device, dtype=linear.weight.dtype)
@@ -196,4 +216,9 @@ class FakeQuantLinear(torch.nn.Module):
                 x, levels=HIF4_ACT_SCALE_LEVELS, col_scale=self.input_scale, rot_signs=self.input_rotation_signs,
                 rot_perm=perm, rot_block=self.input_rotation_block_size, act_min=bounds[0], act_max=bounds[1],
                 compand=compand, hadamard=block, hadamard_generalized=generalized, compand_rcp=rcp)
+        packed = self._packed
+        if (packed is not None and xq.dtype == torch.bfloat16 and xq.device == packed.device
+                and xq.numel() <= self.packed_max_rows * self.in_features):
+            # few rows: the contraction reads the packed weight (faq_hif4_linear_packed)
+            return _lib.forward_only(_ops.linear_packed(xq, packed, self.bias), x)
         return torch.nn.functional.linear(_lib.forward_only(xq, x), self.weight, self.bias)

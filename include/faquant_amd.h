@@ -60,6 +60,9 @@
  *   faq_act_prep_rows     quantization.py:199-276 (the full FakeQuantLinear activation path:
  *                         input scale, HiSQ rotation, clamp, companding, online Hadamard,
  *                         HiF4 QDQ), hisq_rotation.py:50-71
+ *   faq_hif4_linear_packed  the contraction of quantization.py:199-277 FakeQuantLinear.forward
+ *                         (F.linear on the HiF4-exact operands) for few input rows, with the
+ *                         HiF4 weight kept packed (4.5 bits per weight)
  *   faq_mfma_probe        no reference counterpart: a measurement helper (the device's
  *                         sustained bf16 MFMA rate, the reference point of the benchmark)
  *   faq_stream_probe      no reference counterpart: a measurement helper (the device's
@@ -424,6 +427,25 @@ int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t 
                          int64_t o_sb, int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int causal,
                          float scale, int quant_p, int p_levels, int norm_same, float* row_den, int nsplit,
                          void* workspace, int64_t workspace_bytes, faq_stream_t stream);
+
+/*
+ * y [M, N] = x [M, K] W^T (+ bias) with W kept as packed HiF4 rows, for M <= 8 rows of x:
+ * the contraction of FakeQuantLinear.forward (src/faquant/quantization.py:199-277, F.linear
+ * on the activation QDQ x and the weight QDQ W) where reading W dominates (decode steps, small
+ * batches).  W's row for output feature n and columns 128 j .. 128 j + 127 is packed row
+ * n * (K / 128) + j of `w_codes` (16 words per row) and `w_meta` (2 words per row) in the
+ * faq_hif4_kv row format: faq_operand_prep_hif4_kv of W viewed as [1, 1, N K / 128, 128] with
+ * the weight's levels writes it, and it decodes to the bf16 weight QDQ bitwise.  x: bf16
+ * [M, K], 16-byte aligned, row stride x_sm elements (>= K, a multiple of 8); y: fp32 or bf16
+ * [M, N], row stride y_sm (>= N); bias: NULL or fp32 / bf16 [N].  K must be a multiple of 128
+ * and M at most 8 (FAQ_EUNSUP otherwise).  The products of a feature are summed in fp32 in a
+ * fixed order (each lane over its blocks, then the lanes), so every call gives the same bits;
+ * the bias is added to the fp32 sum and y rounded once (bf16: round to nearest even).  Not
+ * bitwise the library GEMM of F.linear, whose fp32 sums run in another order.  No workspace.
+ */
+int faq_hif4_linear_packed(const uint16_t* x, int64_t x_sm, const uint32_t* w_codes, const uint32_t* w_meta,
+                           const void* bias, int bias_dtype, void* y, int y_dtype, int64_t y_sm, int M, int N, int K,
+                           faq_stream_t stream);
 
 /*
  * The attention kernel's in-register P quantizer (the HiF4 QDQ of P along keys,

@@ -42,7 +42,7 @@ def test_header_lists_the_entry_points():
          "faq_attention_fwd_split", "faq_attention_split_workspace", "faq_attention_mask_bounds",
          "faq_mfma_probe", "faq_stream_probe", "faq_pquant_groups", "faq_hadamard_rows_native", "faq_attention_fwd_split_noalloc",
          "faq_operand_prep_hif4_kv", "faq_attention_decode", "faq_attention_decode_workspace",
-         "faq_act_prep_rows", "faq_act_compand_rcp"]
+         "faq_act_prep_rows", "faq_act_compand_rcp", "faq_hif4_linear_packed"]
     )
 
 
@@ -317,6 +317,33 @@ def test_pquant_groups_validation(lib):
     assert lib.faq_hadamard_rows_native(p16, p16, 1, 96, 1, None) == _lib.EINVAL
     assert lib.faq_hadamard_rows_native(p16, p16, 1, 1024, 1, None) == _lib.EUNSUP
     assert lib.faq_hadamard_rows_native(p16, p16, 1, 128, 0, None) == _lib.EINVAL
+
+
+def test_packed_linear_validation(lib):
+    """faq_hif4_linear_packed refuses bad arguments before any device work."""
+    from faquant_amd import _lib
+
+    p16 = ctypes.c_void_p(1 << 20)
+
+    def linear(**kw):
+        a = dict(x=p16, xs=4096, c=p16, m=p16, b=None, bd=0, y=p16, yd=1, ys=4096, M=1, N=4096, K=4096)
+        a.update(kw)
+        return lib.faq_hif4_linear_packed(a["x"], a["xs"], a["c"], a["m"], a["b"], a["bd"], a["y"], a["yd"], a["ys"],
+                                          a["M"], a["N"], a["K"], None)
+
+    assert linear(x=None) == _lib.EINVAL
+    assert linear(K=4000, xs=4000) == _lib.EUNSUP
+    assert "multiple of 128" in lib.faq_last_error().decode()
+    assert linear(M=9) == _lib.EUNSUP
+    assert "at most 8 rows" in lib.faq_last_error().decode()
+    assert linear(N=0) == _lib.EINVAL
+    assert linear(yd=2) == _lib.EUNSUP  # fp16 output
+    assert linear(b=p16, bd=2) == _lib.EUNSUP  # fp16 bias
+    assert linear(xs=4095) == _lib.EINVAL
+    assert linear(ys=4095) == _lib.EINVAL
+    assert linear(m=ctypes.c_void_p((1 << 20) + 4)) == _lib.EINVAL  # meta not 8-byte aligned
+    assert linear(y=ctypes.c_void_p((1 << 20) + 2), yd=0) == _lib.EINVAL  # fp32 y not 4-byte aligned
+    assert linear(M=0, x=None, y=None) == _lib.OK  # no rows: nothing to do
 
 
 def test_decode_and_packed_prep_validation(lib):
