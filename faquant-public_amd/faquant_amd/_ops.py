@@ -467,7 +467,8 @@ def linear_packed(x: torch.Tensor, weight: PackedHiF4Weight, bias: torch.Tensor 
     out_dtype = out_dtype or x.dtype
     x2 = x.reshape(-1, K)
     if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
-        x2 = x2.contiguous()
+        # a fresh copy: contiguous() returns a contiguous view that starts off alignment as is
+        x2 = x2.clone(memory_format=torch.contiguous_format)
     M = x2.shape[0]
     y = torch.empty((M, N), device=x.device, dtype=out_dtype)
     if M:

@@ -177,6 +177,11 @@ def test_linear_packed_leading_shape_strides_and_nan(dev):
     xs[:, :K] = x.reshape(6, K)
     ys = _ops.linear_packed(xs[:, :K], pw)
     assert torch.equal(ys.view(torch.int16), y.reshape(6, N).view(torch.int16))
+    # a view that starts 2 bytes past 16-byte alignment is copied, not refused
+    flat = torch.empty(6 * K + 1, device=dev, dtype=torch.bfloat16)
+    flat[1:].copy_(x.reshape(-1))
+    yo = _ops.linear_packed(flat[1:].view(6, K), pw)
+    assert torch.equal(yo.view(torch.int16), y.reshape(6, N).view(torch.int16))
 
 
 def test_fake_quant_linear_packed_weight(dev):
