@@ -53,7 +53,8 @@ def build(verbose: bool = False) -> str:
     with tempfile.TemporaryDirectory(prefix="faq_build_") as tmp:
         units = [(os.path.join(CSRC, "capi.hip"), [], os.path.join(tmp, "capi.o")),
                  (os.path.join(CSRC, "attn_decode.hip"), [], os.path.join(tmp, "attn_decode.o")),
-                 (os.path.join(CSRC, "hif4_linear.hip"), [], os.path.join(tmp, "hif4_linear.o"))]
+                 (os.path.join(CSRC, "hif4_linear.hip"), [], os.path.join(tmp, "hif4_linear.o")),
+                 (os.path.join(CSRC, "attn_generic.hip"), [], os.path.join(tmp, "attn_generic.o"))]
         for m in range(ATTN_MASK_FORMS):
             units.append((os.path.join(CSRC, "attn_instances.hip"), [f"-DFAQ_ATTN_MASK={m}"],
                           os.path.join(tmp, f"attn_m{m}.o")))

@@ -13,6 +13,7 @@
 #include "../../include/faquant_amd.h"
 #include "attn_aux.hip"
 #include "attn_decode.h"
+#include "attn_generic.h"
 #include "hif4_linear.h"
 #include "hif4_attention.hip"
 #include "hif4_quant.hip"
@@ -972,6 +973,89 @@ int faq_attention_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t 
   faq::SplitCombineArgs ca{a.part_o, a.part_lm, a.rows_total, nsplit, Hq, Lq, o, o_sb, o_sh, o_sl,
                            o_dtype == FAQ_F32, row_den};
   faq::launch_split_combine(ca, st);
+  return check_launch(who);
+}
+
+int faq_attention_fwd_general(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_sl, const void* k,
+                              int k_dtype, int64_t k_sb, int64_t k_sh, int64_t k_sl, const void* v, int v_dtype,
+                              int64_t v_sb, int64_t v_sh, int64_t v_sl, void* o, int o_dtype, int64_t o_sb,
+                              int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int D, int key_tile,
+                              int causal, float scale, int quant_p, int p_levels, int norm_same, float* row_den,
+                              const faq_attn_opts* opts, faq_stream_t stream) {
+  const char* who = "faq_attention_fwd_general";
+  if (B < 0 || Hq < 1 || Hkv < 1 || Lq < 0 || Lk < 1) return fail(FAQ_EINVAL, "%s: bad sizes", who);
+  if (Hq % Hkv) return fail(FAQ_EINVAL, "%s: query heads must be divisible by key/value heads", who);
+  if (D < 1 || D > faq::kGenMaxDim) return fail(FAQ_EUNSUP, "%s: head_dim must lie in [1, %d], got %d", who, faq::kGenMaxDim, D);
+  if (key_tile < 1 || key_tile > faq::kGenMaxTile)
+    return fail(FAQ_EUNSUP, "%s: key tiles must hold 1 to %d keys, got %d", who, faq::kGenMaxTile, key_tile);
+  if (B > 65535 || Hq > 65535) return fail(FAQ_EUNSUP, "%s: at most 65535 batches and query heads", who);
+  for (int dt : {q_dtype, k_dtype, v_dtype, o_dtype})
+    if (dt != FAQ_F32 && dt != FAQ_BF16) return fail(FAQ_EUNSUP, "%s: operands and output must be fp32 or bf16", who);
+  if (quant_p && !valid_levels(p_levels)) return fail(FAQ_EINVAL, "%s: bad P levels %d", who, p_levels);
+  if (!(scale == scale)) return fail(FAQ_EINVAL, "%s: scale is NaN", who);
+  if (B == 0 || Lq == 0) return FAQ_OK;
+  if (!q || !k || !v || !o) return fail(FAQ_EINVAL, "%s: null operand", who);
+  faq::GenAttnArgs a{};
+  a.q = q;
+  a.q_dt = q_dtype == FAQ_BF16;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_sl = q_sl;
+  a.k = k;
+  a.k_dt = k_dtype == FAQ_BF16;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_sl = k_sl;
+  a.v = v;
+  a.v_dt = v_dtype == FAQ_BF16;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.v_sl = v_sl;
+  a.o = o;
+  a.o_dt = o_dtype == FAQ_BF16;
+  a.o_sb = o_sb;
+  a.o_sh = o_sh;
+  a.o_sl = o_sl;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.Lq = Lq;
+  a.Lk = Lk;
+  a.D = D;
+  a.T = key_tile;
+  a.causal = causal != 0;
+  a.scale = scale;
+  a.quant_p = quant_p != 0;
+  a.p_levels = quant_p ? p_levels : 123;
+  a.norm_same = norm_same != 0;
+  a.row_den = row_den;
+  if (opts) {
+    if (opts->p_dump || opts->q_prep) return fail(FAQ_EUNSUP, "%s: p_dump and q_prep are options of faq_attention_fwd", who);
+    if (opts->softcap < 0.0f || !(opts->softcap == opts->softcap)) return fail(FAQ_EINVAL, "%s: bad softcap", who);
+    a.softcap = opts->softcap;
+    const bool any_range = opts->row_lo || opts->row_hi || opts->key_bits;
+    if (any_range && !(opts->row_lo && opts->row_hi && opts->key_bits))
+      return fail(FAQ_EINVAL, "%s: row_lo, row_hi and key_bits go together", who);
+    if (any_range && opts->key_words < (static_cast<int64_t>(Lk) + 31) / 32)
+      return fail(FAQ_EINVAL, "%s: key_words must cover every key", who);
+    if (any_range && opts->dense_mask) return fail(FAQ_EINVAL, "%s: a dense mask and key ranges are exclusive", who);
+    a.row_lo = opts->row_lo;
+    a.row_hi = opts->row_hi;
+    a.key_bits = opts->key_bits;
+    a.key_words = opts->key_words;
+    a.amask = opts->dense_mask;
+    a.am_sb = opts->dm_sb;
+    a.am_sh = opts->dm_sh;
+    a.am_sq = opts->dm_sq;
+    if (opts->pv_probe && !quant_p) return fail(FAQ_EINVAL, "%s: pv_probe needs quant_p", who);
+    a.diag = opts->pv_probe;
+  }
+  const hipError_t e = faq::launch_gen_attention(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(FAQ_ELAUNCH, "%s: LDS limit of %zu bytes refused: %s", who, faq::gen_attention_lds_bytes(D, key_tile),
+                hipGetErrorString(e));
+  }
   return check_launch(who);
 }
 

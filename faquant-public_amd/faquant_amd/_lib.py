@@ -163,6 +163,17 @@ _SIGNATURES = {
         [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _vp],
         _c_int,
     ),
+    "faq_attention_fwd_general": (
+        [
+            _vp, _c_int, _c_i64, _c_i64, _c_i64,
+            _vp, _c_int, _c_i64, _c_i64, _c_i64,
+            _vp, _c_int, _c_i64, _c_i64, _c_i64,
+            _vp, _c_int, _c_i64, _c_i64, _c_i64,
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_int, _vp,
+            _opts_p, _vp,
+        ],
+        _c_int,
+    ),
     "faq_attention_fwd": (
         [
             _vp, _c_i64, _c_i64, _c_i64,

@@ -760,6 +760,90 @@ def attention_fwd(
 
 
 
+GENERAL_MAX_DIM = 256
+GENERAL_MAX_TILE = 1024
+
+
+def attention_general(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    key_tile: int,
+    causal: bool,
+    scale: float,
+    quant_p: bool,
+    p_levels: str,
+    norm_same: bool,
+    out: torch.Tensor,
+    row_den: torch.Tensor | None = None,
+    ranges: KeyRanges | None = None,
+    softcap: float | None = None,
+    pv_probe: torch.Tensor | None = None,
+    dense_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The simulator's recurrence (sfa:457-909) for what attention_fwd does not take: any
+    head_dim up to 256, key tiles of 1..1024 keys, and fp32 or bf16 operands multiplied in
+    fp32.  q [B, Hq, Lq, D], k and v [B, Hkv, Lk, D] (natural layout, already quantized
+    where the caller quantizes), ``out`` a [B, Hq, Lq, D] view (fp32 or bf16).  The masking
+    arguments and ``pv_probe`` mean what they mean for attention_fwd."""
+    _lib.require_device(q, k, v, out, row_den)
+    if softcap is not None and softcap < 0:
+        raise ValueError("softcap must be non-negative")
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    if k.shape != v.shape or k.shape[0] != B or k.shape[-1] != D:
+        raise ValueError("k and v must be [B, Hkv, Lk, D] with the query's batch and head_dim")
+    if D > GENERAL_MAX_DIM:
+        raise NotImplementedError(f"the MI355X attention supports head_dim up to {GENERAL_MAX_DIM}, got {D}")
+    if not 1 <= key_tile <= GENERAL_MAX_TILE:
+        raise NotImplementedError(f"the MI355X attention supports key chunks of 1 to {GENERAL_MAX_TILE} keys, "
+                                  f"got {key_tile}")
+    for t in (q, k, v):
+        if t.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("attention operands must be fp32 or bf16")
+        if t.stride(-1) != 1:
+            raise ValueError("attention operands need a unit stride along head_dim")
+    if out.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("attention output must be fp32 or bf16")
+    if tuple(out.shape) != (B, Hq, Lq, D) or out.stride(-1) != 1:
+        raise ValueError("out must be a [B, Hq, Lq, D] view with a unit stride along head_dim")
+    if row_den is not None and (row_den.dtype != torch.float32 or tuple(row_den.shape) != (B, Hq, Lq)
+                                or not row_den.is_contiguous()):
+        raise ValueError("row_den must be a contiguous fp32 [B, Hq, Lq] tensor")
+    if dense_mask is not None:
+        _lib.require_device(dense_mask)
+        if ranges is not None:
+            raise ValueError("a dense mask and key ranges are exclusive")
+        if (dense_mask.dtype != torch.float32 or dense_mask.ndim != 4 or dense_mask.stride(-1) != 1
+                or dense_mask.shape[-1] < Lk):
+            raise ValueError("dense_mask must be fp32 [B|1, Hq|1, Lq|1, >= Lk] with unit key stride")
+    if ranges is not None:
+        _lib.require_device(ranges.row_lo, ranges.row_hi, ranges.key_bits)
+        if tuple(ranges.row_lo.shape) != (B, Lq) or tuple(ranges.row_hi.shape) != (B, Lq):
+            raise ValueError("key ranges must be [B, Lq]")
+    if pv_probe is not None:
+        _lib.require_device(pv_probe)
+        if pv_probe.dtype != torch.float32 or tuple(pv_probe.shape) != (B, Hq, Lq, 5) \
+                or not pv_probe.is_contiguous():
+            raise ValueError("pv_probe must be a contiguous fp32 [B, Hq, Lq, 5] tensor")
+    held = _attn_opts(ranges, softcap, pv_probe, dense_mask)
+    opts = held[0] if held else None
+    lib = _lib.load()
+    code = _lib.dtype_code
+    _lib.check(
+        lib.faq_attention_fwd_general(
+            q.data_ptr(), code(q.dtype), *_bhld_strides(q), k.data_ptr(), code(k.dtype), *_bhld_strides(k),
+            v.data_ptr(), code(v.dtype), *_bhld_strides(v), out.data_ptr(), code(out.dtype),
+            out.stride(0), out.stride(1), out.stride(2),
+            B, Hq, Hkv, Lq, Lk, D, int(key_tile), int(bool(causal)), float(scale),
+            int(bool(quant_p)), int(p_levels), int(bool(norm_same)), _lib.ptr(row_den), opts,
+            _lib.stream_ptr(q.device),
+        )
+    )
+    return out
+
+
 def _check_attention_tensors(q, out, row_den, B, Hq, Lq):
     """The output and row denominators must cover every query row the kernels write."""
     if tuple(out.shape) != (B, Hq, Lq, HEAD_DIM):

@@ -406,6 +406,25 @@ def kv_operands_and_attend(module, q_op: torch.Tensor, key: torch.Tensor, value:
     return _ops.attention_fwd(q_op, k_op, transposed_values(v_op), key_length, **attn)
 
 
+def _unit_last(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def general_attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, qk_quant: bool, pv_quant: bool,
+                   levels, key_chunk: int, **attn) -> torch.Tensor:
+    """The simulator's operands and tile loop on the general kernel (_ops.attention_general):
+    Q, K and V fake-quantized along head_dim in 64-value groups with a zero-padded tail
+    (sfa:292-338, 592-619) where their matmul is quantized, taken as they are otherwise; P
+    quantized per 64-key group of each key chunk.  K/V are quantized on every call: the
+    reference's decode cache (sfa:243-289) holds the same values, since the QDQ is per
+    position."""
+    q_op = _ops.qdq_rows(query, levels["q"]) if qk_quant else _unit_last(query)
+    k_op = _ops.qdq_rows(key, levels["k"]) if qk_quant else _unit_last(key)
+    v_op = _ops.qdq_rows(value, levels["v"]) if pv_quant else _unit_last(value)
+    return _ops.attention_general(q_op, k_op, v_op, key_tile=key_chunk, quant_p=pv_quant, p_levels=levels["p"],
+                                  **attn)
+
+
 def simulated_flash_attention_forward(
     module: torch.nn.Module,
     query: torch.Tensor,
@@ -474,26 +493,26 @@ def simulated_flash_attention_forward(
 
     if attention_mask is not None and attention_mask.ndim not in (2, 3, 4):
         raise ValueError("attention mask must be rank 2, 3, or 4")
-    if key_chunk != _ops.KEY_TILE:
-        raise NotImplementedError(f"the HIP kernel uses key tiles of {_ops.KEY_TILE}, got {key_chunk}")
+    if key_chunk <= 0:
+        raise ValueError("attention key chunk size must be positive")
     if query_chunk <= 0:
         raise ValueError("attention query chunk size must be positive")
-    if head_dim != _ops.HEAD_DIM:
-        raise NotImplementedError(f"the HIP kernel supports head_dim {_ops.HEAD_DIM}, got {head_dim}")
     for t in (query, key, value):
         if t.dtype not in (torch.float32, torch.bfloat16):
             raise NotImplementedError(f"the HIP attention path takes bf16 or fp32 operands, got {t.dtype}")
-    # The kernel multiplies bf16 operands.  Quantized operands are HiF4 values, exact in bf16;
-    # without quantization the reference multiplies the inputs themselves in fp32 (sfa:723-724,
-    # 848-850), which only bf16 inputs reproduce.
-    if not qk_quant and (query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16):
+    # The MFMA kernel multiplies bf16 operands over key tiles of 128 at head_dim 128.
+    # Quantized operands are HiF4 values, exact in bf16; without quantization the reference
+    # multiplies the inputs themselves in fp32 (sfa:723-724, 848-850), which only bf16 inputs
+    # reproduce on bf16 MFMAs.  Every other shape or operand type runs the general kernel,
+    # which multiplies in fp32.
+    general = (key_chunk != _ops.KEY_TILE or head_dim != _ops.HEAD_DIM
+               or (not qk_quant and (query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16))
+               or (not pv_quant and value.dtype != torch.bfloat16))
+    if general and head_dim > _ops.GENERAL_MAX_DIM:
+        raise NotImplementedError(f"the MI355X attention supports head_dim up to {_ops.GENERAL_MAX_DIM}, got {head_dim}")
+    if general and key_chunk > _ops.GENERAL_MAX_TILE:
         raise NotImplementedError(
-            "QK without quantization multiplies bf16 operands on the MI355X: pass bf16 Q/K or enable "
-            "faquant_qk_matmul_quant (fp32 Q/K would be rounded to bf16)")
-    if not pv_quant and value.dtype != torch.bfloat16:
-        raise NotImplementedError(
-            "PV without quantization multiplies bf16 V on the MI355X: pass bf16 V or enable "
-            "faquant_pv_matmul_quant (fp32 V would be rounded to bf16)")
+            f"the MI355X attention supports key chunks of up to {_ops.GENERAL_MAX_TILE} keys, got {key_chunk}")
     qk_group = _hif4_group(qk_quant_kwargs, "QK") if qk_quant else 64
     pv_group = _hif4_group(pv_quant_kwargs, "PV") if pv_quant else 64
     diagnostics = getattr(module, "faquant_pv_normalizer_diagnostics", None)
@@ -501,9 +520,12 @@ def simulated_flash_attention_forward(
 
     levels = HIF4_ATTN_OPERAND_SCALE_LEVELS
     q_levels = levels["q"] if qk_quant else None
-    # bf16 rows: the attention kernel applies Q's QDQ as it loads them
-    q_prep = (0, q_levels) if _ops.raw_q_operand_ok(query, 0) else None
-    q_op = query if q_prep is not None else _ops.operand_prep(query, levels=q_levels)[0]
+    if general:
+        q_prep = None
+    else:
+        # bf16 rows: the attention kernel applies Q's QDQ as it loads them
+        q_prep = (0, q_levels) if _ops.raw_q_operand_ok(query, 0) else None
+        q_op = query if q_prep is not None else _ops.operand_prep(query, levels=q_levels)[0]
 
     dense = None
     if attention_mask is not None and attention_mask.ndim in (3, 4):
@@ -517,12 +539,17 @@ def simulated_flash_attention_forward(
     output = torch.empty((batch, query_length, query_heads, head_dim), device=query.device, dtype=query.dtype)
     probe = (torch.empty((batch, query_heads, query_length, 5), device=query.device, dtype=torch.float32)
              if collect else None)
-    kv_operands_and_attend(
-        module, q_op, key, value, query_length=query_length, qk_quant=qk_quant, pv_quant=pv_quant, levels=levels,
-        k_prep={}, q_prep=q_prep, causal=is_causal, scale=scale, quant_p=pv_quant, p_levels=levels["p"],
-        norm_same=mode == "quantized_same", out=output.transpose(1, 2), ranges=ranges, softcap=softcap,
-        pv_probe=probe, dense_mask=dense,
-    )
+    if general:
+        general_attend(query, key, value, qk_quant=qk_quant, pv_quant=pv_quant, levels=levels, key_chunk=key_chunk,
+                       causal=is_causal, scale=scale, norm_same=mode == "quantized_same", out=output.transpose(1, 2),
+                       ranges=ranges, softcap=softcap, pv_probe=probe, dense_mask=dense)
+    else:
+        kv_operands_and_attend(
+            module, q_op, key, value, query_length=query_length, qk_quant=qk_quant, pv_quant=pv_quant,
+            levels=levels, k_prep={}, q_prep=q_prep, causal=is_causal, scale=scale, quant_p=pv_quant,
+            p_levels=levels["p"], norm_same=mode == "quantized_same", out=output.transpose(1, 2), ranges=ranges,
+            softcap=softcap, pv_probe=probe, dense_mask=dense,
+        )
     p_values_before = module.faquant_simulated_attention_stats["p_quantized_values"]
     count_tiles(
         module.faquant_simulated_attention_stats,

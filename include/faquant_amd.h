@@ -38,6 +38,9 @@
  *                         simulated_flash_attention_forward (key tiles of 128; masks: none,
  *                         bottom-right causal, or key ranges + valid keys; logit softcap)
  *                         and src/faquant/wan22_attention.py:165-183 hif4_attention
+ *   faq_attention_fwd_general  simulated_flash_attention.py:457-909 for any key chunk
+ *                         (1..1024), head_dim 1..256 and fp32 or bf16 operands multiplied in
+ *                         fp32 (sfa:723-724, 848-850: unquantized fp32 Q/K/V)
  *   faq_attention_mask_bounds  simulated_flash_attention.py:341-368 _two_dimensional_mask and
  *                         the rank form of 371-427 _streaming_mask (padding, sliding window)
  *   faq_attention_fwd_split  the same recurrence divided over key ranges (decode, where
@@ -323,6 +326,29 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
                       int B, int Hq, int Hkv, int Lq, int Lk, int causal, float scale, int quant_p, int p_levels,
                       int norm_same, float* row_den, int out_levels, const faq_attn_opts* opts,
                       faq_stream_t stream);
+
+/*
+ * The same recurrence for the shapes and operand types faq_attention_fwd does not take
+ * (src/faquant/simulated_flash_attention.py:457-909 with any key chunk, head_dim, and fp32
+ * operands that the reference multiplies as they are, sfa:723-724, 848-850): fp32 arithmetic
+ * throughout, P-hat bit for bit the reference quantizer of this kernel's P.
+ *   q, k, v   [B, Hq|Hkv, Lq|Lk, D] at element strides (last stride 1), each FAQ_F32 or
+ *             FAQ_BF16, natural layout (V not transposed); quantized operands come in
+ *             already quantized (faq_hif4_qdq_rows along D)
+ *   o         [B, Hq, Lq, D] via strides, FAQ_F32 or FAQ_BF16
+ *   D         head_dim, 1..256;  key_tile  keys per tile, 1..1024 (the simulator's
+ *             faquant_attention_key_chunk_size; P groups of 64 start at each tile)
+ *   causal, scale, quant_p, p_levels, norm_same, row_den  as faq_attention_fwd
+ *   opts      NULL, or key ranges (row_lo, row_hi, key_bits, key_words; row_blocks unused),
+ *             softcap, dense_mask and pv_probe with the meanings of faq_attn_opts; p_dump and
+ *             q_prep are refused
+ */
+int faq_attention_fwd_general(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_sl, const void* k,
+                              int k_dtype, int64_t k_sb, int64_t k_sh, int64_t k_sl, const void* v, int v_dtype,
+                              int64_t v_sb, int64_t v_sh, int64_t v_sl, void* o, int o_dtype, int64_t o_sb,
+                              int64_t o_sh, int64_t o_sl, int B, int Hq, int Hkv, int Lq, int Lk, int D, int key_tile,
+                              int causal, float scale, int quant_p, int p_levels, int norm_same, float* row_den,
+                              const faq_attn_opts* opts, faq_stream_t stream);
 
 /*
  * Split-key form of faq_attention_fwd for grids that cannot fill the GPU (decode steps,

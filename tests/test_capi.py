@@ -42,7 +42,7 @@ def test_header_lists_the_entry_points():
          "faq_attention_fwd_split", "faq_attention_split_workspace", "faq_attention_mask_bounds",
          "faq_mfma_probe", "faq_stream_probe", "faq_pquant_groups", "faq_hadamard_rows_native", "faq_attention_fwd_split_noalloc",
          "faq_operand_prep_hif4_kv", "faq_attention_decode", "faq_attention_decode_workspace",
-         "faq_act_prep_rows", "faq_act_compand_rcp", "faq_hif4_linear_packed"]
+         "faq_act_prep_rows", "faq_act_compand_rcp", "faq_hif4_linear_packed", "faq_attention_fwd_general"]
     )
 
 
@@ -143,6 +143,27 @@ def test_validation_statuses_without_device_work(lib):
     assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 1 << 20, 1, 0, p16, p16, p16, None, 0, None) == _lib.EUNSUP
     assert lib.faq_attention_mask_bounds(None, 0, 1, 4, 300, 1, 0, p16, p16, p16, p16, 8, None) == _lib.EINVAL
     assert "key_words" in lib.faq_last_error().decode()
+
+
+def test_general_attention_validation_without_device_work(lib):
+    """faq_attention_fwd_general refuses bad sizes and types before touching the device."""
+    from faquant_amd import _lib
+
+    def call(B=1, Hq=2, Hkv=1, Lq=4, Lk=4, D=64, tile=128, dt=_lib.F32, levels=123, quant_p=1, p=1):
+        ptr = p if p else None
+        return lib.faq_attention_fwd_general(ptr, dt, 0, 0, 0, ptr, dt, 0, 0, 0, ptr, dt, 0, 0, 0, ptr, dt, 0, 0, 0,
+                                             B, Hq, Hkv, Lq, Lk, D, tile, 1, 0.125, quant_p, levels, 1, None, None,
+                                             None)
+
+    assert call(D=0) == _lib.EUNSUP and "head_dim" in lib.faq_last_error().decode()
+    assert call(D=257) == _lib.EUNSUP
+    assert call(tile=0) == _lib.EUNSUP and "key tiles" in lib.faq_last_error().decode()
+    assert call(tile=1025) == _lib.EUNSUP
+    assert call(Hq=3, Hkv=2) == _lib.EINVAL
+    assert call(dt=_lib.F16) == _lib.EUNSUP
+    assert call(levels=7) == _lib.EINVAL
+    assert call(p=0) == _lib.EINVAL and "null" in lib.faq_last_error().decode()
+    assert call(B=0) == _lib.OK and call(Lq=0) == _lib.OK  # empty: nothing launched
 
 
 def test_status_maps_to_reference_exception_types(lib):
@@ -274,23 +295,6 @@ def test_decode_split_count_rule():
         tiles = -(-lk // 128)
         tps = -(-tiles // n)
         assert 1 <= n <= 4096 and (n - 1) * tps < tiles  # every range holds a tile
-
-
-def test_unquantized_fp32_matmuls_are_refused():
-    """Without QK (PV) quantization the reference multiplies the fp32 inputs themselves
-    (sfa:723-724, 848-850); the kernel multiplies bf16 operands, so fp32 Q/K (V) with that
-    flag off raise NotImplementedError instead of being rounded silently."""
-    from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward as f
-
-    q, k = torch.zeros(1, 2, 3, 128), torch.zeros(1, 1, 3, 128)
-    mod = _module()
-    mod.faquant_qk_matmul_quant = False
-    with pytest.raises(NotImplementedError, match="bf16 Q/K"):
-        f(mod, q, k, k, None)
-    mod = _module()
-    mod.faquant_pv_matmul_quant = False
-    with pytest.raises(NotImplementedError, match="bf16 V"):
-        f(mod, q.bfloat16(), k.bfloat16(), k, None)
 
 
 def test_attention_core_validates_like_the_drop_in():

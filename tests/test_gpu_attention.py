@@ -303,14 +303,15 @@ def test_unsupported_features_raise(dev):
 
     q = torch.randn(1, 2, 8, 128, device=dev)
     k = torch.randn(1, 1, 8, 128, device=dev)
-    with pytest.raises(NotImplementedError, match="key tiles"):
-        simulated_flash_attention_forward(module(key_chunk=64), q, k, k, None)
+    with pytest.raises(NotImplementedError, match="key chunks"):
+        simulated_flash_attention_forward(module(key_chunk=4096), q, k, k, None)
     mod = module()
     mod.faquant_matmul_quant_kwargs = dict(mod.faquant_matmul_quant_kwargs, quant_format="int")
     with pytest.raises(NotImplementedError, match="quant_format"):
         simulated_flash_attention_forward(mod, q, k, k, None)
+    wide = torch.randn(1, 1, 8, 512, device=dev)
     with pytest.raises(NotImplementedError, match="head_dim"):
-        simulated_flash_attention_forward(module(), q[..., :64], k[..., :64], k[..., :64], None)
+        simulated_flash_attention_forward(module(), wide, wide, wide, None)
     # an all-valid mask is the mask-free case
     out_m, _ = simulated_flash_attention_forward(module(), q, k, k, torch.ones(1, 8, dtype=torch.bool, device=dev))
     out_n, _ = simulated_flash_attention_forward(module(), q, k, k, None)
