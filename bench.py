@@ -207,6 +207,34 @@ def cpu_baseline(cfg, rows, workers):
     }
 
 
+def device_info() -> dict:
+    """The GPU agent as rocminfo reports it: name, architecture, compute units and maximum
+    shader clock, and the dense bf16 MFMA peak they imply (CUs x 4096 FLOP per clock x clock),
+    beside the 2.5 PFLOP/s specification figure the roofline uses."""
+    import subprocess
+
+    try:
+        text = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=120).stdout
+    except (OSError, subprocess.SubprocessError) as e:
+        return {"error": f"rocminfo: {e}"}
+    for block in text.split("\nAgent ")[1:]:
+        fields = {}
+        for line in block.splitlines():
+            key, sep, val = line.strip().partition(":")
+            if sep and key not in fields:
+                fields[key.strip()] = val.strip()
+        if fields.get("Device Type") != "GPU":
+            continue
+        try:
+            cus = int(fields["Compute Unit"])
+            mhz = int(fields["Max Clock Freq. (MHz)"])
+        except (KeyError, ValueError):
+            return {"error": "rocminfo: no compute-unit or clock field"}
+        return {"name": fields.get("Marketing Name", ""), "arch": fields.get("Name", ""), "cus": cus,
+                "max_sclk_mhz": mhz, "bf16_dense_peak_tflops_at_max_sclk": round(cus * 4096 * mhz * 1e6 / 1e12, 1)}
+    return {"error": "rocminfo: no GPU agent"}
+
+
 def mfma_probe(dev) -> float:
     """The device's sustained dense bf16 MFMA rate (TFLOP/s) in the attention kernel's launch
     shape (faq_mfma_probe: MFMA chains only), timed after the benchmark so the clock is warm:
@@ -775,6 +803,7 @@ def main():
         "pct_spec_peak": round(100.0 * probe / MFMA_BF16_PEAK_TFLOPS, 2),
         "kernel_frac_of_probe": round(achieved / probe, 4),
     }
+    result["device"] = device_info()
     if cpu is not None:
         result["cpu_baseline"] = cpu
     print(json.dumps(result), flush=True)
