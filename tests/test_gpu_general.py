@@ -133,6 +133,20 @@ def test_general_masks_window_softcap_and_chunked_prefill(dev):
     assert_close_attention(got, ref, "fp32 unquantized non-causal softcap", **FP32)
 
 
+@pytest.mark.parametrize("Lq,Lk", [(200, 150), (1, 300), (7, 7)])
+def test_general_query_key_lengths(dev, Lq, Lk):
+    """More query rows than keys (bottom-right causal: the first Lq - Lk rows see no key and
+    output zeros), one decode row, and a sequence shorter than one chunk."""
+    q, k, v = _inputs(9, 1, 4, 2, Lq, Lk, 64)
+    q, k, v = (OQ.bf16_round(a) for a in (q, k, v))
+    got, ref, extra = _run(dev, q, k, v, "bfloat16", qk=True, pv=True, mode="quantized_same", key_chunk=64,
+                           query_chunk=32, stats=True)
+    assert extra["stats"][0] == extra["stats"][1]
+    assert_close_attention(got, ref, f"Lq {Lq} Lk {Lk}", **TIGHT)
+    if Lq > Lk:
+        assert not np.any(got[:, : Lq - Lk])
+
+
 def test_general_dense_masks(dev):
     """3-D boolean and 4-D additive masks (sfa:430-454) with head_dim 64 and key chunks of 80."""
     q, k, v = _inputs(6, 1, 2, 1, 70, 140, 64)
