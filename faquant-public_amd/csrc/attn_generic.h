@@ -1,5 +1,5 @@
-// General-shape HiF4 attention (any head_dim up to 256, any key tile up to 1024, fp32 or
-// bf16 operands multiplied in fp32): arguments and launcher.
+// General-shape HiF4 attention (any head_dim up to 256, any key tile up to 1024, fp32, bf16
+// or fp16 operands multiplied in fp32): arguments and launcher.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -13,7 +13,7 @@ constexpr int kGenMaxTile = 1024;    // key tile limit
 constexpr int kGenChunk = 32;        // keys staged in LDS at a time
 
 struct GenAttnArgs {
-  // operands [B, H, L, D] at element strides (last stride 1); dtype 0 fp32, 1 bf16
+  // operands [B, H, L, D] at element strides (last stride 1); dtype 0 fp32, 1 bf16, 2 fp16
   const void* q;
   int q_dt;
   int64_t q_sb, q_sh, q_sl;
@@ -23,7 +23,7 @@ struct GenAttnArgs {
   const void* v;
   int v_dt;
   int64_t v_sb, v_sh, v_sl;
-  void* o;  // [B, Hq, Lq, D], fp32 or bf16
+  void* o;  // [B, Hq, Lq, D], dtype as the operands
   int o_dt;
   int64_t o_sb, o_sh, o_sl;
   int B, Hq, Hkv, Lq, Lk, D, T;

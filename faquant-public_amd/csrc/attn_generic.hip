@@ -1,7 +1,7 @@
 // General-shape HiF4 flash attention on gfx950: the simulator's recurrence
 // (src/faquant/simulated_flash_attention.py:457-909) for the shapes and operand types the
 // MFMA kernel (hif4_attention.hip: head_dim 128, key tiles of 128, bf16 operands) does not
-// take: any head_dim up to 256, any key tile up to 1024 keys, and fp32 or bf16 Q/K/V
+// take: any head_dim up to 256, any key tile up to 1024 keys, and fp32, bf16 or fp16 Q/K/V
 // multiplied in fp32 (the reference multiplies unquantized fp32 operands as they are,
 // sfa:723-724, 848-850).  Quantized operands (sfa:592-619) come in already quantized.
 //
@@ -34,9 +34,11 @@
 namespace faq {
 namespace {
 
+// dt: 0 fp32, 1 bf16, 2 fp16 (the C ABI's dtype codes)
 __device__ __forceinline__ float gen_load(const void* p, int dt, int64_t i) {
   if (dt == 0) return static_cast<const float*>(p)[i];
-  return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  if (dt == 1) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return __half2float(static_cast<const __half*>(p)[i]);
 }
 
 // Reductions over the 16 lanes of one row (lanes 16 r .. 16 r + 15 of a wave).
@@ -290,9 +292,11 @@ __global__ __launch_bounds__(256) void gen_attention_kernel(GenAttnArgs a) {
         const int64_t at = b * a.o_sb + hq * a.o_sh + static_cast<int64_t>(rpos) * a.o_sl + d;
         if (a.o_dt == 0) {
           static_cast<float*>(a.o)[at] = o;
-        } else {
+        } else if (a.o_dt == 1) {
           const __bf16 h = static_cast<__bf16>(o);
           __builtin_memcpy(static_cast<uint16_t*>(a.o) + at, &h, 2);
+        } else {
+          static_cast<__half*>(a.o)[at] = __float2half_rn(o);
         }
       }
     }

@@ -990,29 +990,29 @@ int faq_attention_fwd_general(const void* q, int q_dtype, int64_t q_sb, int64_t 
     return fail(FAQ_EUNSUP, "%s: key tiles must hold 1 to %d keys, got %d", who, faq::kGenMaxTile, key_tile);
   if (B > 65535 || Hq > 65535) return fail(FAQ_EUNSUP, "%s: at most 65535 batches and query heads", who);
   for (int dt : {q_dtype, k_dtype, v_dtype, o_dtype})
-    if (dt != FAQ_F32 && dt != FAQ_BF16) return fail(FAQ_EUNSUP, "%s: operands and output must be fp32 or bf16", who);
+    if (!valid_dtype(dt)) return fail(FAQ_EUNSUP, "%s: operands and output must be fp32, bf16 or fp16", who);
   if (quant_p && !valid_levels(p_levels)) return fail(FAQ_EINVAL, "%s: bad P levels %d", who, p_levels);
   if (!(scale == scale)) return fail(FAQ_EINVAL, "%s: scale is NaN", who);
   if (B == 0 || Lq == 0) return FAQ_OK;
   if (!q || !k || !v || !o) return fail(FAQ_EINVAL, "%s: null operand", who);
   faq::GenAttnArgs a{};
   a.q = q;
-  a.q_dt = q_dtype == FAQ_BF16;
+  a.q_dt = q_dtype;
   a.q_sb = q_sb;
   a.q_sh = q_sh;
   a.q_sl = q_sl;
   a.k = k;
-  a.k_dt = k_dtype == FAQ_BF16;
+  a.k_dt = k_dtype;
   a.k_sb = k_sb;
   a.k_sh = k_sh;
   a.k_sl = k_sl;
   a.v = v;
-  a.v_dt = v_dtype == FAQ_BF16;
+  a.v_dt = v_dtype;
   a.v_sb = v_sb;
   a.v_sh = v_sh;
   a.v_sl = v_sl;
   a.o = o;
-  a.o_dt = o_dtype == FAQ_BF16;
+  a.o_dt = o_dtype;
   a.o_sb = o_sb;
   a.o_sh = o_sh;
   a.o_sl = o_sl;

@@ -783,8 +783,8 @@ def attention_general(
     dense_mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The simulator's recurrence (sfa:457-909) for what attention_fwd does not take: any
-    head_dim up to 256, key tiles of 1..1024 keys, and fp32 or bf16 operands multiplied in
-    fp32.  q [B, Hq, Lq, D], k and v [B, Hkv, Lk, D] (natural layout, already quantized
+    head_dim up to 256, key tiles of 1..1024 keys, and fp32, bf16 or fp16 operands multiplied
+    in fp32.  q [B, Hq, Lq, D], k and v [B, Hkv, Lk, D] (natural layout, already quantized
     where the caller quantizes), ``out`` a [B, Hq, Lq, D] view (fp32 or bf16).  The masking
     arguments and ``pv_probe`` mean what they mean for attention_fwd."""
     _lib.require_device(q, k, v, out, row_den)
@@ -800,12 +800,12 @@ def attention_general(
         raise NotImplementedError(f"the MI355X attention supports key chunks of 1 to {GENERAL_MAX_TILE} keys, "
                                   f"got {key_tile}")
     for t in (q, k, v):
-        if t.dtype not in (torch.float32, torch.bfloat16):
-            raise TypeError("attention operands must be fp32 or bf16")
+        if t.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise TypeError("attention operands must be fp32, bf16 or fp16")
         if t.stride(-1) != 1:
             raise ValueError("attention operands need a unit stride along head_dim")
-    if out.dtype not in (torch.float32, torch.bfloat16):
-        raise TypeError("attention output must be fp32 or bf16")
+    if out.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError("attention output must be fp32, bf16 or fp16")
     if tuple(out.shape) != (B, Hq, Lq, D) or out.stride(-1) != 1:
         raise ValueError("out must be a [B, Hq, Lq, D] view with a unit stride along head_dim")
     if row_den is not None and (row_den.dtype != torch.float32 or tuple(row_den.shape) != (B, Hq, Lq)

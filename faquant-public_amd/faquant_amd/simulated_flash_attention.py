@@ -498,14 +498,15 @@ def simulated_flash_attention_forward(
     if query_chunk <= 0:
         raise ValueError("attention query chunk size must be positive")
     for t in (query, key, value):
-        if t.dtype not in (torch.float32, torch.bfloat16):
-            raise NotImplementedError(f"the HIP attention path takes bf16 or fp32 operands, got {t.dtype}")
+        if t.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise NotImplementedError(f"the HIP attention path takes bf16, fp16 or fp32 operands, got {t.dtype}")
     # The MFMA kernel multiplies bf16 operands over key tiles of 128 at head_dim 128.
     # Quantized operands are HiF4 values, exact in bf16; without quantization the reference
     # multiplies the inputs themselves in fp32 (sfa:723-724, 848-850), which only bf16 inputs
-    # reproduce on bf16 MFMAs.  Every other shape or operand type runs the general kernel,
-    # which multiplies in fp32.
+    # reproduce on bf16 MFMAs.  Every other shape or operand type (fp16 operands included)
+    # runs the general kernel, which multiplies in fp32.
     general = (key_chunk != _ops.KEY_TILE or head_dim != _ops.HEAD_DIM
+               or torch.float16 in (query.dtype, key.dtype, value.dtype)
                or (not qk_quant and (query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16))
                or (not pv_quant and value.dtype != torch.bfloat16))
     if general and head_dim > _ops.GENERAL_MAX_DIM:

@@ -39,8 +39,8 @@
  *                         bottom-right causal, or key ranges + valid keys; logit softcap)
  *                         and src/faquant/wan22_attention.py:165-183 hif4_attention
  *   faq_attention_fwd_general  simulated_flash_attention.py:457-909 for any key chunk
- *                         (1..1024), head_dim 1..256 and fp32 or bf16 operands multiplied in
- *                         fp32 (sfa:723-724, 848-850: unquantized fp32 Q/K/V)
+ *                         (1..1024), head_dim 1..256 and fp32, bf16 or fp16 operands multiplied
+ *                         in fp32 (sfa:723-724, 848-850: unquantized fp32 Q/K/V)
  *   faq_attention_mask_bounds  simulated_flash_attention.py:341-368 _two_dimensional_mask and
  *                         the rank form of 371-427 _streaming_mask (padding, sliding window)
  *   faq_attention_fwd_split  the same recurrence divided over key ranges (decode, where
@@ -332,10 +332,10 @@ int faq_attention_fwd(const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t q_s
  * (src/faquant/simulated_flash_attention.py:457-909 with any key chunk, head_dim, and fp32
  * operands that the reference multiplies as they are, sfa:723-724, 848-850): fp32 arithmetic
  * throughout, P-hat bit for bit the reference quantizer of this kernel's P.
- *   q, k, v   [B, Hq|Hkv, Lq|Lk, D] at element strides (last stride 1), each FAQ_F32 or
- *             FAQ_BF16, natural layout (V not transposed); quantized operands come in
- *             already quantized (faq_hif4_qdq_rows along D)
- *   o         [B, Hq, Lq, D] via strides, FAQ_F32 or FAQ_BF16
+ *   q, k, v   [B, Hq|Hkv, Lq|Lk, D] at element strides (last stride 1), each FAQ_F32,
+ *             FAQ_BF16 or FAQ_F16, natural layout (V not transposed); quantized operands come
+ *             in already quantized (faq_hif4_qdq_rows along D)
+ *   o         [B, Hq, Lq, D] via strides, FAQ_F32, FAQ_BF16 or FAQ_F16
  *   D         head_dim, 1..256;  key_tile  keys per tile, 1..1024 (the simulator's
  *             faquant_attention_key_chunk_size; P groups of 64 start at each tile)
  *   causal, scale, quant_p, p_levels, norm_same, row_den  as faq_attention_fwd

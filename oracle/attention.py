@@ -213,7 +213,8 @@ def simulated_flash_attention(
     """Restatement of ``simulated_flash_attention_forward``; returns [B, Lq, Hq, D] float32.
 
     ``query``/``key``/``value`` are float32 arrays holding ``dtype`` values
-    ("float32" or "bfloat16"); the output is rounded to ``dtype``.
+    ("float32", "bfloat16" or "float16"); the output is rounded to ``dtype`` (sfa:871-884,
+    ``.to(query.dtype)``).
     """
     query = np.asarray(query, dtype=_F32)
     key = np.asarray(key, dtype=_F32)
@@ -356,7 +357,11 @@ def simulated_flash_attention(
         with np.errstate(invalid="ignore", divide="ignore"):
             norm = np.where(den > 0, acc / np.maximum(den, np.finfo(np.float32).tiny), _F32(0)).astype(_F32)
         out = norm.transpose(1, 2, 0, 3, 4).reshape(B, Hq, tiles * rows, D)
-        output[:, :, q0:q1] = hif4.bf16_round(out) if dtype == "bfloat16" else out
+        if dtype == "bfloat16":
+            out = hif4.bf16_round(out)
+        elif dtype == "float16":
+            out = hif4.fp16_round(out)
+        output[:, :, q0:q1] = out
 
     full = Lq // cfg.query_chunk
     if full:

@@ -160,7 +160,7 @@ def test_general_attention_validation_without_device_work(lib):
     assert call(tile=0) == _lib.EUNSUP and "key tiles" in lib.faq_last_error().decode()
     assert call(tile=1025) == _lib.EUNSUP
     assert call(Hq=3, Hkv=2) == _lib.EINVAL
-    assert call(dt=_lib.F16) == _lib.EUNSUP
+    assert call(dt=7) == _lib.EUNSUP
     assert call(levels=7) == _lib.EINVAL
     assert call(p=0) == _lib.EINVAL and "null" in lib.faq_last_error().decode()
     assert call(B=0) == _lib.OK and call(Lq=0) == _lib.OK  # empty: nothing launched

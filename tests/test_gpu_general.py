@@ -46,7 +46,7 @@ def _run(dev, q, k, v, dt, *, qk, pv, mode, causal=True, key_chunk=128, query_ch
         simulated_flash_attention_forward,
     )
 
-    tdt = torch.bfloat16 if dt == "bfloat16" else torch.float32
+    tdt = {"bfloat16": torch.bfloat16, "float16": torch.float16}.get(dt, torch.float32)
     qt, kt, vt = (to_dev(a, dev, tdt) for a in (q, k, v))
     mod = module(qk=qk, pv=pv, mode=mode, causal=causal, key_chunk=key_chunk, query_chunk=query_chunk)
     if diagnostics:
@@ -183,6 +183,20 @@ def test_general_path_single_key_rows_are_exact(dev):
     for mode in ("quantized_same", "unquantized"):
         got, ref, _ = _run(dev, q, k, v, "float32", qk=True, pv=True, mode=mode, key_chunk=16, sliding_window=1)
         assert np.array_equal(got, ref), mode
+
+
+@pytest.mark.parametrize("qk,pv,mode", [(True, True, "quantized_same"), (False, False, "unquantized"),
+                                        (True, False, "unquantized")])
+def test_fp16_operands(dev, qk, pv, mode):
+    """fp16 Q/K/V (the reference quantizes them in fp16 and multiplies in fp32; the output keeps
+    the query's dtype): the general kernel, against the oracle in fp16."""
+    q, k, v = _inputs(10, 1, 4, 2, 130, 130, 128)
+    q, k, v = (OQ.fp16_round(a) for a in (q, k, v))
+    got, ref, extra = _run(dev, q, k, v, "float16", qk=qk, pv=pv, mode=mode, stats=True)
+    assert extra["stats"][0] == extra["stats"][1]
+    # fp16 outputs: one-ulp rounding differences (2^-11 relative) where P is not quantized
+    # (reached 4.6e-6 / 6.8e-5), none where it is
+    assert_close_attention(got, ref, f"fp16 qk={qk} pv={pv} {mode}", **(TIGHT if pv else FEW_FLIPS))
 
 
 def test_general_refusals(dev):
