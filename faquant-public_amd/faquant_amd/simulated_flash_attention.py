@@ -412,17 +412,31 @@ def _unit_last(t: torch.Tensor) -> torch.Tensor:
 
 def general_attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, qk_quant: bool, pv_quant: bool,
                    levels, key_chunk: int, **attn) -> torch.Tensor:
-    """The simulator's operands and tile loop on the general kernel (_ops.attention_general):
-    Q, K and V fake-quantized along head_dim in 64-value groups with a zero-padded tail
-    (sfa:292-338, 592-619) where their matmul is quantized, taken as they are otherwise; P
-    quantized per 64-key group of each key chunk.  K/V are quantized on every call: the
-    reference's decode cache (sfa:243-289) holds the same values, since the QDQ is per
-    position."""
+    """The simulator's operands and tile loop where the MFMA kernel's bf16 operands do not
+    carry them as given: Q, K and V fake-quantized along head_dim in 64-value groups with a
+    zero-padded tail (sfa:292-338, 592-619) where their matmul is quantized, taken as they are
+    otherwise; P quantized per 64-key group of each key chunk.  K/V are quantized on every
+    call: the reference's decode cache (sfa:243-289) holds the same values, since the QDQ is
+    per position.
+
+    Quantized fp16 operands at head_dim 128 with key chunks of 128 run on the MFMA kernel: a
+    HiF4 value rounded to fp16 keeps at most six significant bits inside bf16's range (an
+    fp16 subnormal or infinity included), so the bf16 copy is exact, and the fp32 output is
+    rounded to fp16 once, as the reference's ``.to(query.dtype)`` does.  Everything else runs
+    the general kernel (_ops.attention_general)."""
+    out = attn.pop("out")
     q_op = _ops.qdq_rows(query, levels["q"]) if qk_quant else _unit_last(query)
     k_op = _ops.qdq_rows(key, levels["k"]) if qk_quant else _unit_last(key)
     v_op = _ops.qdq_rows(value, levels["v"]) if pv_quant else _unit_last(value)
+    if (qk_quant and pv_quant and key_chunk == _ops.KEY_TILE and query.shape[-1] == _ops.HEAD_DIM
+            and all(t.dtype in (torch.float16, torch.bfloat16) for t in (q_op, k_op, v_op))):
+        bf = lambda t: t.to(torch.bfloat16)  # noqa: E731 - exact for HiF4 values
+        out32 = torch.empty(out.shape, device=out.device, dtype=torch.float32)
+        _ops.attention_fwd(bf(q_op), bf(k_op), transposed_values(bf(v_op)), key.shape[2], quant_p=True,
+                           p_levels=levels["p"], out=out32, **attn)
+        return out.copy_(out32)
     return _ops.attention_general(q_op, k_op, v_op, key_tile=key_chunk, quant_p=pv_quant, p_levels=levels["p"],
-                                  **attn)
+                                  out=out, **attn)
 
 
 def simulated_flash_attention_forward(

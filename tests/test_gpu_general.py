@@ -199,6 +199,19 @@ def test_fp16_operands(dev, qk, pv, mode):
     assert_close_attention(got, ref, f"fp16 qk={qk} pv={pv} {mode}", **(TIGHT if pv else FEW_FLIPS))
 
 
+def test_fp16_quantized_operands_in_the_subnormal_range(dev):
+    """Quantized fp16 operands run on the MFMA kernel through exact bf16 copies: V rows scaled
+    into fp16's subnormal range (HiF4 values there are rounded to fp16 first, as the reference
+    rounds its QDQ output to the input dtype) and tiny queries, against the oracle in fp16."""
+    q, k, v = _inputs(11, 1, 4, 2, 200, 200, 128)
+    v[:, 0] *= np.float32(2.0**-20)
+    q[:, 1] *= np.float32(2.0**-12)
+    q, k, v = (OQ.fp16_round(a) for a in (q, k, v))
+    got, ref, _ = _run(dev, q, k, v, "float16", qk=True, pv=True, mode="quantized_same")
+    assert np.any((np.abs(ref) < 2.0**-14) & (ref != 0))  # outputs in fp16's subnormal range
+    assert_close_attention(got, ref, "fp16 subnormal operands", **TIGHT)
+
+
 def test_general_refusals(dev):
     from faquant_amd.simulated_flash_attention import simulated_flash_attention_forward
 
