@@ -709,6 +709,15 @@ __device__ __forceinline__ void generalized_row(float (&v)[R][8], float* lds, in
   __syncthreads();
 }
 
+// v as a T value before the companding quotient.  v is the QDQ output (a HiF4 value: at most
+// six significant bits, exact in bf16 and fp32, while fp16 can round it below its normal
+// range) or an earlier step's value already rounded to T, so only fp16 rounds here.
+template <typename T>
+__device__ __forceinline__ float in_dtype(float v) {
+  if constexpr (std::is_same<T, __half>::value) return Io<T>::round(v);
+  else return v;
+}
+
 // Whether the companding quotient T(x / c) of every T value x equals T(x * fp32(1 / c)):
 // bf16 scales that are normal numbers, fp16 scales below 8 in magnitude (the reference's
 // scales exp(clamp(log_scale, -2.079, 2.079)) lie in (0.125, 8)).  Proved over every pair of
@@ -785,7 +794,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 8 :
         const int4 pb = *reinterpret_cast<const int4*>(a.rot_perm + c0 + 4);
         const int pp[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[r][i] = act_row_lds[lds_pad(min(max(pp[i], 0), a.cols - 1))];  // (a valid permutation stays in range)
+        for (int i = 0; i < 8; ++i)  // (one unsigned min keeps any index in range; a valid permutation is)
+          v[r][i] = act_row_lds[lds_pad(static_cast<int>(min(static_cast<uint32_t>(pp[i]), static_cast<uint32_t>(a.cols - 1))))];
       }
     }
     // every gather has read the row before the transform writes it
@@ -841,12 +851,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 8 :
       if (__all(ok)) {
         if (c0 < a.cols)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(Io<T>::round(v[r][i]) * rc[i]);
+          for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(in_dtype<T>(v[r][i]) * rc[i]);
       } else if (c0 < a.cols) {
         float cs[8];
         Io<float>::load8(a.compand + c0, cs);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(Io<T>::round(v[r][i]) / cs[i]);
+        for (int i = 0; i < 8; ++i) v[r][i] = Io<T>::round(in_dtype<T>(v[r][i]) / cs[i]);
       }
     }
     if (c0 < a.cols) Io<T>::store8(y + c0, v[r]);
