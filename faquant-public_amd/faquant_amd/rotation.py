@@ -1,8 +1,8 @@
 """Normalized Walsh-Hadamard transforms on the MI355X: drop-in for faquant.rotation (hot-path subset).
 
 Reference: src/faquant/rotation.py:14-29 (``hadamard_transform``), 53-84
-(``generalized_hadamard_transform`` and its chunked form) and 117-135
-(``chunked_block_hadamard_transform``).  The HIP kernels run the same fp32
+(``generalized_hadamard_transform`` and its chunked form), 87-114 (``OnlineHadamardLinear``)
+and 117-135 (``chunked_block_hadamard_transform``).  The HIP kernels run the same fp32
 butterfly stages in the same order (strides 1, 2, ..., n/2) and divide by
 fp32(sqrt(n)) exactly as CPU torch does, so fp32 results are bit-identical.  Blocks
 above 512 and the generalized transform run in the row kernel of the Linear activation
@@ -12,6 +12,7 @@ path (rows of at most 32768 features, a multiple of 64).
 from __future__ import annotations
 
 import torch
+from torch import nn
 
 from . import _ops
 
@@ -88,3 +89,34 @@ def chunked_generalized_hadamard_transform(x: torch.Tensor, *, chunk_rows: int =
     if not _is_power_of_two(size) and (size % 12 or not _is_power_of_two(size // 12)):
         raise ValueError(f"unsupported generalized Hadamard dimension: {size}")
     return _row_path(x, hadamard_generalized=True)
+
+
+class OnlineHadamardLinear(nn.Module):
+    """The online rotation right before a linear layer (rotation.py:87-114): the chunked
+    generalized transform of the whole input row (``block_size`` None) or the per-block
+    transform, then the wrapped module.  The rotation runs in the HIP row kernels above; the
+    wrapped module is called as it is."""
+
+    faquant_online_hadamard = True
+
+    def __init__(self, module: nn.Linear, *, block_size: int | None = None) -> None:
+        super().__init__()
+        self.module = module
+        self.in_features = module.in_features
+        self.out_features = module.out_features
+        self.faquant_online_hadamard_block_size = block_size
+
+    @property
+    def weight(self) -> nn.Parameter:
+        return self.module.weight
+
+    @property
+    def bias(self) -> nn.Parameter | None:
+        return self.module.bias
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.faquant_online_hadamard_block_size is None:
+            rotated = chunked_generalized_hadamard_transform(x)
+        else:
+            rotated = chunked_block_hadamard_transform(x, block_size=self.faquant_online_hadamard_block_size)
+        return self.module(rotated)

@@ -305,3 +305,24 @@ def test_in_dtype_transforms_on_the_row_kernel_match_reference_goldens(dev, dt):
             assert got.dtype == tdt
             np.testing.assert_array_equal(got.float().cpu().numpy().view(np.uint32),
                                           _from_bits(g[f"{kind}h_{dt}_{n}"], dt).view(np.uint32))
+
+
+@pytest.mark.parametrize("block", [None, 64, 1024])
+def test_online_hadamard_linear(dev, block):
+    """OnlineHadamardLinear (rotation.py:87-114): the chunked generalized transform of the
+    whole row (block None; 12 * 256 = 3072 features) or the per-block transform, cast back
+    once, then the wrapped Linear: bitwise the same Linear on the oracle's rotated input."""
+    from faquant_amd.rotation import OnlineHadamardLinear
+
+    cols = 3072 if block is None else 2048
+    g = np.random.default_rng(70 + (block or 0))
+    x = OQ.bf16_round(g.standard_normal((37, cols)).astype(np.float32))
+    lin = torch.nn.Linear(cols, 96, bias=True).to(dev).to(torch.bfloat16)
+    mod = OnlineHadamardLinear(lin, block_size=block)
+    assert mod.faquant_online_hadamard and mod.in_features == cols and mod.out_features == 96
+    assert mod.weight is lin.weight and mod.bias is lin.bias
+    rot = OH.generalized_hadamard_transform(x) if block is None else OH.block_hadamard_transform(x, block)
+    with torch.no_grad():
+        got = mod(to_dev(x, dev, torch.bfloat16))
+        ref = lin(to_dev(OQ.bf16_round(rot), dev, torch.bfloat16))
+    assert torch.equal(got, ref)
