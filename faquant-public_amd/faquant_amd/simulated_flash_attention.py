@@ -419,22 +419,30 @@ def general_attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, 
     call: the reference's decode cache (sfa:243-289) holds the same values, since the QDQ is
     per position.
 
-    Quantized fp16 operands at head_dim 128 with key chunks of 128 run on the MFMA kernel: a
-    HiF4 value rounded to fp16 keeps at most six significant bits inside bf16's range (an
-    fp16 subnormal or infinity included), so the bf16 copy is exact, and the fp32 output is
-    rounded to fp16 once, as the reference's ``.to(query.dtype)`` does.  Everything else runs
-    the general kernel (_ops.attention_general)."""
+    With key chunks of 128 and head_dim up to 128 the MFMA kernel takes the call whenever its
+    bf16 operands hold the values exactly: HiF4 values (at most six significant bits; rounded
+    to fp16 they keep that inside bf16's range, fp16 subnormals and infinities included) or
+    bf16 inputs.  Operands narrower than 128 are zero-padded to 128 dims, which adds exact zeros
+    to every score and fills output columns that are dropped; the fp32 output is rounded to the
+    query's dtype once, as the reference's ``.to(query.dtype)`` does.  Everything else (other
+    key chunks, head_dim above 128, unquantized fp32 or fp16 operands) runs the general kernel
+    (_ops.attention_general)."""
     out = attn.pop("out")
     q_op = _ops.qdq_rows(query, levels["q"]) if qk_quant else _unit_last(query)
     k_op = _ops.qdq_rows(key, levels["k"]) if qk_quant else _unit_last(key)
     v_op = _ops.qdq_rows(value, levels["v"]) if pv_quant else _unit_last(value)
-    if (qk_quant and pv_quant and key_chunk == _ops.KEY_TILE and query.shape[-1] == _ops.HEAD_DIM
-            and all(t.dtype in (torch.float16, torch.bfloat16) for t in (q_op, k_op, v_op))):
-        bf = lambda t: t.to(torch.bfloat16)  # noqa: E731 - exact for HiF4 values
-        out32 = torch.empty(out.shape, device=out.device, dtype=torch.float32)
-        _ops.attention_fwd(bf(q_op), bf(k_op), transposed_values(bf(v_op)), key.shape[2], quant_p=True,
+    D = query.shape[-1]
+    exact_qk = qk_quant or (q_op.dtype == torch.bfloat16 and k_op.dtype == torch.bfloat16)
+    exact_v = pv_quant or v_op.dtype == torch.bfloat16
+    if key_chunk == _ops.KEY_TILE and D <= _ops.HEAD_DIM and exact_qk and exact_v:
+        def bf(t):  # exact: HiF4 or bf16 values
+            t = t.to(torch.bfloat16)
+            return torch.nn.functional.pad(t, (0, _ops.HEAD_DIM - D)) if D < _ops.HEAD_DIM else t
+        B, Hq, Lq = out.shape[:3]
+        out32 = torch.empty((B, Hq, Lq, _ops.HEAD_DIM), device=out.device, dtype=torch.float32)
+        _ops.attention_fwd(bf(q_op), bf(k_op), transposed_values(bf(v_op)), key.shape[2], quant_p=pv_quant,
                            p_levels=levels["p"], out=out32, **attn)
-        return out.copy_(out32)
+        return out.copy_(out32[..., :D])
     return _ops.attention_general(q_op, k_op, v_op, key_tile=key_chunk, quant_p=pv_quant, p_levels=levels["p"],
                                   out=out, **attn)
 

@@ -133,6 +133,35 @@ def test_general_masks_window_softcap_and_chunked_prefill(dev):
     assert_close_attention(got, ref, "fp32 unquantized non-causal softcap", **FP32)
 
 
+@pytest.mark.parametrize("D,qk,pv,mode", [(64, False, False, "unquantized"), (96, True, True, "unquantized"),
+                                          (72, True, False, "unquantized"), (32, False, True, "quantized_same"),
+                                          (112, True, True, "quantized_same")])
+def test_narrow_heads_on_the_mfma_kernel(dev, D, qk, pv, mode):
+    """head_dim below 128 with key chunks of 128 and bf16-exact operands: zero-padded to 128 on
+    the MFMA kernel (padding adds exact zeros to every score), with a padding mask, a window
+    and the PV probe, against the oracle.  The MFMA kernel's P is exp2 of log2-scaled scores,
+    a few ulp from the reference's exp, so a P-hat code on a rounding boundary can flip (one
+    key's weight moves by a code step), as on the 128-dim path: the inputs and the bar are
+    those of the MFMA kernel's random-configuration tests (queries x2, the FLIPS bar of
+    tests/test_gpu_attention.py).  Unquantized P enters the MFMAs as two bf16 parts (16
+    significant bits), as on the 128-dim path."""
+    g = np.random.default_rng(12)
+    q = OQ.bf16_round(g.standard_normal((2, 4, 150, D)).astype(np.float32) * 2)
+    k = OQ.bf16_round(g.standard_normal((2, 2, 190, D)).astype(np.float32))
+    v = OQ.bf16_round(g.standard_normal((2, 2, 190, D)).astype(np.float32))
+    mask = np.ones((2, 190), dtype=bool)
+    mask[1, :30] = False
+    got, ref, extra = _run(dev, q, k, v, "bfloat16", qk=qk, pv=pv, mode=mode, mask=mask, stats=True,
+                           diagnostics=pv)
+    assert extra["stats"][0] == extra["stats"][1]
+    assert_close_attention(got, ref, f"narrow D {D} qk={qk} pv={pv} {mode}")
+    got, ref, _ = _run(dev, q, k, v, "bfloat16", qk=qk, pv=pv, mode=mode, sliding_window=40)
+    assert_close_attention(got, ref, f"narrow D {D} window")
+    if pv:
+        mine, theirs = extra["diag"]
+        assert mine["rows"] == theirs["rows"] and mine["p_values"] == theirs["p_values"]
+
+
 @pytest.mark.parametrize("Lq,Lk", [(200, 150), (1, 300), (7, 7)])
 def test_general_query_key_lengths(dev, Lq, Lk):
     """More query rows than keys (bottom-right causal: the first Lq - Lk rows see no key and
