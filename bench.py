@@ -562,6 +562,56 @@ def linear_prep_bench(tokens: int, steps: int, warmup: int) -> dict:
             "steps": steps, "warmup": warmup, "dtype": "bf16", "layers": rows}
 
 
+GENERAL_SHAPES = (
+    # (label, head_dim, key tile, operand dtype, P quantized with the quantized_same normalizer)
+    ("key_chunk_64", 128, 64, "bf16", True),
+    ("key_chunk_256", 128, 256, "bf16", True),
+    ("head_dim_256", 256, 128, "bf16", True),
+    ("head_dim_64_key_chunk_64", 64, 64, "bf16", True),
+    ("fp32_unquantized", 128, 128, "fp32", False),
+)
+
+
+def general_bench(length: int, steps: int, warmup: int) -> dict:
+    """The general attention kernel (faq_attention_fwd_general: key tiles and head dims the
+    MFMA kernel does not take, fp32 operands) on Qwen3-8B heads (32 query / 8 KV heads),
+    causal prefill over `length` tokens, HIP events around `steps` launches.  The kernel
+    multiplies in fp32 on the VALU; its roofline is MI355X's fp32 peak (157.3 TFLOP/s)."""
+    import torch
+
+    from faquant_amd import _ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(5)
+    B, Hq, Hkv = 1, 32, 8
+    rows = []
+    for label, D, T, dt, quant in GENERAL_SHAPES:
+        dtype = torch.bfloat16 if dt == "bf16" else torch.float32
+        q, k, v = (torch.randn((B, h, length, D), device=dev, generator=gen).to(dtype) for h in (Hq, Hkv, Hkv))
+        out = torch.empty((B, Hq, length, D), device=dev, dtype=dtype)
+
+        def call():
+            _ops.attention_general(q, k, v, key_tile=T, causal=True, scale=D**-0.5, quant_p=quant, p_levels="123",
+                                   norm_same=quant, out=out)
+
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            call()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / steps
+        tflops = _ops.attention_flops(B, Hq, length, length, True, head_dim=D) / (ms * 1e-3) / 1e12
+        rows.append({"shape": label, "head_dim": D, "key_chunk": T, "dtype": dt, "quant_p": quant,
+                     "ms": round(ms, 3), "tflops": round(tflops, 2), "fp32_peak_frac": round(tflops / 157.3, 3)})
+        del q, k, v, out
+    return {"metric": "general attention kernel, Qwen3-8B heads, causal prefill, 1 GPU", "seq_len": length,
+            "steps": steps, "warmup": warmup, "shapes": rows}
+
+
 def stream_reference() -> dict:
     """This device's practical rates for plain streams, the measured reference points beside
     the 8 TB/s specification for the HBM-bound decode kernels: torch's copy and sum over
@@ -639,6 +689,9 @@ def main():
     ap.add_argument("--linear-prep", type=int, default=0, metavar="TOKENS",
                     help="time the quantized Linear's activation path (HiSQ rotation, clamp, companding) "
                          "at the Qwen3-8B input widths over TOKENS rows instead")
+    ap.add_argument("--general", type=int, default=0, metavar="TOKENS",
+                    help="time the general attention kernel (key chunks and head dims other than 128, fp32 "
+                         "operands) on Qwen3-8B heads over a causal prefill of TOKENS instead")
     ap.add_argument("--stream-reference", action="store_true",
                     help="measure only the device's practical HBM stream rate (torch copy and sum over 1 GiB)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -664,6 +717,10 @@ def main():
 
     if args.linear_decode:
         print(json.dumps(linear_decode_bench(args.linear_decode, args.steps, warmup)), flush=True)
+        return
+
+    if args.general:
+        print(json.dumps(general_bench(args.general, args.steps, warmup)), flush=True)
         return
 
     if args.stream_reference:

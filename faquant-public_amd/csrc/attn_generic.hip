@@ -87,6 +87,55 @@ __device__ __forceinline__ void gen_qdq8(float* v) {
 __device__ __forceinline__ int gen_dim_pad(int D) { return (D + 3) / 4 * 4 + 4; }
 __device__ __forceinline__ int gen_tile_pad(int T) { return (T + 7) / 8 * 8 + 4; }
 
+// Rows j < nk of a key chunk into LDS as fp32 (dst[j Dp + d], d < D; rows nk .. 31 as zeros):
+// the row of key j starts at element base + j sl of src.  16-byte loads (8 bf16 / fp16 or
+// 4 fp32 values) where the dims, the strides and the pointer allow them, so that one load
+// and one index division serve 4-8 values; otherwise one value per load, every padding
+// word included.
+__device__ __forceinline__ void gen_stage_chunk(float* dst, const void* src, int dt, int64_t base, int64_t sl,
+                                                int nk, int D, int Dp, int tid) {
+  const int vw = dt == 0 ? 4 : 8;  // values per 16 bytes
+  const bool vec = D % vw == 0 && base % vw == 0 && sl % vw == 0 &&
+                   (reinterpret_cast<uintptr_t>(src) & 15u) == 0;
+  if (vec) {
+    const int upr = D / vw;  // 16-byte units per row
+    for (int u = tid; u < kGenChunk * upr; u += 256) {
+      const int j = u / upr, d0 = (u - j * upr) * vw;
+      float* o = dst + j * Dp + d0;
+      if (j < nk) {
+        const int64_t at = base + static_cast<int64_t>(j) * sl + d0;
+        if (dt == 0) {
+          *reinterpret_cast<float4*>(o) = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + at);
+        } else {
+          const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + at);
+          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+          float f[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (dt == 1) {
+              f[2 * i] = __uint_as_float(ws[i] << 16);
+              f[2 * i + 1] = __uint_as_float(ws[i] & 0xFFFF0000u);
+            } else {
+              f[2 * i] = __half2float(__ushort_as_half(static_cast<unsigned short>(ws[i] & 0xFFFFu)));
+              f[2 * i + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(ws[i] >> 16)));
+            }
+          }
+          *reinterpret_cast<float4*>(o) = make_float4(f[0], f[1], f[2], f[3]);
+          *reinterpret_cast<float4*>(o + 4) = make_float4(f[4], f[5], f[6], f[7]);
+        }
+      } else {
+        *reinterpret_cast<float4*>(o) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (dt != 0) *reinterpret_cast<float4*>(o + 4) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    }
+  } else {
+    for (int idx = tid; idx < kGenChunk * Dp; idx += 256) {
+      const int j = idx / Dp, d = idx - j * Dp;
+      dst[idx] = (j < nk && d < D) ? gen_load(src, dt, base + static_cast<int64_t>(j) * sl + d) : 0.0f;
+    }
+  }
+}
+
 template <int LV>
 __global__ __launch_bounds__(256) void gen_attention_kernel(GenAttnArgs a) {
   extern __shared__ float4 gen_lds4[];
@@ -167,27 +216,33 @@ __global__ __launch_bounds__(256) void gen_attention_kernel(GenAttnArgs a) {
     for (int c0 = 0; c0 < W; c0 += kGenChunk) {
       const int nk = min(kGenChunk, W - c0);
       __syncthreads();
-      for (int idx = tid; idx < kGenChunk * Dp; idx += 256) {
-        const int j = idx / Dp, d = idx - j * Dp;
-        KV[idx] = (j < nk && d < D)
-                      ? gen_load(a.k, a.k_dt, b * a.k_sb + kvh * a.k_sh + static_cast<int64_t>(key0 + c0 + j) * a.k_sl + d)
-                      : 0.0f;
-      }
+      gen_stage_chunk(KV, a.k, a.k_dt, b * a.k_sb + kvh * a.k_sh + static_cast<int64_t>(key0 + c0) * a.k_sl, a.k_sl,
+                      nk, D, Dp, tid);
       __syncthreads();
+      // both keys' dot products in one pass over d (each Q read serves two keys; every KV row
+      // of the chunk is written, rows past nk as zeros), each summed in d order
+      float dots[2] = {0.0f, 0.0f};
+      {
+        const float4* qp = reinterpret_cast<const float4*>(Qs + sr * Dp);
+        const float4* kp0 = reinterpret_cast<const float4*>(KV + sj * Dp);
+        const float4* kp1 = reinterpret_cast<const float4*>(KV + (sj + 16) * Dp);
+        for (int d4 = 0; d4 < (D + 3) / 4; ++d4) {
+          const float4 qv = qp[d4], k0 = kp0[d4], k1 = kp1[d4];
+          dots[0] = __builtin_fmaf(qv.x, k0.x, dots[0]);
+          dots[1] = __builtin_fmaf(qv.x, k1.x, dots[1]);
+          dots[0] = __builtin_fmaf(qv.y, k0.y, dots[0]);
+          dots[1] = __builtin_fmaf(qv.y, k1.y, dots[1]);
+          dots[0] = __builtin_fmaf(qv.z, k0.z, dots[0]);
+          dots[1] = __builtin_fmaf(qv.z, k1.z, dots[1]);
+          dots[0] = __builtin_fmaf(qv.w, k0.w, dots[0]);
+          dots[1] = __builtin_fmaf(qv.w, k1.w, dots[1]);
+        }
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int j = sj + 16 * h;
         if (j < nk) {
-          const float4* qp = reinterpret_cast<const float4*>(Qs + sr * Dp);
-          const float4* kp = reinterpret_cast<const float4*>(KV + j * Dp);
-          float dot = 0.0f;
-          for (int d4 = 0; d4 < (D + 3) / 4; ++d4) {
-            const float4 qv = qp[d4], kv = kp[d4];
-            dot = __builtin_fmaf(qv.x, kv.x, dot);
-            dot = __builtin_fmaf(qv.y, kv.y, dot);
-            dot = __builtin_fmaf(qv.z, kv.z, dot);
-            dot = __builtin_fmaf(qv.w, kv.w, dot);
-          }
+          const float dot = dots[h];
           const int key = key0 + c0 + j;
           float s = dot * a.scale;
           if (a.softcap > 0.0f) s = tanhf(s / a.softcap) * a.softcap;
@@ -249,12 +304,8 @@ __global__ __launch_bounds__(256) void gen_attention_kernel(GenAttnArgs a) {
     for (int c0 = 0; c0 < W; c0 += kGenChunk) {
       const int nk = min(kGenChunk, W - c0);
       __syncthreads();
-      for (int idx = tid; idx < kGenChunk * Dp; idx += 256) {
-        const int j = idx / Dp, d = idx - j * Dp;
-        KV[idx] = (j < nk && d < D)
-                      ? gen_load(a.v, a.v_dt, b * a.v_sb + kvh * a.v_sh + static_cast<int64_t>(key0 + c0 + j) * a.v_sl + d)
-                      : 0.0f;
-      }
+      gen_stage_chunk(KV, a.v, a.v_dt, b * a.v_sb + kvh * a.v_sh + static_cast<int64_t>(key0 + c0) * a.v_sl, a.v_sl,
+                      nk, D, Dp, tid);
       __syncthreads();
       for (int j = 0; j < nk; ++j) {
         const float pj = S[rr * Tp + c0 + j];
